@@ -1,0 +1,126 @@
+/*
+ * rotor_hip.h - C ABI of the MI355X (gfx950) ternary-linear library librotor_hip.so.
+ *
+ * This is the drop-in boundary for the hot path of BikerSam86/rotor-RAG: the
+ * reference's GPU plug-in (src/rotor/gpu_ternary.py GPUTernaryOps, reached through
+ * src/rotor/gpu_layers.py:14-25 get_gpu() from TernaryLinear,
+ * src/rotor/transformer.py:70-75,106-109,131-147) and its CPU twin
+ * (src/rotor/transformer.py:150, np.dot(x, W_i8.T) * scale).  Python binds it with
+ * ctypes exactly as the reference binds its C core (src/rotor/bitnet_fast.py:15-48,
+ * 86-102): plain pointers and sizes, no C++ or torch types.
+ *
+ * Conventions
+ *  - Every function returns an int status: RT_OK (0) or a negative RT_E* code;
+ *    rt_last_error() then returns a thread-local message.  Nothing aborts the process.
+ *  - Weights are given in the rotor 2-bit format: row-major [N][ceil(K/4)] bytes,
+ *    element j of a byte in bits (2j+1, 2j) = (bit0, bit1), value = bit0 - bit1
+ *    (00 -> 0, 10 -> +1, 01 -> -1, 11 -> 0).  src/rotor/core.py:75-110 and
+ *    native/c/rotor_core.c:202-260 define this code; it is byte-identical to the
+ *    BitNet tensors load_from_bitnet receives (src/rotor/transformer.py:77-92).
+ *  - Activation / output pointers are DEVICE pointers (hipMalloc'd or torch CUDA
+ *    tensors), row-major and contiguous.  Work is enqueued on the context's stream;
+ *    call rt_sync() before reading results on the host.
+ *  - One rt_ctx per host thread; a context is not thread-safe.
+ */
+#ifndef ROTOR_HIP_H
+#define ROTOR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RT_OK 0
+#define RT_EINVAL (-1)     /* bad argument (null pointer, size out of range, ...) */
+#define RT_EHIP (-2)       /* a HIP runtime call failed; message names it */
+#define RT_ENOMEM (-3)     /* device allocation failed */
+#define RT_ENODEV (-4)     /* no usable gfx950 device */
+
+typedef struct rt_ctx rt_ctx;         /* device + stream + activation scratch */
+typedef struct rt_weights rt_weights; /* one device-resident ternary matrix   */
+typedef struct rt_plan rt_plan;       /* a prepared multi-matrix launch        */
+
+/* Thread-local text of the last error (never NULL).  Replaces the reference's
+ * exception text (src/rotor/gpu_layers.py:21-24). */
+const char* rt_last_error(void);
+
+/* ABI version (major*100 + minor). */
+int rt_version(void);
+
+/* Number of visible HIP devices (0 when none); RT_OK even when 0. */
+int rt_device_count(int* n);
+
+/* Create a context on `device`: checks the device is gfx950, makes it current and
+ * uses the null stream until rt_ctx_set_stream.  Replaces GPUTernaryOps.__init__
+ * (src/rotor/gpu_ternary.py:78-110: platform scan, context, queue, kernel build). */
+int rt_ctx_create(int device, rt_ctx** out);
+int rt_ctx_destroy(rt_ctx* ctx);
+
+/* Enqueue subsequent work on an existing hipStream_t (e.g. torch's current stream).
+ * The stream must be of default priority; NULL selects the null stream. */
+int rt_ctx_set_stream(rt_ctx* ctx, void* hip_stream);
+
+/* Wait for all work enqueued on the context's stream
+ * (the blocking read of src/rotor/gpu_ternary.py:199-200). */
+int rt_sync(rt_ctx* ctx);
+
+/* Upload a ternary matrix given as rotor bytes [N][ceil(K/4)] in HOST memory and
+ * re-lay it on the device in the GEMV/GEMM tile layout.  scale = the per-tensor
+ * weight scale (src/rotor/bitnet_model.py:182-185).  Replaces
+ * GPUTernaryOps.pack_ternary_weights (src/rotor/gpu_ternary.py:112-136) and the
+ * per-call weight upload of ternary_matmul (:160-164): weights stay resident. */
+int rt_weights_upload(rt_ctx* ctx, const uint8_t* rotor_host, int N, int K, float scale, rt_weights** out);
+
+/* Same, from rotor bytes already in DEVICE memory (row-major [N][ceil(K/4)]). */
+int rt_weights_upload_device(rt_ctx* ctx, const uint8_t* rotor_dev, int N, int K, float scale, rt_weights** out);
+
+/* Copy the matrix back as host rotor bytes [N][ceil(K/4)] (exact inverse of upload). */
+int rt_weights_download(rt_ctx* ctx, const rt_weights* w, uint8_t* rotor_host);
+
+int rt_weights_info(const rt_weights* w, int* N, int* K, float* scale);
+int rt_weights_free(rt_weights* w);
+
+/* Per-row (per-token) absmax int8 quantiser on x fp32 [M][K] (device):
+ * s[m] = max|x[m,:]| / 127 (1 when the row is all zero), q = clip(rint(x / s), -128, 127),
+ * fp32 IEEE division, round-half-even.  Writes q int8 [M][K] and s fp32 [M] (device).
+ * The formula of src/rotor/quantization.py:137-149, applied per row. */
+int rt_quantize_rows(rt_ctx* ctx, const float* x, int M, int K, int8_t* q, float* s);
+
+/* Exact int32 accumulators acc[m][n] = sum_k q[m][k] * W[n][k] for int8 q [M][K]
+ * (device) -> acc int32 [M][N] (device).  The parity hook of the W2A8 path. */
+int rt_linear_i32(rt_ctx* ctx, const rt_weights* w, const int8_t* q, int M, int32_t* acc);
+
+/* The ternary linear, W2A8: per-token quantise x fp32 [M][K], accumulate in int32,
+ * y[m][n] = ((float)acc[m][n] * s_x[m]) * s_w.  y fp32 [M][N] (device).
+ * Replaces TernaryLinear.forward (src/rotor/transformer.py:111-155; the op at :150)
+ * and, per token, GPUTernaryOps.ternary_matmul (src/rotor/gpu_ternary.py:138-202). */
+int rt_linear_f32(rt_ctx* ctx, const rt_weights* w, const float* x, int M, float* y);
+
+/* As rt_linear_f32 with a per-output-row scale vector row_scale fp32 [N] (device)
+ * in place of s_w: y[m][n] = ((float)acc * s_x[m]) * row_scale[n].  This is the
+ * `scales` argument of ternary_matmul (src/rotor/gpu_ternary.py:141,175). */
+int rt_linear_f32_rowscale(rt_ctx* ctx, const rt_weights* w, const float* x, int M,
+                           const float* row_scale, float* y);
+
+/* Prepared launch of G ternary linears in one kernel (e.g. q/k/v or gate/up, which
+ * share their input, src/rotor/transformer.py:235-237,329-330): problem g reads
+ * x[g] fp32 [M][K_g] and writes y[g] fp32 [M][N_g].  Problems whose x pointers are
+ * equal share one quantisation.  The pointer arrays are host arrays copied at
+ * creation; the device buffers they name must outlive the plan. */
+int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* const* x, int M,
+                   float* const* y, rt_plan** out);
+int rt_plan_run(rt_ctx* ctx, const rt_plan* plan);
+/* The two launches of rt_plan_run, for callers that schedule them apart (e.g. to time
+ * or overlap them): quantise the plan's distinct inputs, then run its GEMV launch on
+ * the activations quantised last. */
+int rt_plan_quantize(rt_ctx* ctx, const rt_plan* plan);
+int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan);
+int rt_plan_free(rt_plan* plan);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ROTOR_HIP_H */

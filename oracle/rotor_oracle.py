@@ -1,0 +1,273 @@
+"""CPU oracle for the rotor ternary-linear path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product package (``rotor-rag_amd/``)
+imports this module; only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may use it, and only as the checker.
+
+Every function restates, in NumPy, the algorithm of a reference function and
+cites it (paths relative to the reference repository BikerSam86/rotor-RAG).
+How each function is pinned (golden vectors / closed forms / invariants /
+cross-check against the reference's own C core built under ``oracle/_ref``)
+is listed in ``PINNED`` at the bottom of this file; the tests in
+``tests/test_oracle_*.py`` carry out those checks.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# a1: the rotor 2-bit code.  value = bit0 - bit1;  00 -> 0, 10 -> +1, 01 -> -1,
+# 11 -> error (decodes to 0).  Element j of a packed byte sits in bits
+# (2j+1, 2j) = (bit0, bit1), i.e. the 2-bit field (byte >> 2j) & 3 is 2*bit0+bit1.
+# ---------------------------------------------------------------------------
+
+
+def encode(values):
+    """{-1,0,+1} -> (bit0, bit1).  src/rotor/core.py:27-53."""
+    v = np.asarray(values).astype(np.int8)
+    return (v == 1).astype(np.uint8), (v == -1).astype(np.uint8)
+
+
+def decode(bit0, bit1):
+    """(bit0, bit1) -> bit0 - bit1 as int8.  src/rotor/core.py:56-72."""
+    return np.asarray(bit0).astype(np.int8) - np.asarray(bit1).astype(np.int8)
+
+
+def check_errors(bit0, bit1):
+    """True where both bits are set (the reserved 11 code).  src/rotor/core.py:233-243."""
+    return (np.asarray(bit0) & np.asarray(bit1)).astype(bool)
+
+
+def pack(bit0, bit1):
+    """Pack 4 rotors per byte, element j -> bits (2j+1, 2j) = (bit0, bit1).
+
+    src/rotor/core.py:75-110 (layout at :99-108).  Length must be a multiple of 4.
+    """
+    b0 = np.asarray(bit0).astype(np.uint8).reshape(-1, 4)
+    b1 = np.asarray(bit1).astype(np.uint8).reshape(-1, 4)
+    out = np.zeros(b0.shape[0], dtype=np.uint8)
+    for j in range(4):
+        out |= (b0[:, j] << (2 * j + 1)).astype(np.uint8)
+        out |= (b1[:, j] << (2 * j)).astype(np.uint8)
+    return out
+
+
+def unpack(packed, n_rotors):
+    """Inverse of :func:`pack`, truncated to ``n_rotors``.  src/rotor/core.py:113-141."""
+    p = np.asarray(packed, dtype=np.uint8)[: (n_rotors + 3) // 4]
+    b0 = np.stack([(p >> (2 * j + 1)) & 1 for j in range(4)], axis=1).ravel()[:n_rotors]
+    b1 = np.stack([(p >> (2 * j)) & 1 for j in range(4)], axis=1).ravel()[:n_rotors]
+    return b0.astype(np.uint8), b1.astype(np.uint8)
+
+
+def pack_rotor(W):
+    """Ternary matrix W [N, K] (int) -> rotor bytes [N, ceil(K/4)], rows packed
+    independently (K padded with zero codes to a multiple of 4).
+
+    This is the host-facing weight format of the build: the same per-byte layout as
+    src/rotor/core.py:99-108 and the same row convention as the reference's BitNet
+    tensors ``[out_features, in_features_packed]`` (src/rotor/transformer.py:82,90;
+    native/c/rotor_core.c:221-242).
+    """
+    W = np.asarray(W)
+    N, K = W.shape
+    Kp = (K + 3) // 4 * 4
+    Wp = np.zeros((N, Kp), dtype=np.int8)
+    Wp[:, :K] = W
+    b0, b1 = encode(Wp)
+    return pack(b0.ravel(), b1.ravel()).reshape(N, Kp // 4)
+
+
+def unpack_rotor(packed, K):
+    """Rotor bytes [N, Kb] -> int8 W [N, K].  Field value f = (byte >> 2j) & 3,
+    w = (f >> 1) - (f & 1): 00->0, 10->+1, 01->-1, 11->0
+    (native/c/rotor_core.c:240-256; src/rotor/core.py:56-72,113-141)."""
+    p = np.asarray(packed, dtype=np.uint8)
+    N, Kb = p.shape
+    f = np.stack([(p >> (2 * j)) & 3 for j in range(4)], axis=2).reshape(N, Kb * 4)
+    w = ((f >> 1).astype(np.int8) - (f & 1).astype(np.int8))
+    return w[:, :K].copy()
+
+
+# ---------------------------------------------------------------------------
+# a2/a3: BitNet bytes <-> LSB-first bit planes <-> int8 (the reference's load path)
+# ---------------------------------------------------------------------------
+
+
+def bitnet_to_rotor(bitnet_packed, cols=None):
+    """4/byte codes [rows, cb] -> planes (bit0, bit1) [rows, ceil(cols/8)], LSB-first.
+
+    native/c/rotor_core.c:202-260 (and the Python twin src/rotor/bitnet.py:76-151).
+    ``cols`` defaults to 4*cb as in src/rotor/bitnet_fast.py:71.
+    """
+    p = np.asarray(bitnet_packed, dtype=np.uint8)
+    rows, cb = p.shape
+    cols = cb * 4 if cols is None else cols
+    f = np.stack([(p >> (2 * j)) & 3 for j in range(4)], axis=2).reshape(rows, cb * 4)[:, :cols]
+    nb = (cols + 7) // 8
+    pos = np.zeros((rows, nb * 8), dtype=np.uint8)
+    neg = np.zeros((rows, nb * 8), dtype=np.uint8)
+    pos[:, :cols] = (f == 2)
+    neg[:, :cols] = (f == 1)
+    weights = (1 << np.arange(8, dtype=np.uint16))
+    bit0 = (pos.reshape(rows, nb, 8) * weights).sum(axis=2).astype(np.uint8)
+    bit1 = (neg.reshape(rows, nb, 8) * weights).sum(axis=2).astype(np.uint8)
+    return bit0, bit1
+
+
+def rotor_unpack_weights(bit0, bit1, rows, cols):
+    """Planes [rows, ceil(cols/8)] -> int8 [rows, cols], w = bit0 - bit1, LSB-first.
+
+    native/c/rotor_core.c:270-299 (called via src/rotor/transformer.py:157-171).
+    """
+    b0 = np.unpackbits(np.asarray(bit0, dtype=np.uint8).reshape(rows, -1), axis=1, bitorder="little")
+    b1 = np.unpackbits(np.asarray(bit1, dtype=np.uint8).reshape(rows, -1), axis=1, bitorder="little")
+    return (b0[:, :cols].astype(np.int8) - b1[:, :cols].astype(np.int8))
+
+
+# ---------------------------------------------------------------------------
+# a4: absmax int8 quantiser, applied per row (per token)
+# ---------------------------------------------------------------------------
+
+
+def quant_rows(x):
+    """Per-row symmetric absmax int8 quantiser.
+
+    The formula is src/rotor/quantization.py:137-149 (bits=8, symmetric) applied to
+    each row: s = max|x| / 127 (1.0 when max|x| == 0), q = clip(round_half_even(x / s),
+    -128, 127).  All arithmetic is pinned to float32 (IEEE division, NumPy's
+    round-half-even), which is what the reference computes under NumPy 2 for fp32 x.
+    Returns q int8 [M, K] and s float32 [M].
+    """
+    x = np.asarray(x, dtype=np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    amax = np.max(np.abs(x2), axis=1) if x2.shape[1] else np.zeros(x2.shape[0], np.float32)
+    safe = np.where(amax > 0, amax, np.float32(127.0)).astype(np.float32)
+    s = np.where(amax > 0, safe / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+    q = np.clip(np.round(x2 / s[:, None]), -128, 127).astype(np.int8)
+    return q.reshape(x.shape), s
+
+
+def dequant_rows(q, s):
+    """x_hat = q * s (fp32), the per-row form of src/rotor/quantization.py:169-183."""
+    q = np.asarray(q)
+    return (q.astype(np.float32) * np.asarray(s, np.float32).reshape(-1, 1)).reshape(q.shape)
+
+
+# ---------------------------------------------------------------------------
+# a5: the ternary linear
+# ---------------------------------------------------------------------------
+
+
+def linear_i64(q, W):
+    """Exact integer accumulators acc[m, n] = sum_k q[m, k] * W[n, k] in int64."""
+    return np.asarray(q, dtype=np.int64) @ np.asarray(W, dtype=np.int64).T
+
+
+def linear_i64_fast(q, W):
+    """Same result as :func:`linear_i64` computed with float64 BLAS.
+
+    Exact: every product and partial sum is an integer of magnitude < 2**53
+    (|q| <= 128, |W| <= 1, K < 2**40), so no rounding occurs.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    W = np.asarray(W, dtype=np.float64)
+    assert q.shape[-1] < (1 << 40)
+    return (q @ W.T).astype(np.int64)
+
+
+def linear_ref_f32(x, W_i8, scale):
+    """The reference's CPU ternary path: ``np.dot(x_flat, weights_cache.T) * scale``.
+
+    src/rotor/transformer.py:150 (2-D/3-D reshape rules :121-128, :152-155).  Note
+    NumPy up-casts the int8 weight cache to float32 for the product (as the
+    reference does on every call).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    shp = x.shape
+    xf = x.reshape(-1, shp[-1])
+    y = np.dot(xf, np.asarray(W_i8).T) * np.float32(scale)
+    y = y.astype(np.float32)
+    return y.reshape(shp[:-1] + (y.shape[-1],))
+
+
+def ternary_linear(x, W_i8, scale):
+    """fp32 parity reference for the W2A8 path on the *same quantised inputs*:
+    q, s = quant_rows(x); x_hat = q * s; y = np.dot(x_hat, W.T) * scale.
+
+    Returns (y, q, s, acc) where acc is the exact int64 accumulator.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    q, s = quant_rows(x.reshape(-1, x.shape[-1]))
+    xh = dequant_rows(q, s)
+    y = linear_ref_f32(xh, W_i8, scale).reshape(x.shape[:-1] + (np.asarray(W_i8).shape[0],))
+    return y, q, s, linear_i64_fast(q, W_i8)
+
+
+# ---------------------------------------------------------------------------
+# a9/a10 glue (cfg 1): RMSNorm and the FFN block restated with the config semantics
+# ---------------------------------------------------------------------------
+
+
+def rms_norm(x, weight, eps=1e-6):
+    """x / sqrt(mean(x^2) + eps) * w.  src/rotor/transformer.py:24-36 (eps :20)."""
+    x = np.asarray(x, dtype=np.float32)
+    norm = np.sqrt(np.mean(x ** 2, axis=-1, keepdims=True) + np.float32(eps)).astype(np.float32)
+    return ((x / norm) * np.asarray(weight, np.float32)).astype(np.float32)
+
+
+def relu2_gate(g, u):
+    """relu(g)^2 * u in float32 (the configuration's FFN activation)."""
+    g = np.asarray(g, np.float32)
+    r = np.maximum(g, np.float32(0))
+    return (r * r * np.asarray(u, np.float32)).astype(np.float32)
+
+
+def ffn_block(x, norm_w, Wg, sg, Wu, su, Wd, sd, eps=1e-6):
+    """cfg 1: RMSNorm -> gate & up ternary linears -> relu^2(gate)*up -> down.
+
+    Every ternary linear is the W2A8 form of :func:`ternary_linear` (per-token int8
+    activations); the callers it restates are GatedFFN.forward
+    (src/rotor/transformer.py:320-341) with the configuration's relu^2 activation in
+    place of the reference's SiLU and no sub-norm.  Returns y and the intermediates.
+    """
+    h = rms_norm(x, norm_w, eps)
+    g, qh, sh, acc_g = ternary_linear(h, Wg, sg)
+    u, _, _, acc_u = ternary_linear(h, Wu, su)
+    a = relu2_gate(g, u)
+    y, qa, sa, acc_d = ternary_linear(a, Wd, sd)
+    return y, dict(h=h, qh=qh, sh=sh, g=g, u=u, acc_g=acc_g, acc_u=acc_u, a=a, qa=qa, sa=sa, acc_d=acc_d)
+
+
+# ---------------------------------------------------------------------------
+# Seeded synthetic inputs (the generators of the benchmark configurations)
+# ---------------------------------------------------------------------------
+
+
+def make_ternary(rng, N, K):
+    """W iid with P(-1)=0.3, P(0)=0.4, P(+1)=0.3, then a per-tensor scale ~ U(0.01, 0.05)."""
+    W = rng.choice(np.array([-1, 0, 1], dtype=np.int8), size=(N, K), p=[0.3, 0.4, 0.3]).astype(np.int8)
+    scale = np.float32(rng.uniform(0.01, 0.05))
+    return W, scale
+
+
+def make_linear_case(seed, M, N, K):
+    """One seeded ternary-linear case: (x fp32 [M,K] ~ N(0,1), W int8 [N,K], scale)."""
+    rng = np.random.default_rng(seed)
+    W, scale = make_ternary(rng, N, K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    return x, W, scale
+
+
+PINNED = {
+    "encode/decode/pack/unpack": "reference KATs (tests/test_core.py:19-34,85-107; src/rotor/bitnet.py:95,345-354; "
+                                 "tests/debug_bitnet_format.py:20-27) + oracle/_ref round-trip",
+    "pack_rotor/unpack_rotor": "byte KATs 0x86/0x21/0x24/0x12/0x68/0x81/0x60/0x80 + exhaustive 256-byte table vs "
+                               "oracle/_ref bitnet_to_rotor+rotor_unpack_weights",
+    "bitnet_to_rotor/rotor_unpack_weights": "bit-exact vs oracle/_ref (reference C core) on random and ragged shapes",
+    "quant_rows": "KAT [127,.5,1.5,2.5,-.5,-1.5,3.49,-126.5] -> [127,0,2,2,0,-2,3,-126]; zero row; invariants "
+                  "(max element -> +-127, |x - q s| <= s/2, scale equivariance)",
+    "linear_i64": "brute-force loops on tiny shapes; linear_i64 == linear_i64_fast; linearity in q",
+    "linear_ref_f32/ternary_linear": "float64 closed form on the same quantised inputs (|diff| << 3e-4)",
+    "rms_norm/relu2_gate/ffn_block": "closed forms: constant rows, unit weight, sign cases",
+}

@@ -1,0 +1,452 @@
+// C ABI of librotor_hip.so (declared in include/rotor_hip.h).
+//
+// The reference's GPU plug-in object (src/rotor/gpu_ternary.py:73-208) becomes an
+// opaque context plus device-resident weight handles; every entry point returns a
+// status code and leaves a thread-local message instead of raising
+// (src/rotor/gpu_layers.py:18-25 latches on exceptions).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/rotor_hip.h"
+#include "rt_internal.h"
+
+using namespace rt;
+
+namespace {
+
+thread_local std::string g_err = "";
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(RT_EHIP, std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")");
+}
+
+#define RT_HIP(call)                                   \
+    do {                                               \
+        hipError_t _e = (call);                        \
+        if (_e != hipSuccess) return hip_fail(_e, #call); \
+    } while (0)
+
+// Keeps the device current for the scope of an entry point.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+// Device buffer that only grows.
+struct Scratch {
+    void* p = nullptr;
+    size_t bytes = 0;
+    hipError_t ensure(size_t need) {
+        if (need <= bytes) return hipSuccess;
+        if (p) {
+            hipError_t e = hipFree(p);
+            if (e != hipSuccess) return e;
+            p = nullptr;
+            bytes = 0;
+        }
+        size_t cap = need < 4096 ? 4096 : need;
+        hipError_t e = hipMalloc(&p, cap);
+        if (e == hipSuccess) bytes = cap;
+        return e;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+};
+
+}  // namespace
+
+struct rt_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    Scratch act;  // qx [Mpad][Kp] followed by sx [Mpad]
+};
+
+struct rt_weights {
+    int device = 0;
+    int N = 0, K = 0, Kp = 0, C = 0, Np = 0;
+    float scale = 1.0f;
+    v4u* tiles = nullptr;
+    size_t bytes = 0;
+};
+
+struct rt_plan {
+    int device = 0;
+    int G = 0, M = 0, Mpad = 0, mt = 1, nw = 1, total_wgs = 0, U = 0;
+    GemvProb* dev_probs = nullptr;   // [G]
+    QuantProb* dev_quant = nullptr;  // [U]
+    void* act = nullptr;             // quantised activations of the U distinct inputs
+    std::vector<GemvProb> probs;
+    std::vector<QuantProb> quant;
+};
+
+extern "C" {
+
+const char* rt_last_error(void) { return g_err.c_str(); }
+
+int rt_version(void) { return 100; }
+
+int rt_device_count(int* n) {
+    if (!n) return fail(RT_EINVAL, "rt_device_count: n is NULL");
+    int c = 0;
+    hipError_t e = hipGetDeviceCount(&c);
+    *n = e == hipSuccess ? c : 0;
+    return RT_OK;
+}
+
+int rt_ctx_create(int device, rt_ctx** out) {
+    if (!out) return fail(RT_EINVAL, "rt_ctx_create: out is NULL");
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(RT_ENODEV, "rt_ctx_create: no HIP device visible");
+    if (device < 0 || device >= n) return fail(RT_EINVAL, "rt_ctx_create: device index out of range");
+    hipDeviceProp_t prop;
+    RT_HIP(hipGetDeviceProperties(&prop, device));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(RT_ENODEV, std::string("rt_ctx_create: device is ") + prop.gcnArchName +
+                                   ", this library is built for gfx950 only");
+    RT_HIP(hipSetDevice(device));
+    rt_ctx* c = new rt_ctx();
+    c->device = device;
+    *out = c;
+    return RT_OK;
+}
+
+int rt_ctx_destroy(rt_ctx* ctx) {
+    if (!ctx) return RT_OK;
+    DeviceGuard g(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream); else (void)hipDeviceSynchronize();
+    ctx->act.release();
+    delete ctx;
+    return RT_OK;
+}
+
+int rt_ctx_set_stream(rt_ctx* ctx, void* hip_stream) {
+    if (!ctx) return fail(RT_EINVAL, "rt_ctx_set_stream: ctx is NULL");
+    ctx->stream = static_cast<hipStream_t>(hip_stream);
+    return RT_OK;
+}
+
+int rt_sync(rt_ctx* ctx) {
+    if (!ctx) return fail(RT_EINVAL, "rt_sync: ctx is NULL");
+    DeviceGuard g(ctx->device);
+    RT_HIP(hipStreamSynchronize(ctx->stream));
+    return RT_OK;
+}
+
+static int weights_alloc(rt_ctx* ctx, int N, int K, float scale, rt_weights** out) {
+    if (!ctx || !out) return fail(RT_EINVAL, "rt_weights_upload: ctx/out is NULL");
+    if (N <= 0 || K <= 0) return fail(RT_EINVAL, "rt_weights_upload: N and K must be positive");
+    if ((long long)K > (1LL << 24) || (long long)N > (1LL << 26))
+        return fail(RT_EINVAL, "rt_weights_upload: N or K too large");
+    rt_weights* w = new rt_weights();
+    w->device = ctx->device;
+    w->N = N;
+    w->K = K;
+    w->Kp = round_up(K, kChunk);
+    w->C = w->Kp / kChunk;
+    w->Np = round_up(N, kRowBlock);
+    w->scale = scale;
+    w->bytes = (size_t)w->Np * w->Kp / 4;
+    hipError_t e = hipMalloc(&w->tiles, w->bytes);
+    if (e != hipSuccess) {
+        delete w;
+        return fail(RT_ENOMEM, std::string("rt_weights_upload: hipMalloc failed: ") + hipGetErrorName(e));
+    }
+    *out = w;
+    return RT_OK;
+}
+
+int rt_weights_upload_device(rt_ctx* ctx, const uint8_t* rotor_dev, int N, int K, float scale, rt_weights** out) {
+    if (!rotor_dev) return fail(RT_EINVAL, "rt_weights_upload_device: source is NULL");
+    DeviceGuard g(ctx ? ctx->device : 0);
+    int rc = weights_alloc(ctx, N, K, scale, out);
+    if (rc) return rc;
+    hipError_t e = launch_relayout(rotor_dev, N, K, (*out)->tiles, ctx->stream);
+    if (e != hipSuccess) {
+        rt_weights_free(*out);
+        *out = nullptr;
+        return hip_fail(e, "relayout launch");
+    }
+    return RT_OK;
+}
+
+int rt_weights_upload(rt_ctx* ctx, const uint8_t* rotor_host, int N, int K, float scale, rt_weights** out) {
+    if (!rotor_host) return fail(RT_EINVAL, "rt_weights_upload: source is NULL");
+    if (!ctx) return fail(RT_EINVAL, "rt_weights_upload: ctx is NULL");
+    DeviceGuard g(ctx->device);
+    int rc = weights_alloc(ctx, N, K, scale, out);
+    if (rc) return rc;
+    const size_t src_bytes = (size_t)N * ((K + 3) / 4);
+    uint8_t* tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, src_bytes);
+    if (e == hipSuccess) e = hipMemcpyAsync(tmp, rotor_host, src_bytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = launch_relayout(tmp, N, K, (*out)->tiles, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (tmp) (void)hipFree(tmp);
+    if (e != hipSuccess) {
+        rt_weights_free(*out);
+        *out = nullptr;
+        return hip_fail(e, "rt_weights_upload");
+    }
+    return RT_OK;
+}
+
+int rt_weights_download(rt_ctx* ctx, const rt_weights* w, uint8_t* rotor_host) {
+    if (!ctx || !w || !rotor_host) return fail(RT_EINVAL, "rt_weights_download: NULL argument");
+    DeviceGuard g(ctx->device);
+    const size_t bytes = (size_t)w->N * ((w->K + 3) / 4);
+    uint8_t* tmp = nullptr;
+    hipError_t e = hipMalloc(&tmp, bytes);
+    if (e == hipSuccess) e = launch_unrelayout(w->tiles, w->N, w->K, tmp, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(rotor_host, tmp, bytes, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (tmp) (void)hipFree(tmp);
+    if (e != hipSuccess) return hip_fail(e, "rt_weights_download");
+    return RT_OK;
+}
+
+int rt_weights_info(const rt_weights* w, int* N, int* K, float* scale) {
+    if (!w) return fail(RT_EINVAL, "rt_weights_info: w is NULL");
+    if (N) *N = w->N;
+    if (K) *K = w->K;
+    if (scale) *scale = w->scale;
+    return RT_OK;
+}
+
+int rt_weights_free(rt_weights* w) {
+    if (!w) return RT_OK;
+    DeviceGuard g(w->device);
+    if (w->tiles) (void)hipFree(w->tiles);
+    delete w;
+    return RT_OK;
+}
+
+// --- activations -----------------------------------------------------------------
+
+static int check_act(const rt_ctx* ctx, int M, int K, const char* who) {
+    if (!ctx) return fail(RT_EINVAL, std::string(who) + ": ctx is NULL");
+    if (M <= 0 || K <= 0) return fail(RT_EINVAL, std::string(who) + ": M and K must be positive");
+    if (M > (1 << 24)) return fail(RT_EINVAL, std::string(who) + ": M too large");
+    return RT_OK;
+}
+
+// Quantise (x != NULL) or permute (q_in != NULL) M rows of K into the context scratch.
+static int stage_activations(rt_ctx* ctx, const float* x, const int8_t* q_in, int M, int K, int Mpad,
+                             int8_t* q_nat, float* s_out, int8_t** qx, float** sx) {
+    const int Kp = round_up(K, kChunk);
+    const size_t qbytes = (size_t)Mpad * Kp;
+    RT_HIP(ctx->act.ensure(qbytes + (size_t)Mpad * sizeof(float)));
+    *qx = static_cast<int8_t*>(ctx->act.p);
+    *sx = reinterpret_cast<float*>(static_cast<char*>(ctx->act.p) + qbytes);
+    QuantArgs a{};
+    a.dev = nullptr;
+    a.U = 1;
+    a.M = M;
+    a.Mpad = Mpad;
+    a.p[0] = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp};
+    RT_HIP(launch_quant(a, ctx->stream));
+    if (s_out) RT_HIP(hipMemcpyAsync(s_out, *sx, (size_t)M * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+    return RT_OK;
+}
+
+int rt_quantize_rows(rt_ctx* ctx, const float* x, int M, int K, int8_t* q, float* s) {
+    int rc = check_act(ctx, M, K, "rt_quantize_rows");
+    if (rc) return rc;
+    if (!x || !q || !s) return fail(RT_EINVAL, "rt_quantize_rows: NULL pointer");
+    DeviceGuard g(ctx->device);
+    int8_t* qx;
+    float* sx;
+    return stage_activations(ctx, x, nullptr, M, K, round_up(M, kTokPad), q, s, &qx, &sx);
+}
+
+static int run_linear(rt_ctx* ctx, const rt_weights* w, const float* x, const int8_t* q, int M,
+                      const float* row_scale, void* out, bool out_i32, const char* who) {
+    if (!w) return fail(RT_EINVAL, std::string(who) + ": weights are NULL");
+    int rc = check_act(ctx, M, w->K, who);
+    if (rc) return rc;
+    if ((!x && !q) || !out) return fail(RT_EINVAL, std::string(who) + ": NULL pointer");
+    if (w->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": weights live on another device");
+    DeviceGuard g(ctx->device);
+    const int mt = gemv_mt(M);
+    int8_t* qx;
+    float* sx;
+    rc = stage_activations(ctx, x, q, M, w->K, round_up(M, kTokPad), nullptr, nullptr, &qx, &sx);
+    if (rc) return rc;
+    GemvArgs a{};
+    a.dev = nullptr;
+    a.G = 1;
+    a.M = M;
+    a.out_i32 = out_i32 ? 1 : 0;
+    a.p[0] = GemvProb{w->tiles, qx, sx, row_scale, out, w->scale, w->N, w->C, w->N, 0};
+    const int wgs = w->Np / kRowBlock;
+    const int nw = gemv_waves(wgs * ((M + mt - 1) / mt), w->C);
+    RT_HIP(launch_gemv(a, wgs, mt, nw, ctx->stream));
+    return RT_OK;
+}
+
+int rt_linear_i32(rt_ctx* ctx, const rt_weights* w, const int8_t* q, int M, int32_t* acc) {
+    if (!q) return fail(RT_EINVAL, "rt_linear_i32: q is NULL");
+    return run_linear(ctx, w, nullptr, q, M, nullptr, acc, true, "rt_linear_i32");
+}
+
+int rt_linear_f32(rt_ctx* ctx, const rt_weights* w, const float* x, int M, float* y) {
+    if (!x) return fail(RT_EINVAL, "rt_linear_f32: x is NULL");
+    return run_linear(ctx, w, x, nullptr, M, nullptr, y, false, "rt_linear_f32");
+}
+
+int rt_linear_f32_rowscale(rt_ctx* ctx, const rt_weights* w, const float* x, int M, const float* row_scale,
+                           float* y) {
+    if (!x || !row_scale) return fail(RT_EINVAL, "rt_linear_f32_rowscale: NULL pointer");
+    return run_linear(ctx, w, x, nullptr, M, row_scale, y, false, "rt_linear_f32_rowscale");
+}
+
+// --- plans -----------------------------------------------------------------------
+
+int rt_plan_free(rt_plan* plan) {
+    if (!plan) return RT_OK;
+    DeviceGuard g(plan->device);
+    if (plan->dev_probs) (void)hipFree(plan->dev_probs);
+    if (plan->dev_quant) (void)hipFree(plan->dev_quant);
+    if (plan->act) (void)hipFree(plan->act);
+    delete plan;
+    return RT_OK;
+}
+
+int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* const* x, int M, float* const* y,
+                   rt_plan** out) {
+    if (!ctx || !w || !x || !y || !out) return fail(RT_EINVAL, "rt_plan_create: NULL argument");
+    *out = nullptr;
+    if (G <= 0 || G > (1 << 16)) return fail(RT_EINVAL, "rt_plan_create: G out of range");
+    if (M <= 0 || M > (1 << 24)) return fail(RT_EINVAL, "rt_plan_create: M out of range");
+    for (int g = 0; g < G; ++g) {
+        if (!w[g] || !x[g] || !y[g]) return fail(RT_EINVAL, "rt_plan_create: NULL entry in a pointer array");
+        if (w[g]->device != ctx->device) return fail(RT_EINVAL, "rt_plan_create: weights live on another device");
+    }
+    DeviceGuard guard(ctx->device);
+    rt_plan* p = new rt_plan();
+    p->device = ctx->device;
+    p->G = G;
+    p->M = M;
+    p->Mpad = round_up(M, kTokPad);
+    p->mt = gemv_mt(M);
+    // distinct inputs (same pointer => same quantisation; their K must agree)
+    std::unordered_map<const float*, int> uid;
+    std::vector<int> which(G);
+    std::vector<int> Ku;
+    for (int g = 0; g < G; ++g) {
+        auto it = uid.find(x[g]);
+        if (it == uid.end()) {
+            which[g] = (int)Ku.size();
+            uid.emplace(x[g], which[g]);
+            Ku.push_back(w[g]->K);
+        } else {
+            which[g] = it->second;
+            if (Ku[it->second] != w[g]->K) {
+                delete p;
+                return fail(RT_EINVAL, "rt_plan_create: problems sharing an input have different K");
+            }
+        }
+    }
+    p->U = (int)Ku.size();
+    std::vector<size_t> qoff(p->U), soff(p->U);
+    size_t total = 0;
+    for (int u = 0; u < p->U; ++u) {
+        qoff[u] = total;
+        total += (size_t)p->Mpad * round_up(Ku[u], kChunk);
+        total = (total + 255) / 256 * 256;
+    }
+    for (int u = 0; u < p->U; ++u) {
+        soff[u] = total;
+        total += (size_t)p->Mpad * sizeof(float);
+        total = (total + 255) / 256 * 256;
+    }
+    hipError_t e = hipMalloc(&p->act, total);
+    if (e != hipSuccess) {
+        delete p;
+        return fail(RT_ENOMEM, "rt_plan_create: activation buffer allocation failed");
+    }
+    char* base = static_cast<char*>(p->act);
+    p->quant.resize(p->U);
+    for (int g = 0; g < G; ++g) {
+        const int u = which[g];
+        p->quant[u] = QuantProb{x[g], nullptr, reinterpret_cast<int8_t*>(base + qoff[u]),
+                                reinterpret_cast<float*>(base + soff[u]), nullptr, Ku[u], round_up(Ku[u], kChunk)};
+    }
+    int wg = 0, minC = 1 << 30;
+    p->probs.resize(G);
+    for (int g = 0; g < G; ++g) {
+        const int u = which[g];
+        p->probs[g] = GemvProb{w[g]->tiles, p->quant[u].qx, p->quant[u].sx, nullptr, y[g], w[g]->scale,
+                               w[g]->N, w[g]->C, w[g]->N, wg};
+        wg += w[g]->Np / kRowBlock;
+        if (w[g]->C < minC) minC = w[g]->C;
+    }
+    p->total_wgs = wg;
+    p->nw = gemv_waves(wg * ((M + p->mt - 1) / p->mt), minC);
+    e = hipMalloc(&p->dev_probs, sizeof(GemvProb) * G);
+    if (e == hipSuccess) e = hipMalloc(&p->dev_quant, sizeof(QuantProb) * p->U);
+    if (e == hipSuccess)
+        e = hipMemcpy(p->dev_probs, p->probs.data(), sizeof(GemvProb) * G, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(p->dev_quant, p->quant.data(), sizeof(QuantProb) * p->U, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        rt_plan_free(p);
+        return hip_fail(e, "rt_plan_create");
+    }
+    *out = p;
+    return RT_OK;
+}
+
+int rt_plan_quantize(rt_ctx* ctx, const rt_plan* plan) {
+    if (!ctx || !plan) return fail(RT_EINVAL, "rt_plan_quantize: NULL argument");
+    if (plan->device != ctx->device) return fail(RT_EINVAL, "rt_plan_quantize: plan belongs to another device");
+    DeviceGuard g(ctx->device);
+    QuantArgs q{};
+    q.dev = plan->dev_quant;
+    q.U = plan->U;
+    q.M = plan->M;
+    q.Mpad = plan->Mpad;
+    RT_HIP(launch_quant(q, ctx->stream));
+    return RT_OK;
+}
+
+int rt_plan_run(rt_ctx* ctx, const rt_plan* plan) {
+    int rc = rt_plan_quantize(ctx, plan);
+    return rc ? rc : rt_plan_gemv(ctx, plan);
+}
+
+int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
+    if (!ctx || !plan) return fail(RT_EINVAL, "rt_plan_gemv: NULL argument");
+    if (plan->device != ctx->device) return fail(RT_EINVAL, "rt_plan_gemv: plan belongs to another device");
+    DeviceGuard g(ctx->device);
+    GemvArgs a{};
+    a.dev = plan->dev_probs;
+    a.G = plan->G;
+    a.M = plan->M;
+    a.out_i32 = 0;
+    RT_HIP(launch_gemv(a, plan->total_wgs, plan->mt, plan->nw, ctx->stream));
+    return RT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,83 @@
+"""ctypes binding of librotor_hip.so (the C ABI in include/rotor_hip.h).
+
+Follows the reference's ctypes pattern for its native core
+(src/rotor/bitnet_fast.py:15-48 library search, :86-102 argtypes/restype), with two
+differences: every call's status is checked and turned into ``RuntimeError`` with the
+library's own message, and a missing library is an error, never a silent fallback.
+
+Library search order: ``$ROTOR_HIP_LIB`` if set, else ``rotor/lib/librotor_hip.so``
+next to this file (built in-tree by ``rotor-rag_amd/csrc/build.py``).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "librotor_hip.so"
+
+# name -> (restype, argtypes); every entry point of include/rotor_hip.h
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+SIGNATURES = {
+    "rt_last_error": (ctypes.c_char_p, []),
+    "rt_version": (_I, []),
+    "rt_device_count": (_I, [ctypes.POINTER(_I)]),
+    "rt_ctx_create": (_I, [_I, ctypes.POINTER(_P)]),
+    "rt_ctx_destroy": (_I, [_P]),
+    "rt_ctx_set_stream": (_I, [_P, _P]),
+    "rt_sync": (_I, [_P]),
+    "rt_weights_upload": (_I, [_P, _P, _I, _I, _F, ctypes.POINTER(_P)]),
+    "rt_weights_upload_device": (_I, [_P, _P, _I, _I, _F, ctypes.POINTER(_P)]),
+    "rt_weights_download": (_I, [_P, _P, _P]),
+    "rt_weights_info": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_F)]),
+    "rt_weights_free": (_I, [_P]),
+    "rt_quantize_rows": (_I, [_P, _P, _I, _I, _P, _P]),
+    "rt_linear_i32": (_I, [_P, _P, _P, _I, _P]),
+    "rt_linear_f32": (_I, [_P, _P, _P, _I, _P]),
+    "rt_linear_f32_rowscale": (_I, [_P, _P, _P, _I, _P, _P]),
+    "rt_plan_create": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, ctypes.POINTER(_P),
+                            ctypes.POINTER(_P)]),
+    "rt_plan_run": (_I, [_P, _P]),
+    "rt_plan_quantize": (_I, [_P, _P]),
+    "rt_plan_gemv": (_I, [_P, _P]),
+    "rt_plan_free": (_I, [_P]),
+}
+
+_lib = None
+
+
+def lib_path() -> Path:
+    env = os.environ.get("ROTOR_HIP_LIB")
+    return Path(env) if env else LIB_PATH
+
+
+def load():
+    """Load (once) and return the library; raises RuntimeError when it cannot be loaded."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = lib_path()
+    if not path.exists():
+        raise RuntimeError(f"librotor_hip.so not found at {path} (build it with rotor-rag_amd/csrc/build.py)")
+    try:
+        lib = ctypes.CDLL(str(path))
+    except OSError as e:
+        raise RuntimeError(f"cannot load {path}: {e}") from e
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError here = ABI mismatch, let it surface
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().rt_last_error().decode(errors="replace")
+
+
+def check(rc: int, what: str = "") -> None:
+    """Raise RuntimeError with the library's message for a non-zero status."""
+    if rc != 0:
+        raise RuntimeError(f"{what or 'librotor_hip'} failed (status {rc}): {last_error()}")

@@ -1,0 +1,261 @@
+"""HIP backend of the ternary linear for MI355X (gfx950).
+
+Drop-in for the reference's OpenCL plug-in ``GPUTernaryOps``
+(src/rotor/gpu_ternary.py:73-208): same duck type -- ``pack_ternary_weights(W)`` and
+``ternary_matmul(packed, scales, input_vec, in_dim, out_dim)`` -- plus batched entry
+points (``linear``, ``linear_i32``, ``quantize_rows``, ``plan``) that the reference
+lacks (it loops over tokens, src/rotor/transformer.py:134-143).
+
+Differences from the reference, by design:
+  * weights are uploaded once and stay resident (the reference re-uploads them on
+    every call, src/rotor/gpu_ternary.py:160-164);
+  * activations are quantised per token to int8 (absmax, src/rotor/quantization.py:
+    137-149 per row) and accumulated exactly in int32 (W2A8);
+  * any failure raises ``RuntimeError``; nothing falls back to the CPU.
+
+PyTorch supplies device memory and the stream; the compute is the HIP library.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _hip
+from .format import pack_rotor_rows, unpack_rotor_rows
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+class DeviceTernaryWeights:
+    """A device-resident ternary matrix (opaque ``rt_weights`` handle)."""
+
+    def __init__(self, backend: "HIPTernaryOps", handle: ctypes.c_void_p, N: int, K: int, scale: float):
+        self._backend = backend
+        self.handle = handle
+        self.out_features = N
+        self.in_features = K
+        self.scale = float(scale)
+
+    @property
+    def shape(self):
+        return (self.out_features, self.in_features)
+
+    def download(self) -> np.ndarray:
+        """Rotor bytes [N, ceil(K/4)] read back from the device (inverse of the upload)."""
+        out = np.empty((self.out_features, (self.in_features + 3) // 4), dtype=np.uint8)
+        lib = _hip.load()
+        _hip.check(lib.rt_weights_download(self._backend.ctx, self.handle, out.ctypes.data), "rt_weights_download")
+        return out
+
+    def free(self) -> None:
+        if self.handle:
+            _hip.load().rt_weights_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class LinearPlan:
+    """G ternary linears prepared for one launch (see rt_plan_create)."""
+
+    def __init__(self, backend, handle, keep):
+        self._backend = backend
+        self.handle = handle
+        self._keep = keep  # tensors / weights the plan's device pointers refer to
+
+    def run(self) -> None:
+        b = self._backend
+        b._bind_stream()
+        _hip.check(_hip.load().rt_plan_run(b.ctx, self.handle), "rt_plan_run")
+
+    def quantize(self) -> None:
+        """First launch of run(): per-token quantisation of the distinct inputs."""
+        b = self._backend
+        b._bind_stream()
+        _hip.check(_hip.load().rt_plan_quantize(b.ctx, self.handle), "rt_plan_quantize")
+
+    def gemv(self) -> None:
+        """Second launch of run(): the ternary GEMV over all problems."""
+        b = self._backend
+        b._bind_stream()
+        _hip.check(_hip.load().rt_plan_gemv(b.ctx, self.handle), "rt_plan_gemv")
+
+    def free(self) -> None:
+        if self.handle:
+            _hip.load().rt_plan_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HIPTernaryOps:
+    """GPUTernaryOps-compatible HIP backend bound to one device."""
+
+    def __init__(self, device: int = 0):
+        torch = _torch()
+        self.lib = _hip.load()
+        if not torch.cuda.is_available():
+            raise RuntimeError("HIPTernaryOps: no GPU visible to PyTorch-ROCm")
+        self.device_index = int(device)
+        self.device = torch.device("cuda", self.device_index)
+        ctx = ctypes.c_void_p()
+        _hip.check(self.lib.rt_ctx_create(self.device_index, ctypes.byref(ctx)), "rt_ctx_create")
+        self.ctx = ctx
+        self._bind_stream()
+
+    # -- plumbing -----------------------------------------------------------------
+    def _bind_stream(self):
+        torch = _torch()
+        s = torch.cuda.current_stream(self.device)
+        _hip.check(self.lib.rt_ctx_set_stream(self.ctx, ctypes.c_void_p(s.cuda_stream)), "rt_ctx_set_stream")
+
+    def _dev(self, a, dtype):
+        """numpy/torch -> contiguous device tensor of `dtype` on this device."""
+        torch = _torch()
+        if isinstance(a, torch.Tensor):
+            t = a.to(device=self.device, dtype=dtype)
+        else:
+            t = torch.from_numpy(np.ascontiguousarray(a)).to(device=self.device, dtype=dtype)
+        return t.contiguous()
+
+    def synchronize(self):
+        _hip.check(self.lib.rt_sync(self.ctx), "rt_sync")
+
+    # -- weights ------------------------------------------------------------------
+    def upload(self, rotor_bytes, in_features: int, scale: float = 1.0) -> DeviceTernaryWeights:
+        """Rotor bytes [N, ceil(K/4)] (host) -> device-resident weights."""
+        p = np.ascontiguousarray(rotor_bytes, dtype=np.uint8)
+        if p.ndim != 2 or p.shape[1] != (in_features + 3) // 4:
+            raise ValueError(f"rotor bytes of shape {p.shape} do not hold rows of {in_features} weights")
+        h = ctypes.c_void_p()
+        _hip.check(self.lib.rt_weights_upload(self.ctx, p.ctypes.data, p.shape[0], int(in_features),
+                                              float(scale), ctypes.byref(h)), "rt_weights_upload")
+        return DeviceTernaryWeights(self, h, p.shape[0], int(in_features), scale)
+
+    def upload_device(self, rotor_bytes_dev, in_features: int, scale: float = 1.0) -> DeviceTernaryWeights:
+        """Rotor bytes already on the device (uint8 tensor [N, ceil(K/4)])."""
+        t = self._dev(rotor_bytes_dev, _torch().uint8)
+        if t.ndim != 2 or t.shape[1] != (in_features + 3) // 4:
+            raise ValueError(f"rotor bytes of shape {tuple(t.shape)} do not hold rows of {in_features} weights")
+        self._bind_stream()
+        h = ctypes.c_void_p()
+        _hip.check(self.lib.rt_weights_upload_device(self.ctx, t.data_ptr(), t.shape[0], int(in_features),
+                                                     float(scale), ctypes.byref(h)), "rt_weights_upload_device")
+        self.synchronize()
+        return DeviceTernaryWeights(self, h, t.shape[0], int(in_features), scale)
+
+    def pack_ternary_weights(self, weights, scale: float = 1.0) -> DeviceTernaryWeights:
+        """{-1,0,+1} [N, K] -> device weights.  src/rotor/gpu_ternary.py:112-136 (which
+        returned host bytes in a w+1 code); here the rotor code is uploaded once."""
+        W = np.asarray(weights)
+        if W.ndim != 2:
+            raise ValueError("pack_ternary_weights expects a 2-D [out, in] matrix")
+        return self.upload(pack_rotor_rows(W), W.shape[1], scale)
+
+    # -- compute ------------------------------------------------------------------
+    def quantize_rows(self, x):
+        """Per-token absmax int8: x [M, K] -> (q int8 [M, K], s fp32 [M]) device tensors."""
+        torch = _torch()
+        xt = self._dev(x, torch.float32)
+        M, K = xt.shape
+        q = torch.empty((M, K), dtype=torch.int8, device=self.device)
+        s = torch.empty((M,), dtype=torch.float32, device=self.device)
+        self._bind_stream()
+        _hip.check(self.lib.rt_quantize_rows(self.ctx, xt.data_ptr(), M, K, q.data_ptr(), s.data_ptr()),
+                   "rt_quantize_rows")
+        return q, s
+
+    def linear_i32(self, w: DeviceTernaryWeights, q):
+        """Exact int32 accumulators q [M, K] int8 x W^T -> [M, N] (device tensor)."""
+        torch = _torch()
+        qt = self._dev(q, torch.int8)
+        if qt.ndim != 2 or qt.shape[1] != w.in_features:
+            raise ValueError(f"q of shape {tuple(qt.shape)} does not match K={w.in_features}")
+        acc = torch.empty((qt.shape[0], w.out_features), dtype=torch.int32, device=self.device)
+        self._bind_stream()
+        _hip.check(self.lib.rt_linear_i32(self.ctx, w.handle, qt.data_ptr(), qt.shape[0], acc.data_ptr()),
+                   "rt_linear_i32")
+        return acc
+
+    def linear_device(self, w: DeviceTernaryWeights, x, row_scale=None, out=None):
+        """W2A8 ternary linear on device tensors: x [M, K] fp32 -> y [M, N] fp32."""
+        torch = _torch()
+        xt = self._dev(x, torch.float32)
+        if xt.ndim != 2 or xt.shape[1] != w.in_features:
+            raise ValueError(f"x of shape {tuple(xt.shape)} does not match K={w.in_features}")
+        M = xt.shape[0]
+        y = out if out is not None else torch.empty((M, w.out_features), dtype=torch.float32, device=self.device)
+        self._bind_stream()
+        if row_scale is None:
+            _hip.check(self.lib.rt_linear_f32(self.ctx, w.handle, xt.data_ptr(), M, y.data_ptr()), "rt_linear_f32")
+        else:
+            rs = self._dev(row_scale, torch.float32).reshape(-1)
+            if rs.numel() != w.out_features:
+                raise ValueError("row scales must have out_features entries")
+            _hip.check(self.lib.rt_linear_f32_rowscale(self.ctx, w.handle, xt.data_ptr(), M, rs.data_ptr(),
+                                                       y.data_ptr()), "rt_linear_f32_rowscale")
+        return y
+
+    def linear(self, w: DeviceTernaryWeights, x):
+        """x [M, K] numpy -> numpy y [M, N]; torch in -> torch (device) out."""
+        torch = _torch()
+        y = self.linear_device(w, x)
+        if isinstance(x, torch.Tensor):
+            return y
+        return y.cpu().numpy()
+
+    def ternary_matmul(self, packed_weights, scales, input_vec, in_dim: int, out_dim: int) -> np.ndarray:
+        """Reference duck type (src/rotor/gpu_ternary.py:138-202): one token, per-row
+        scales, numpy in and out.  ``packed_weights`` is what pack_ternary_weights
+        returned."""
+        if not isinstance(packed_weights, DeviceTernaryWeights):
+            raise TypeError("packed_weights must come from HIPTernaryOps.pack_ternary_weights")
+        if packed_weights.shape != (out_dim, in_dim):
+            raise ValueError(f"weights are {packed_weights.shape}, call asked for ({out_dim}, {in_dim})")
+        x = np.asarray(input_vec, dtype=np.float32).reshape(1, in_dim)
+        y = self.linear_device(packed_weights, x, row_scale=np.asarray(scales, dtype=np.float32))
+        return y.cpu().numpy().reshape(out_dim)
+
+    def plan(self, weights, xs, ys) -> LinearPlan:
+        """Prepare one launch of len(weights) linears: ys[g] = W_g(xs[g]); device tensors,
+        all xs with the same number of rows.  Equal xs tensors share one quantisation."""
+        G = len(weights)
+        if not (G == len(xs) == len(ys)) or G == 0:
+            raise ValueError("plan needs equal, non-zero numbers of weights, inputs and outputs")
+        M = xs[0].shape[0]
+        for w, x, y in zip(weights, xs, ys):
+            if x.shape != (M, w.in_features) or y.shape != (M, w.out_features):
+                raise ValueError("plan: tensor shapes do not match the weights")
+            if not (x.is_contiguous() and y.is_contiguous()) or x.device != self.device or y.device != self.device:
+                raise ValueError("plan: tensors must be contiguous and on the backend's device")
+        P = ctypes.c_void_p
+        wa = (P * G)(*[w.handle for w in weights])
+        xa = (P * G)(*[x.data_ptr() for x in xs])
+        ya = (P * G)(*[y.data_ptr() for y in ys])
+        h = ctypes.c_void_p()
+        _hip.check(self.lib.rt_plan_create(self.ctx, G, wa, xa, M, ya, ctypes.byref(h)), "rt_plan_create")
+        return LinearPlan(self, h, (list(weights), list(xs), list(ys)))
+
+    def __del__(self):
+        try:
+            if getattr(self, "ctx", None):
+                self.lib.rt_ctx_destroy(self.ctx)
+                self.ctx = None
+        except Exception:
+            pass
+
+
+__all__ = ["HIPTernaryOps", "DeviceTernaryWeights", "LinearPlan", "unpack_rotor_rows"]

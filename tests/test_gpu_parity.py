@@ -1,0 +1,177 @@
+"""GPU parity of the HIP ternary-linear path against the CPU oracle (through the C ABI).
+
+Bar: bit-exact int8 quantisation and int32 accumulators (vs int64 NumPy on the same
+quantised inputs); fp32 outputs within atol 3e-4 / rtol 1e-5 of the reference's
+NumPy formula np.dot(x_hat, W.T) * scale evaluated on the same quantised inputs.
+"""
+import numpy as np
+import pytest
+
+from oracle import rotor_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 3e-4, 1e-5
+
+# (M, N, K): the BASELINE shapes at decode plus ragged edge cases
+LINEAR_CASES = [
+    (1, 2560, 2560),   # cfg 0
+    (1, 6912, 2560),   # metric shape (gate/up)
+    (1, 2560, 6912),   # down
+    (1, 640, 2560),    # k/v
+    (2, 6912, 2560),
+    (3, 2560, 2560),
+    (4, 640, 2560),
+    (5, 2560, 6912),
+    (8, 6912, 2560),
+    (13, 2560, 2560),
+    (64, 640, 2560),   # cfg 2 M
+    (1, 1, 1),
+    (1, 7, 5),
+    (3, 77, 130),
+    (9, 65, 63),
+    (2, 129, 1000),
+]
+
+
+def _case(seed, M, N, K):
+    return O.make_linear_case(seed, M, N, K)
+
+
+@pytest.mark.parametrize("M,K", [(1, 2560), (64, 2560), (2048, 2560 // 8), (3, 6912), (5, 17), (1, 1), (70, 100)])
+def test_quantize_rows_bit_exact(hip, M, K):
+    import torch
+
+    rng = np.random.default_rng(M * 1000 + K)
+    x = rng.standard_normal((M, K), dtype=np.float32) * rng.uniform(0.001, 50, size=(M, 1)).astype(np.float32)
+    if M > 2:
+        x[1] = 0.0  # all-zero row -> s = 1, q = 0
+    q, s = hip.quantize_rows(torch.from_numpy(x))
+    qo, so = O.quant_rows(x)
+    assert np.array_equal(s.cpu().numpy(), so)
+    assert np.array_equal(q.cpu().numpy(), qo)
+
+
+def test_quantize_kat(hip):
+    import json
+    from pathlib import Path
+
+    import torch
+
+    k = json.loads((Path(__file__).parent / "golden" / "kats.json").read_text())["quant"]
+    q, s = hip.quantize_rows(torch.tensor([k["x"]], dtype=torch.float32))
+    assert q.cpu().numpy()[0].tolist() == k["q"] and float(s.cpu()[0]) == k["s"]
+
+
+@pytest.mark.parametrize("M,N,K", LINEAR_CASES)
+def test_linear_i32_bit_exact(hip, M, N, K):
+    import torch
+
+    rng = np.random.default_rng(M + 7 * N + 13 * K)
+    W = rng.choice(np.array([-1, 0, 1], np.int8), size=(N, K), p=[0.3, 0.4, 0.3])
+    q = rng.integers(-128, 128, size=(M, K), dtype=np.int8)  # full int8 range incl. -128
+    w = hip.upload(O.pack_rotor(W), K, 1.0)
+    acc = hip.linear_i32(w, torch.from_numpy(q)).cpu().numpy()
+    assert np.array_equal(acc.astype(np.int64), O.linear_i64_fast(q, W))
+
+
+@pytest.mark.parametrize("M,N,K", LINEAR_CASES)
+def test_linear_f32_parity(hip, M, N, K):
+    import torch
+
+    x, W, scale = _case(M * 31 + N + K, M, N, K)
+    w = hip.upload(O.pack_rotor(W), K, scale)
+    y = hip.linear_device(w, torch.from_numpy(x)).cpu().numpy()
+    y_ref, q, s, acc = O.ternary_linear(x, W, scale)
+    np.testing.assert_allclose(y, y_ref, atol=ATOL, rtol=RTOL)
+    # the fp32 epilogue is exactly ((float)acc * s_x) * s_w
+    y_exact = (acc.astype(np.float32) * s[:, None]) * np.float32(scale)
+    assert np.array_equal(y, y_exact)
+
+
+def test_extreme_accumulators(hip):
+    import torch
+
+    K = 6912
+    W = np.stack([np.ones(K, np.int8), -np.ones(K, np.int8), np.zeros(K, np.int8)])
+    q = np.full((2, K), -128, np.int8)
+    q[1] = 127
+    w = hip.upload(O.pack_rotor(W), K, 1.0)
+    acc = hip.linear_i32(w, torch.from_numpy(q)).cpu().numpy()
+    assert acc.tolist() == [[-128 * K, 128 * K, 0], [127 * K, -127 * K, 0]]
+
+
+def test_error_codes_in_weights_decode_to_zero(hip):
+    import torch
+
+    rng = np.random.default_rng(9)
+    raw = rng.integers(0, 256, size=(70, 40), dtype=np.uint8)  # includes reserved 11 codes
+    K = 160
+    W = O.unpack_rotor(raw, K)
+    q = rng.integers(-128, 128, size=(3, K), dtype=np.int8)
+    w = hip.upload(raw, K, 1.0)
+    acc = hip.linear_i32(w, torch.from_numpy(q)).cpu().numpy()
+    assert np.array_equal(acc.astype(np.int64), O.linear_i64(q, W))
+
+
+@pytest.mark.parametrize("N,K", [(2560, 2560), (77, 130), (1, 5), (640, 2560)])
+def test_upload_download_roundtrip(hip, N, K):
+    rng = np.random.default_rng(N + K)
+    W = rng.choice(np.array([-1, 0, 1], np.int8), size=(N, K))
+    p = O.pack_rotor(W)
+    w = hip.upload(p, K, 0.5)
+    assert np.array_equal(w.download(), p)
+    # the same from device bytes
+    w2 = hip.upload_device(p, K, 0.5)
+    assert np.array_equal(w2.download(), p)
+
+
+def test_ternary_matmul_duck_type(hip):
+    x, W, _ = _case(3, 1, 300, 256)
+    scales = np.random.default_rng(4).uniform(0.01, 0.05, 300).astype(np.float32)
+    packed = hip.pack_ternary_weights(W)
+    y = hip.ternary_matmul(packed, scales, x[0], 256, 300)
+    q, s = O.quant_rows(x)
+    y_ref = (O.linear_i64(q, W)[0].astype(np.float32) * s[0]) * scales
+    np.testing.assert_allclose(y, y_ref, atol=ATOL, rtol=RTOL)
+    assert y.shape == (300,)
+
+
+def test_plan_matches_single_calls(hip):
+    import torch
+
+    rng = np.random.default_rng(12)
+    M = 1
+    x1 = torch.from_numpy(rng.standard_normal((M, 2560), dtype=np.float32)).cuda()
+    x2 = torch.from_numpy(rng.standard_normal((M, 6912), dtype=np.float32)).cuda()
+    shapes = [(2560, 2560, x1), (640, 2560, x1), (640, 2560, x1), (2560, 6912, x2)]
+    ws, xs, ys = [], [], []
+    for i, (N, K, x) in enumerate(shapes):
+        W, scale = O.make_ternary(rng, N, K)
+        ws.append(hip.upload(O.pack_rotor(W), K, scale))
+        xs.append(x)
+        ys.append(torch.empty((M, N), dtype=torch.float32, device="cuda"))
+    plan = hip.plan(ws, xs, ys)
+    for _ in range(2):  # replays give the same answer
+        plan.run()
+        torch.cuda.synchronize()
+        for w, x, y in zip(ws, xs, ys):
+            assert torch.equal(y, hip.linear_device(w, x))
+
+
+def test_ternary_linear_layer_gpu(hip):
+    from rotor import gpu_layers
+    from rotor.transformer import TernaryLinear
+
+    x, W, scale = _case(21, 6, 640, 2560)
+    gpu_layers._gpu_instance = hip  # share the session backend
+    try:
+        layer = TernaryLinear(2560, 640, use_gpu=True)
+        layer.load_from_bitnet(O.pack_rotor(W), scale)
+        y = layer.forward(x.reshape(2, 3, 2560))
+        assert isinstance(y, np.ndarray) and y.shape == (2, 3, 640)
+        y_ref = O.ternary_linear(x, W, scale)[0]
+        np.testing.assert_allclose(y.reshape(6, 640), y_ref, atol=ATOL, rtol=RTOL)
+        assert np.abs(y.reshape(6, 640) - O.linear_ref_f32(x, W, scale)).max() < 0.05
+    finally:
+        gpu_layers._gpu_instance = None

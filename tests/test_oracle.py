@@ -1,0 +1,273 @@
+"""Pins the CPU oracle (oracle/rotor_oracle.py, oracle/rotor_oracle.c) before it is
+trusted as the checker of the HIP path:
+  * the reference's known-answer vectors (tests/golden/kats.json, with citations);
+  * vectors produced by the reference's own C core (tests/golden/ref_core_vectors.npz,
+    written by tests/golden/make_golden.py from native/c/rotor_core.c);
+  * closed forms and invariants that a dropped term, a wrong sign or index, or a
+    transposed operand would break;
+  * the C restatement against the NumPy one.
+"""
+import ctypes
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import rotor_oracle as O
+
+ROOT = Path(__file__).resolve().parents[1]
+GOLD = ROOT / "tests" / "golden"
+KATS = json.loads((GOLD / "kats.json").read_text())
+REF = np.load(GOLD / "ref_core_vectors.npz", allow_pickle=False)
+
+
+# ---------------------------------------------------------------- format KATs
+
+
+def test_encode_kat():
+    k = KATS["encode"]
+    b0, b1 = O.encode(k["values"])
+    assert b0.tolist() == k["bit0"] and b1.tolist() == k["bit1"]
+    assert O.decode(b0, b1).tolist() == k["values"]
+
+
+def test_pack_kat_and_roundtrip():
+    k = KATS["pack"]
+    b0, b1 = O.encode(k["values"])
+    packed = O.pack(b0, b1)
+    assert packed.tolist() == k["packed"]
+    u0, u1 = O.unpack(packed, 8)
+    assert O.decode(u0, u1).tolist() == k["values"]
+    assert O.pack_rotor(np.array([k["values"]])).tolist() == [k["packed"]]
+
+
+@pytest.mark.parametrize("case", KATS["bytes"], ids=lambda c: hex(c["byte"]))
+def test_byte_kats(case):
+    w = O.unpack_rotor(np.array([[case["byte"]]], np.uint8), 4)
+    assert w[0].tolist() == case["weights"]
+    b0, b1 = O.bitnet_to_rotor(np.array([[case["byte"]]], np.uint8))
+    if "bit0" in case:
+        assert int(b0[0, 0]) == case["bit0"] and int(b1[0, 0]) == case["bit1"]
+    assert O.rotor_unpack_weights(b0, b1, 1, 4)[0].tolist() == case["weights"]
+
+
+def test_error_code_decodes_to_zero_and_is_flagged():
+    # code 11 is reserved: value bit0 - bit1 = 0 (src/rotor/core.py:233-243; C treats it as 0)
+    assert O.unpack_rotor(np.array([[0xFF]], np.uint8), 4)[0].tolist() == [0, 0, 0, 0]
+    assert O.check_errors(np.array([1, 0, 1]), np.array([1, 1, 0])).tolist() == [True, False, False]
+
+
+# ---------------------------------------------------------------- vs the reference C core
+
+
+@pytest.mark.parametrize("name", ["all_bytes", "ragged", "square"])
+def test_conversion_matches_reference_core(name):
+    src, cols = REF[f"{name}_src"], int(REF[f"{name}_cols"])
+    b0, b1 = O.bitnet_to_rotor(src, cols)
+    assert np.array_equal(b0, REF[f"{name}_bit0"]) and np.array_equal(b1, REF[f"{name}_bit1"])
+    assert np.array_equal(O.rotor_unpack_weights(b0, b1, src.shape[0], cols), REF[f"{name}_w"])
+    # the 4/byte rotor code read directly gives the same weights
+    assert np.array_equal(O.unpack_rotor(src, cols), REF[f"{name}_w"])
+
+
+def test_pack_unpack_match_reference_core():
+    v = REF["enc_values"]
+    b0, b1 = O.encode(v)
+    assert np.array_equal(b0, REF["enc_bit0"]) and np.array_equal(b1, REF["enc_bit1"])
+    assert np.array_equal(O.pack(b0, b1), REF["enc_packed"])
+    u0, u1 = O.unpack(REF["enc_packed"], len(v))
+    assert np.array_equal(u0, REF["unp_bit0"]) and np.array_equal(u1, REF["unp_bit1"])
+
+
+def test_exhaustive_byte_table():
+    # every byte value, independent statement: field f -> {0:0, 1:-1, 2:+1, 3:0}
+    table = {0: 0, 1: -1, 2: 1, 3: 0}
+    allb = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    w = O.unpack_rotor(allb, 1024).reshape(256, 4)
+    for b in range(256):
+        assert w[b].tolist() == [table[(b >> (2 * j)) & 3] for j in range(4)]
+    # pack_rotor inverts unpack_rotor on valid codes
+    W = np.random.default_rng(0).choice([-1, 0, 1], size=(7, 33)).astype(np.int8)
+    assert np.array_equal(O.unpack_rotor(O.pack_rotor(W), 33), W)
+
+
+def test_live_reference_core_if_built():
+    lib_path = ROOT / "oracle" / "_ref" / "librotor_core.so"
+    if not lib_path.exists():
+        pytest.skip("oracle/_ref not built")
+    lib = ctypes.CDLL(str(lib_path))
+    sz = ctypes.c_size_t
+    lib.bitnet_to_rotor.argtypes = [ctypes.c_void_p, sz, sz, ctypes.c_void_p, ctypes.c_void_p]
+    lib.bitnet_to_rotor.restype = None
+    rng = np.random.default_rng(5)
+    for rows, cols in [(1, 1), (3, 7), (11, 129), (65, 640)]:
+        src = rng.integers(0, 256, size=(rows, (cols + 3) // 4), dtype=np.uint8)
+        ob = (cols + 7) // 8
+        b0 = np.zeros((rows, ob), np.uint8)
+        b1 = np.zeros((rows, ob), np.uint8)
+        lib.bitnet_to_rotor(src.ctypes.data, rows, cols, b0.ctypes.data, b1.ctypes.data)
+        o0, o1 = O.bitnet_to_rotor(src, cols)
+        assert np.array_equal(b0, o0) and np.array_equal(b1, o1)
+
+
+# ---------------------------------------------------------------- quantiser
+
+
+def test_quant_kat():
+    k = KATS["quant"]
+    q, s = O.quant_rows(np.array([k["x"]], np.float32))
+    assert q[0].tolist() == k["q"] and float(s[0]) == k["s"]
+
+
+def test_quant_zero_row_and_sign():
+    q, s = O.quant_rows(np.zeros((2, 5), np.float32))
+    assert (q == 0).all() and (s == 1.0).all()
+    q, s = O.quant_rows(np.array([[-3.0, 1.5, 0.0]], np.float32))
+    assert q[0].tolist() == [-127, 64, 0]  # 1.5/(3/127) = 63.5 -> 64 (half to even)
+
+
+def test_quant_invariants():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((40, 333), dtype=np.float32) * rng.uniform(0.01, 100, size=(40, 1)).astype(np.float32)
+    q, s = O.quant_rows(x)
+    assert q.dtype == np.int8 and s.dtype == np.float32
+    # the largest |x| of each row maps to +-127 with the sign of x
+    i = np.argmax(np.abs(x), axis=1)
+    assert np.array_equal(q[np.arange(40), i], (127 * np.sign(x[np.arange(40), i])).astype(np.int8))
+    assert np.abs(q.astype(int)).max() <= 127
+    # reconstruction error at most half a step (plus fp32 rounding)
+    err = np.abs(x - q.astype(np.float32) * s[:, None])
+    assert (err <= 0.5 * s[:, None] * (1 + 1e-5)).all()
+    # s = amax/127 in float32
+    assert np.array_equal(s, (np.abs(x).max(axis=1) / np.float32(127)).astype(np.float32))
+    # per-row independence: quantising one row alone gives the same row
+    q1, s1 = O.quant_rows(x[7:8])
+    assert np.array_equal(q1[0], q[7]) and s1[0] == s[7]
+
+
+def test_quant_against_float64_rounding():
+    # q = round(x/s) computed in float64 agrees except where x/s sits within fp32
+    # rounding of a .5 tie -- none occur for these inputs
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((8, 1000), dtype=np.float32)
+    q, s = O.quant_rows(x)
+    r64 = x.astype(np.float64) / s.astype(np.float64)[:, None]
+    near_tie = np.abs(np.abs(r64 - np.floor(r64)) - 0.5) < 1e-4
+    assert np.array_equal(q[~near_tie], np.clip(np.round(r64), -128, 127).astype(np.int8)[~near_tie])
+
+
+# ---------------------------------------------------------------- linear
+
+
+def test_linear_i64_brute_force():
+    rng = np.random.default_rng(3)
+    q = rng.integers(-128, 128, size=(3, 9)).astype(np.int8)
+    W = rng.choice([-1, 0, 1], size=(4, 9)).astype(np.int8)
+    acc = O.linear_i64(q, W)
+    for m in range(3):
+        for n in range(4):
+            assert acc[m, n] == sum(int(q[m, k]) * int(W[n, k]) for k in range(9))
+    # not transposed: shape [M, N]
+    assert acc.shape == (3, 4)
+
+
+def test_linear_i64_fast_and_linearity():
+    rng = np.random.default_rng(4)
+    q1 = rng.integers(-128, 128, size=(5, 700)).astype(np.int8)
+    q2 = rng.integers(-64, 64, size=(5, 700)).astype(np.int8)
+    W = rng.choice([-1, 0, 1], size=(31, 700)).astype(np.int8)
+    a1 = O.linear_i64(q1, W)
+    assert np.array_equal(a1, O.linear_i64_fast(q1, W))
+    # linearity in q
+    assert np.array_equal(O.linear_i64(q1.astype(np.int64) + q2, W), a1 + O.linear_i64(q2, W))
+    # extreme magnitudes: all -128 against all +1 / -1
+    K = 6912
+    qmin = np.full((1, K), -128, np.int8)
+    Wpm = np.stack([np.ones(K, np.int8), -np.ones(K, np.int8)])
+    assert O.linear_i64_fast(qmin, Wpm).tolist() == [[-128 * K, 128 * K]]
+
+
+def test_ternary_linear_closed_form():
+    # y = (q*s) . W * scale evaluated in float64 on the same quantised inputs
+    x, W, scale = O.make_linear_case(11, 3, 50, 256)
+    y, q, s, acc = O.ternary_linear(x, W, scale)
+    y64 = (acc.astype(np.float64) * s.astype(np.float64)[:, None]) * np.float64(scale)
+    assert np.abs(y - y64).max() < 1e-5
+    assert np.array_equal(acc, O.linear_i64(q, W))
+    # the reference formula on unquantised x stays within the quantisation error
+    yr = O.linear_ref_f32(x, W, scale)
+    assert np.abs(yr - y).max() < 0.05
+
+
+def test_linear_ref_reshape_rules():
+    # 3-D inputs flatten to [B*S, K] and come back as [B, S, N] (src/rotor/transformer.py:121-155)
+    x = np.random.default_rng(6).standard_normal((2, 3, 16), dtype=np.float32)
+    W = np.eye(4, 16, dtype=np.int8)
+    y = O.linear_ref_f32(x, W, 2.0)
+    assert y.shape == (2, 3, 4)
+    assert np.allclose(y, 2.0 * x[..., :4])
+
+
+def test_rms_norm_and_relu2_closed_forms():
+    x = np.full((2, 8), 3.0, np.float32)
+    assert np.allclose(O.rms_norm(x, np.ones(8), eps=0.0), 1.0)
+    w = np.arange(8, dtype=np.float32)
+    assert np.allclose(O.rms_norm(-x, w, eps=0.0), -w)
+    g = np.array([-2.0, 0.0, 3.0], np.float32)
+    u = np.array([5.0, 5.0, -2.0], np.float32)
+    assert O.relu2_gate(g, u).tolist() == [0.0, 0.0, -18.0]
+
+
+# ---------------------------------------------------------------- C restatement
+
+
+@pytest.fixture(scope="module")
+def corc():
+    p = ROOT / "oracle" / "liboracle.so"
+    if not p.exists():
+        pytest.skip("oracle/liboracle.so not built (make -C oracle)")
+    lib = ctypes.CDLL(str(p))
+    v, sz = ctypes.c_void_p, ctypes.c_size_t
+    lib.orc_pack_rotor.argtypes = [v, sz, sz, v]
+    lib.orc_unpack_rotor.argtypes = [v, sz, sz, v]
+    lib.orc_bitnet_to_rotor.argtypes = [v, sz, sz, v, v]
+    lib.orc_unpack_planes.argtypes = [v, v, sz, sz, v]
+    lib.orc_quant_rows.argtypes = [v, sz, sz, v, v]
+    lib.orc_linear_i64.argtypes = [v, v, sz, sz, sz, v]
+    lib.orc_linear_i64_packed.argtypes = [v, v, sz, sz, sz, v]
+    return lib
+
+
+def test_c_oracle_matches_numpy_oracle(corc):
+    rng = np.random.default_rng(7)
+    N, K, M = 45, 203, 6
+    W = rng.choice([-1, 0, 1], size=(N, K)).astype(np.int8)
+    kb = (K + 3) // 4
+    p = np.zeros((N, kb), np.uint8)
+    corc.orc_pack_rotor(W.ctypes.data, N, K, p.ctypes.data)
+    assert np.array_equal(p, O.pack_rotor(W))
+    W2 = np.zeros((N, K), np.int8)
+    corc.orc_unpack_rotor(p.ctypes.data, N, K, W2.ctypes.data)
+    assert np.array_equal(W2, W)
+    b0 = np.zeros((N, (K + 7) // 8), np.uint8)
+    b1 = np.zeros_like(b0)
+    corc.orc_bitnet_to_rotor(p.ctypes.data, N, K, b0.ctypes.data, b1.ctypes.data)
+    o0, o1 = O.bitnet_to_rotor(p, K)
+    assert np.array_equal(b0, o0) and np.array_equal(b1, o1)
+    W3 = np.zeros((N, K), np.int8)
+    corc.orc_unpack_planes(b0.ctypes.data, b1.ctypes.data, N, K, W3.ctypes.data)
+    assert np.array_equal(W3, W)
+    x = rng.standard_normal((M, K), dtype=np.float32) * 3
+    x[2] = 0
+    q = np.zeros((M, K), np.int8)
+    s = np.zeros(M, np.float32)
+    corc.orc_quant_rows(x.ctypes.data, M, K, q.ctypes.data, s.ctypes.data)
+    qo, so = O.quant_rows(x)
+    assert np.array_equal(q, qo) and np.array_equal(s, so)
+    acc = np.zeros((M, N), np.int64)
+    corc.orc_linear_i64(q.ctypes.data, W.ctypes.data, M, N, K, acc.ctypes.data)
+    assert np.array_equal(acc, O.linear_i64(q, W))
+    acc2 = np.zeros((M, N), np.int64)
+    corc.orc_linear_i64_packed(q.ctypes.data, p.ctypes.data, M, N, K, acc2.ctypes.data)
+    assert np.array_equal(acc2, acc)

@@ -39,6 +39,21 @@ N_OUT, K_IN = 6912, 2560
 METRIC = "Ternary GEMV HBM GB/s (% peak) @2560x6912; BitNet-2B-shape decode tok/s"
 
 
+PROFILE = ROOT / "profiles" / "gemv_2560x6912_m1_g128.md"
+
+
+def profiled_traffic():
+    """HBM bytes per GEMV launch measured by the committed rocprofv3 PMC passes
+    (FETCH_SIZE/WRITE_SIZE scaled by a plain-copy calibration), or None."""
+    try:
+        for line in PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def gemv_bytes(M, N, K):
     return N * K // 4 + M * K + 4 * M + 4 * M * N + 4
 
@@ -104,6 +119,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--groups", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
+                    help="run one plain device copy of MIB MiB first (reference point for HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build's hot path runs on a single MI355X "
@@ -130,6 +147,14 @@ def main():
         ys.append(torch.empty((1, N_OUT), device=dev, dtype=torch.float32))
     plan = hip.plan(ws, xs, ys)
     torch.cuda.synchronize()
+    if args.copy_calib:
+        # an elementwise kernel that reads and writes exactly MIB MiB each
+        src = torch.ones((args.copy_calib << 20) // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     print(f"bench: {G} x ternary GEMV {K_IN}->{N_OUT}, M=1; warmup {args.warmup}, steps {args.steps}",
           file=sys.stderr, flush=True)
 
@@ -208,8 +233,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "rt::gemv_kernel<1>",
+            "traffic": profiled_traffic() if G == 128 else None,
+            "traffic_source": "profiles/gemv_2560x6912_m1_g128.md (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
+            "kernel": "rt::gemv_rows_kernel<1>",
             "bytes_per_launch": bytes_step,
             "avg_launch_ms": round(gemv_avg, 5),
         },

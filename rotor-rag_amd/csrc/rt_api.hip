@@ -92,8 +92,10 @@ struct rt_weights {
 
 struct rt_plan {
     int device = 0;
-    int G = 0, M = 0, Mpad = 0, mt = 1, nw = 1, total_wgs = 0, U = 0;
+    int G = 0, M = 0, Mpad = 0, mt = 1, total_rb = 0, U = 0;
+    GemvShape shape{};
     GemvProb* dev_probs = nullptr;   // [G]
+    int* dev_rb2p = nullptr;         // [total_rb]
     QuantProb* dev_quant = nullptr;  // [U]
     void* act = nullptr;             // quantised activations of the U distinct inputs
     std::vector<GemvProb> probs;
@@ -168,8 +170,10 @@ static int weights_alloc(rt_ctx* ctx, int N, int K, float scale, rt_weights** ou
     w->Np = round_up(N, kRowBlock);
     w->scale = scale;
     w->bytes = (size_t)w->Np * w->Kp / 4;
-    hipError_t e = hipMalloc(&w->tiles, w->bytes);
+    hipError_t e = hipMalloc(&w->tiles, w->bytes + kTileSlack);
+    if (e == hipSuccess) e = hipMemsetAsync(reinterpret_cast<char*>(w->tiles) + w->bytes, 0, kTileSlack, ctx->stream);
     if (e != hipSuccess) {
+        if (w->tiles) (void)hipFree(w->tiles);
         delete w;
         return fail(RT_ENOMEM, std::string("rt_weights_upload: hipMalloc failed: ") + hipGetErrorName(e));
     }
@@ -264,7 +268,7 @@ static int stage_activations(rt_ctx* ctx, const float* x, const int8_t* q_in, in
     a.U = 1;
     a.M = M;
     a.Mpad = Mpad;
-    a.p[0] = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp};
+    a.p = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp};
     RT_HIP(launch_quant(a, ctx->stream));
     if (s_out) RT_HIP(hipMemcpyAsync(s_out, *sx, (size_t)M * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
     return RT_OK;
@@ -277,7 +281,7 @@ int rt_quantize_rows(rt_ctx* ctx, const float* x, int M, int K, int8_t* q, float
     DeviceGuard g(ctx->device);
     int8_t* qx;
     float* sx;
-    return stage_activations(ctx, x, nullptr, M, K, round_up(M, kTokPad), q, s, &qx, &sx);
+    return stage_activations(ctx, x, nullptr, M, K, M, q, s, &qx, &sx);
 }
 
 static int run_linear(rt_ctx* ctx, const rt_weights* w, const float* x, const int8_t* q, int M,
@@ -291,17 +295,18 @@ static int run_linear(rt_ctx* ctx, const rt_weights* w, const float* x, const in
     const int mt = gemv_mt(M);
     int8_t* qx;
     float* sx;
-    rc = stage_activations(ctx, x, q, M, w->K, round_up(M, kTokPad), nullptr, nullptr, &qx, &sx);
+    rc = stage_activations(ctx, x, q, M, w->K, round_up(M, mt), nullptr, nullptr, &qx, &sx);
     if (rc) return rc;
     GemvArgs a{};
     a.dev = nullptr;
+    a.rb2p = nullptr;
     a.G = 1;
     a.M = M;
     a.out_i32 = out_i32 ? 1 : 0;
-    a.p[0] = GemvProb{w->tiles, qx, sx, row_scale, out, w->scale, w->N, w->C, w->N, 0};
-    const int wgs = w->Np / kRowBlock;
-    const int nw = gemv_waves(wgs * ((M + mt - 1) / mt), w->C);
-    RT_HIP(launch_gemv(a, wgs, mt, nw, ctx->stream));
+    a.total_rb = w->Np / kRowBlock;
+    a.p = GemvProb{w->tiles, qx, sx, row_scale, out, w->scale, w->N, w->C, w->N, 0};
+    const GemvShape shape = gemv_shape(a.total_rb, (M + mt - 1) / mt, w->C);
+    RT_HIP(launch_gemv(a, mt, shape, ctx->stream));
     return RT_OK;
 }
 
@@ -327,6 +332,7 @@ int rt_plan_free(rt_plan* plan) {
     if (!plan) return RT_OK;
     DeviceGuard g(plan->device);
     if (plan->dev_probs) (void)hipFree(plan->dev_probs);
+    if (plan->dev_rb2p) (void)hipFree(plan->dev_rb2p);
     if (plan->dev_quant) (void)hipFree(plan->dev_quant);
     if (plan->act) (void)hipFree(plan->act);
     delete plan;
@@ -348,8 +354,8 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
     p->device = ctx->device;
     p->G = G;
     p->M = M;
-    p->Mpad = round_up(M, kTokPad);
     p->mt = gemv_mt(M);
+    p->Mpad = round_up(M, p->mt);
     // distinct inputs (same pointer => same quantisation; their K must agree)
     std::unordered_map<const float*, int> uid;
     std::vector<int> which(G);
@@ -402,9 +408,14 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
         wg += w[g]->Np / kRowBlock;
         if (w[g]->C < minC) minC = w[g]->C;
     }
-    p->total_wgs = wg;
-    p->nw = gemv_waves(wg * ((M + p->mt - 1) / p->mt), minC);
+    p->total_rb = wg;
+    p->shape = gemv_shape(wg, (M + p->mt - 1) / p->mt, minC);
+    std::vector<int> rb2p(wg);
+    for (int g = 0; g < G; ++g)
+        for (int r = 0; r < w[g]->Np / kRowBlock; ++r) rb2p[p->probs[g].wg_begin + r] = g;
     e = hipMalloc(&p->dev_probs, sizeof(GemvProb) * G);
+    if (e == hipSuccess) e = hipMalloc(&p->dev_rb2p, sizeof(int) * wg);
+    if (e == hipSuccess) e = hipMemcpy(p->dev_rb2p, rb2p.data(), sizeof(int) * wg, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMalloc(&p->dev_quant, sizeof(QuantProb) * p->U);
     if (e == hipSuccess)
         e = hipMemcpy(p->dev_probs, p->probs.data(), sizeof(GemvProb) * G, hipMemcpyHostToDevice);
@@ -442,10 +453,12 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
     DeviceGuard g(ctx->device);
     GemvArgs a{};
     a.dev = plan->dev_probs;
+    a.rb2p = plan->dev_rb2p;
     a.G = plan->G;
     a.M = plan->M;
     a.out_i32 = 0;
-    RT_HIP(launch_gemv(a, plan->total_wgs, plan->mt, plan->nw, ctx->stream));
+    a.total_rb = plan->total_rb;
+    RT_HIP(launch_gemv(a, plan->mt, plan->shape, ctx->stream));
     return RT_OK;
 }
 

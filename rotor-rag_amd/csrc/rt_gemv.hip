@@ -4,13 +4,17 @@
 // and its CPU twin np.dot(x, W_i8.T) * scale (src/rotor/transformer.py:150).
 //
 // Mapping (lane-per-row, wave-per-row-tile):
-//   * a workgroup owns one 64-row block of one problem and `nw` waves split its
-//     K chunks; lane r of every wave accumulates row 64*rb + r, so no cross-lane
-//     reduction is needed, only a cross-wave one through LDS when nw > 1;
-//   * each chunk step is one coalesced 16-byte-per-lane (1 KiB per wave)
-//     non-temporal load of rotor bytes;
+//   * a wave owns one 64-row block of one problem; lane r accumulates row 64*rb + r,
+//     so no cross-lane reduction is needed;
+//   * each chunk step is one coalesced 16-byte-per-lane (1 KiB per wave) non-temporal
+//     buffer load of rotor bytes; loads run one batch of U chunks ahead of the math;
 //   * the activations of a chunk are the same for all 64 lanes, so they are read
 //     with scalar loads into SGPRs and fed to v_dot4_i32_i8 as the scalar operand.
+// Two launch shapes share the body:
+//   * ROWS   (many row blocks, e.g. plans): a workgroup of nw waves covers nw
+//     consecutive row blocks, each wave the whole K range;
+//   * KSPLIT (few row blocks, e.g. one 6912x2560 GEMV): a workgroup is one row block
+//     and its nw waves split the K chunks, combined through LDS.
 //
 // Decoding the rotor code (value = bit0 - bit1, field f = 2*bit0 + bit1) costs
 // 9 VALU ops per 16 weights: for a weight dword u
@@ -29,26 +33,17 @@ namespace rt {
 
 constexpr unsigned kLutLo = 0x0001FF00u;  // src1 of v_perm_b32
 constexpr unsigned kLutHi = 0x00000001u;  // src0 of v_perm_b32
+constexpr int kBufDword3 = 0x00020000;    // buffer resource word 3 for gfx9 raw buffers
+constexpr int kAuxNT = 2;                 // cache policy: non-temporal (streamed once)
 
-// Address-space views: weights are global memory; the activations are read-only for
-// the whole launch, so the constant address space lets uniform reads become s_load.
-typedef __attribute__((address_space(1))) const v4u gv4u;
+// The activations are read-only for the whole launch, so the constant address space
+// lets uniform reads become s_load.
 typedef __attribute__((address_space(4))) const int cint;
 
-__device__ __forceinline__ GemvProb select_prob(const GemvArgs& a, int wg) {
-    if (a.dev) {  // binary search over wg_begin (uniform, scalar loads)
-        int lo = 0, hi = a.G - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (a.dev[mid].wg_begin <= wg) lo = mid; else hi = mid - 1;
-        }
-        return a.dev[lo];
-    }
-    GemvProb p = a.p[0];
-#pragma unroll
-    for (int j = 1; j < kMaxInline; ++j)
-        if (j < a.G && a.p[j].wg_begin <= wg) p = a.p[j];
-    return p;
+// Problem of global row block rbg: two dependent scalar loads (table, descriptor).
+__device__ __forceinline__ GemvProb find_prob(const GemvArgs& a, int rbg) {
+    if (!a.dev) return a.p;
+    return a.dev[a.rb2p[rbg]];
 }
 
 template <int MT>
@@ -77,59 +72,88 @@ __device__ __forceinline__ void chunk_step(const v4u v, cint* __restrict__ xc, c
     }
 }
 
-template <int MT>
-__device__ __forceinline__ void gemv_body(gv4u* __restrict__ wp, cint* __restrict__ xq, const int ldx,
-                                          const int cb, const int ce, int (&accP)[MT], int (&accN)[MT]) {
-    constexpr int U = 4;  // chunks in flight per wave per batch
-    int c = cb;
-    for (; c + U <= ce; c += U) {
-        v4u v[U];
+// Accumulate chunks [cb, ce) of one row block.  `rsrc` starts at the row block and
+// ends at chunk ce (num_records = ce KiB).  The chunk offset goes into the VGPR offset,
+// which the buffer unit range-checks (the SGPR offset is not checked), so the loads
+// that run past the range come back as zeros without touching memory.  That keeps
+// every load unconditional -- two batches of U chunks in flight -- while the math on
+// chunks >= ce is skipped.
+template <int MT, int U>
+__device__ __forceinline__ void gemv_body(__amdgpu_buffer_rsrc_t rsrc, const int lane_off, cint* __restrict__ xq,
+                                          const int ldx, const int cb, const int ce, int (&accP)[MT],
+                                          int (&accN)[MT]) {
+    auto ld = [&](int c) {
+        return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off + c * 1024, 0, kAuxNT));
+    };
+    v4u A[U], B[U];
 #pragma unroll
-        for (int i = 0; i < U; ++i) v[i] = __builtin_nontemporal_load(wp + (size_t)(c + i) * kRowBlock);
+    for (int i = 0; i < U; ++i) A[i] = ld(cb + i);
+    for (int c = cb; c < ce; c += 2 * U) {
 #pragma unroll
-        for (int i = 0; i < U; ++i) chunk_step<MT>(v[i], xq + (c + i) * 16, ldx, accP, accN);
-    }
-    for (; c < ce; ++c) {
-        const v4u v = __builtin_nontemporal_load(wp + (size_t)c * kRowBlock);
-        chunk_step<MT>(v, xq + c * 16, ldx, accP, accN);
+        for (int i = 0; i < U; ++i) B[i] = ld(c + U + i);
+#pragma unroll
+        for (int i = 0; i < U; ++i)
+            if (c + i < ce) chunk_step<MT>(A[i], xq + (c + i) * 16, ldx, accP, accN);
+#pragma unroll
+        for (int i = 0; i < U; ++i) A[i] = ld(c + 2 * U + i);
+#pragma unroll
+        for (int i = 0; i < U; ++i)
+            if (c + U + i < ce) chunk_step<MT>(B[i], xq + (c + U + i) * 16, ldx, accP, accN);
     }
 }
 
 template <int MT>
-__global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
-    extern __shared__ int red[];  // [nw][MT][64] when nw > 1
-    const GemvProb P = select_prob(a, blockIdx.x);
-    const int rb = blockIdx.x - P.wg_begin;
-    const int m0 = blockIdx.y * MT;
+__device__ __forceinline__ void emit(const GemvArgs& a, const GemvProb& P, int rb, int m0, int m, int r, int acc) {
+    const int n = rb * kRowBlock + r, mg = m0 + m;
+    if (n >= P.N || mg >= a.M) return;
+    if (a.out_i32) {
+        static_cast<int*>(P.out)[(size_t)mg * P.ldo + n] = acc;
+    } else {
+        const float sw = P.rs ? P.rs[n] : P.s_w;
+        static_cast<float*>(P.out)[(size_t)mg * P.ldo + n] = ((float)acc * P.sx[mg]) * sw;
+    }
+}
+
+template <int MT>
+__global__ void __launch_bounds__(1024) gemv_rows_kernel(GemvArgs a) {
+    constexpr int U = MT == 1 ? 4 : 2;
     const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
-    const int C = P.C;
-    const int cb = (wave * C) / nw, ce = ((wave + 1) * C) / nw;
-    const int ldx = C * 16;  // dwords per qx row
-    gv4u* wp = (gv4u*)(P.w + (size_t)rb * C * kRowBlock) + lane;
+    const int rbg = blockIdx.x * nw + wave;                               // global row block
+    if (rbg >= a.total_rb) return;
+    const GemvProb P = find_prob(a, rbg);
+    const int rb = rbg - P.wg_begin;
+    const int m0 = blockIdx.y * MT;
+    const int C = P.C, ldx = C * 16;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, C * 1024, kBufDword3);
     cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
-
     int accP[MT], accN[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
-    gemv_body<MT>(wp, xq, ldx, cb, ce, accP, accN);
-
-    const int M = a.M;
-    auto emit = [&](int m, int r, int acc) {
-        const int n = rb * kRowBlock + r, mg = m0 + m;
-        if (n >= P.N || mg >= M) return;
-        if (a.out_i32) {
-            static_cast<int*>(P.out)[(size_t)mg * P.ldo + n] = acc;
-        } else {
-            const float sw = P.rs ? P.rs[n] : P.s_w;
-            static_cast<float*>(P.out)[(size_t)mg * P.ldo + n] = ((float)acc * P.sx[mg]) * sw;
-        }
-    };
-    if (nw == 1) {
+    gemv_body<MT, U>(rsrc, lane * 16, xq, ldx, 0, C, accP, accN);
 #pragma unroll
-        for (int m = 0; m < MT; ++m) emit(m, lane, accP[m] - accN[m]);
-        return;
-    }
+    for (int m = 0; m < MT; ++m) emit<MT>(a, P, rb, m0, m, lane, accP[m] - accN[m]);
+}
+
+template <int MT>
+__global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
+    constexpr int U = MT == 1 ? 4 : 2;
+    extern __shared__ int red[];  // [nw][MT][64]
+    const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const GemvProb P = find_prob(a, blockIdx.x);
+    const int rb = blockIdx.x - P.wg_begin;
+    const int m0 = blockIdx.y * MT;
+    const int C = P.C, ldx = C * 16;
+    const int cb = (wave * C) / nw, ce = ((wave + 1) * C) / nw;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, ce * 1024, kBufDword3);
+    cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
+    int accP[MT], accN[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
+    gemv_body<MT, U>(rsrc, lane * 16, xq, ldx, cb, ce, accP, accN);
 #pragma unroll
     for (int m = 0; m < MT; ++m) red[(wave * MT + m) * kRowBlock + lane] = accP[m] - accN[m];
     __syncthreads();
@@ -137,30 +161,50 @@ __global__ void __launch_bounds__(1024) gemv_kernel(GemvArgs a) {
         const int m = idx / kRowBlock, r = idx % kRowBlock;
         int s = 0;
         for (int w = 0; w < nw; ++w) s += red[(w * MT + m) * kRowBlock + r];
-        emit(m, r, s);
+        emit<MT>(a, P, rb, m0, m, r, s);
     }
 }
 
-int gemv_waves(int total_wgs, int C) {
-    // Aim for ~8 waves per CU on 256 CUs; every wave keeps >= 2 chunks.
-    int nw = (2048 + total_wgs - 1) / total_wgs;
+GemvShape gemv_shape(int total_rb, int m_blocks, int min_C) {
+    // Enough waves to fill 256 CUs x 8 waves; split K only when rows alone cannot.
+    const long long waves_rows = (long long)total_rb * m_blocks;
+    GemvShape s;
+    if (waves_rows >= 1024 || min_C < 4) {
+        s.ksplit = false;
+        s.nw = 4;
+        return s;
+    }
+    int nw = (int)((2048 + waves_rows - 1) / waves_rows);
     if (nw > 16) nw = 16;
-    if (nw > C / 2) nw = C / 2;
-    if (nw < 1) nw = 1;
-    return nw;
+    if (nw > min_C / 2) nw = min_C / 2;
+    s.ksplit = nw > 1;
+    s.nw = s.ksplit ? nw : 4;
+    return s;
 }
 
-hipError_t launch_gemv(const GemvArgs& a, int total_wgs, int mt, int nw, hipStream_t s) {
-    if (total_wgs <= 0 || a.M <= 0) return hipSuccess;
-    const dim3 grid((unsigned)total_wgs, (unsigned)((a.M + mt - 1) / mt));
-    const dim3 block((unsigned)(64 * nw));
-    const size_t lds = nw > 1 ? (size_t)nw * mt * kRowBlock * sizeof(int) : 0;
-    switch (mt) {
-        case 1: hipLaunchKernelGGL(gemv_kernel<1>, grid, block, lds, s, a); break;
-        case 2: hipLaunchKernelGGL(gemv_kernel<2>, grid, block, lds, s, a); break;
-        case 4: hipLaunchKernelGGL(gemv_kernel<4>, grid, block, lds, s, a); break;
-        case 8: hipLaunchKernelGGL(gemv_kernel<8>, grid, block, lds, s, a); break;
-        default: return hipErrorInvalidValue;
+hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s) {
+    if (a.total_rb <= 0 || a.M <= 0) return hipSuccess;
+    const unsigned mblocks = (unsigned)((a.M + mt - 1) / mt);
+    const dim3 block((unsigned)(64 * shape.nw));
+    if (shape.ksplit) {
+        const dim3 grid((unsigned)a.total_rb, mblocks);
+        const size_t lds = (size_t)shape.nw * mt * kRowBlock * sizeof(int);
+        switch (mt) {
+            case 1: hipLaunchKernelGGL(gemv_ksplit_kernel<1>, grid, block, lds, s, a); break;
+            case 2: hipLaunchKernelGGL(gemv_ksplit_kernel<2>, grid, block, lds, s, a); break;
+            case 4: hipLaunchKernelGGL(gemv_ksplit_kernel<4>, grid, block, lds, s, a); break;
+            case 8: hipLaunchKernelGGL(gemv_ksplit_kernel<8>, grid, block, lds, s, a); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        const dim3 grid((unsigned)((a.total_rb + shape.nw - 1) / shape.nw), mblocks);
+        switch (mt) {
+            case 1: hipLaunchKernelGGL(gemv_rows_kernel<1>, grid, block, 0, s, a); break;
+            case 2: hipLaunchKernelGGL(gemv_rows_kernel<2>, grid, block, 0, s, a); break;
+            case 4: hipLaunchKernelGGL(gemv_rows_kernel<4>, grid, block, 0, s, a); break;
+            case 8: hipLaunchKernelGGL(gemv_rows_kernel<8>, grid, block, 0, s, a); break;
+            default: return hipErrorInvalidValue;
+        }
     }
     return hipGetLastError();
 }

@@ -16,7 +16,7 @@
 //    so that dword i of a group holds element i of each of the 4 weight bytes of the
 //    matching weight dword: the decoded weight dword for field position i of a weight
 //    dword pairs with activation dword i in one v_dot4_i32_i8.  Padding is 0.
-//    Rows are padded to a multiple of 8 tokens with zeros.
+//    Rows are padded with zeros to a multiple of the GEMV's tokens per workgroup.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -30,8 +30,11 @@ typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kRowBlock = 64;   // rows per weight tile (one per lane)
 constexpr int kChunk = 64;      // weights per 16-byte chunk
-constexpr int kTokPad = 8;      // qx rows are padded to a multiple of this
-constexpr int kMaxInline = 4;   // problems passed by value in kernel arguments
+// Zeroed bytes allocated after every weight tile buffer.  The GEMV issues its next
+// loads before it knows whether the range has ended; those loads are range-checked
+// by the buffer unit (and return zeros), and this slack keeps them inside the
+// allocation even so.
+constexpr size_t kTileSlack = 16384;
 
 inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 
@@ -44,13 +47,20 @@ struct GemvProb {
     void* out;           // float y[M][ldo] or int32 acc[M][ldo]
     float s_w;
     int N, C, ldo;
-    int wg_begin;        // first workgroup (blockIdx.x) of this problem
+    int wg_begin;        // first global row block of this problem (prefix sum over problems)
 };
 
 struct GemvArgs {
-    const GemvProb* dev;  // device descriptor array (plans) or nullptr -> p[]
+    const GemvProb* dev;  // device descriptor array [G] (plans) or nullptr -> p
+    const int* rb2p;      // [total_rb] problem index of every global row block (plans)
     int G, M, out_i32;
-    GemvProb p[kMaxInline];
+    int total_rb;         // row blocks over all problems
+    GemvProb p;           // the problem of a single-problem launch
+};
+
+struct GemvShape {
+    bool ksplit;  // true: one row block per workgroup, waves split K
+    int nw;       // waves per workgroup
 };
 
 // ---- one quantisation problem (x fp32 [M][K] -> qx, sx) -------------------------
@@ -64,21 +74,21 @@ struct QuantProb {
 };
 
 struct QuantArgs {
-    const QuantProb* dev;
+    const QuantProb* dev;  // device descriptor array [U] or nullptr -> p
     int U, M, Mpad;
-    QuantProb p[kMaxInline];
+    QuantProb p;
 };
 
 // Launchers (return hipSuccess or the launch error).
 hipError_t launch_relayout(const uint8_t* src, int N, int K, v4u* tiles, hipStream_t s);
 hipError_t launch_unrelayout(const v4u* tiles, int N, int K, uint8_t* dst, hipStream_t s);
 hipError_t launch_quant(const QuantArgs& a, hipStream_t s);
-// mt = tokens per workgroup (1, 2, 4 or 8), nw = waves per workgroup (K split).
-hipError_t launch_gemv(const GemvArgs& a, int total_wgs, int mt, int nw, hipStream_t s);
+// mt = tokens per workgroup (1, 2, 4 or 8).
+hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s);
 
 // Host policy: tokens per workgroup for M tokens.
 inline int gemv_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
-// Host policy: waves per workgroup so that small launches still fill the chip.
-int gemv_waves(int total_wgs, int C);
+// Host policy: launch shape so that small launches still fill the chip.
+GemvShape gemv_shape(int total_rb, int m_blocks, int min_C);
 
 }  // namespace rt

@@ -38,7 +38,7 @@ def _case(seed, M, N, K):
     return O.make_linear_case(seed, M, N, K)
 
 
-@pytest.mark.parametrize("M,K", [(1, 2560), (64, 2560), (2048, 2560 // 8), (3, 6912), (5, 17), (1, 1), (70, 100)])
+@pytest.mark.parametrize("M,K", [(1, 2560), (64, 2560), (2048, 2560 // 8), (3, 6912), (5, 17), (1, 1), (70, 100), (2, 20000), (3, 16384), (2, 2576), (2, 16400)])
 def test_quantize_rows_bit_exact(hip, M, K):
     import torch
 

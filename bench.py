@@ -112,6 +112,62 @@ def torch_from(a):
     return torch.from_numpy(a)
 
 
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA, no sparsity
+
+
+def time_plan_gemv(torch, plan, reps):
+    """Average duration (ms) of the plan's GEMV/GEMM launches, HIP events on the stream."""
+    plan.quantize()
+    plan.gemv()
+    torch.cuda.synchronize()
+    evs = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        plan.quantize()
+        a.record()
+        plan.gemv()
+        b.record()
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    return float(sum(a.elapsed_time(b) for a, b in evs) / reps)
+
+
+def prefill_and_layer(torch, hip, gen, dev, reps=20):
+    """cfg 3 (prefill GEMMs, M=2048) and cfg 2 (one layer's 7 projections at M=64)."""
+    import numpy as np
+
+    out = {}
+    M = 2048
+    for name, (N, K) in {"gate_up_6912x2560": (6912, 2560), "down_2560x6912": (2560, 6912)}.items():
+        w = hip.upload_device(make_weights_device(torch, gen, N, K, dev), K, 0.03)
+        x = torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32)
+        y = torch.empty((M, N), device=dev, dtype=torch.float32)
+        plan = hip.plan([w], [x], [y])
+        ms = time_plan_gemv(torch, plan, reps)
+        ops = 2.0 * M * N * K
+        out[name] = {"M": M, "N": N, "K": K, "us": round(ms * 1e3, 2), "TOPS": round(ops / (ms * 1e-3) / 1e12, 1),
+                     "mfma_util": round(ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
+        del plan, w, x, y
+    # cfg 2: q, k, v, o, gate, up, down at M = 64 (projections sharing an input share its quantisation)
+    M = 64
+    shapes = [(2560, 2560, 0), (640, 2560, 0), (640, 2560, 0), (2560, 2560, 1), (6912, 2560, 2), (6912, 2560, 2),
+              (2560, 6912, 3)]
+    xs_in = [torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32) for K in (2560, 2560, 2560, 6912)]
+    ws, xs, ys = [], [], []
+    for N, K, xi in shapes:
+        ws.append(hip.upload_device(make_weights_device(torch, gen, N, K, dev), K, 0.03))
+        xs.append(xs_in[xi])
+        ys.append(torch.empty((M, N), device=dev, dtype=torch.float32))
+    plan = hip.plan(ws, xs, ys)
+    ms = time_plan_gemv(torch, plan, reps)
+    ops = sum(2.0 * M * N * K for N, K, _ in shapes)
+    wbytes = sum(N * K // 4 for N, K, _ in shapes)
+    out["layer_m64_7proj"] = {"M": M, "us": round(ms * 1e3, 2), "TOPS": round(ops / (ms * 1e-3) / 1e12, 1),
+                              "weight_GB_per_s": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                              "note": "7 projections of one BitNet-2B layer, one plan, projection launches only"}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -119,6 +175,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--groups", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the prefill / M=64 layer measurements")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (reference point for HBM counters)")
     args = ap.parse_args()
@@ -198,6 +255,8 @@ def main():
     lat_ms = [a.elapsed_time(b) for a, b in lat[G:]]
     single_ms = float(np.median(lat_ms))
 
+    extra = prefill_and_layer(torch, hip, gen, dev) if not args.no_extra else None
+
     # re-run the plan so ys[0] holds the plan's output for the parity check
     plan.run()
     torch.cuda.synchronize()
@@ -245,6 +304,7 @@ def main():
             "GB_per_s": round(gemv_bytes(1, N_OUT, K_IN) / (single_ms * 1e-3) / 1e9, 1),
             "note": "one rt_linear_f32 (quantise + GEMV launch) per matrix, rotating over the G matrices",
         },
+        "cfg3_prefill_and_cfg2_layer": extra,
         "cpu_baseline": cpu,
         "parity_checked": parity,
         "wall_s": round(wall, 3),

@@ -41,6 +41,7 @@ extern "C" {
 typedef struct rt_ctx rt_ctx;         /* device + stream + activation scratch */
 typedef struct rt_weights rt_weights; /* one device-resident ternary matrix   */
 typedef struct rt_plan rt_plan;       /* a prepared multi-matrix launch        */
+typedef struct rt_act rt_act;         /* reusable quantised activations        */
 
 /* Thread-local text of the last error (never NULL).  Replaces the reference's
  * exception text (src/rotor/gpu_layers.py:21-24). */
@@ -118,6 +119,40 @@ int rt_plan_run(rt_ctx* ctx, const rt_plan* plan);
 int rt_plan_quantize(rt_ctx* ctx, const rt_plan* plan);
 int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan);
 int rt_plan_free(rt_plan* plan);
+
+/* ---- reusable quantised activations ---------------------------------------------
+ * An rt_act holds up to M tokens of K int8 activations (device layout) and their
+ * per-token scales.  Filling one quantises fp32 values produced elsewhere, optionally
+ * fused with the operation that produces them; the linears then read it directly, so
+ * several projections of the same input share one quantisation
+ * (src/rotor/transformer.py:235-237 q/k/v, :329-330 gate/up). */
+int rt_act_create(rt_ctx* ctx, int M, int K, rt_act** out);
+int rt_act_free(rt_act* act);
+
+/* act <- per-token absmax int8 of x fp32 [M][K] (device). */
+int rt_act_quantize(rt_ctx* ctx, const float* x, int M, rt_act* act);
+
+/* act <- quantise(RMSNorm(x) * norm_w), RMSNorm of src/rotor/transformer.py:24-36:
+ * h = (x / sqrt(mean(x^2) + eps)) * norm_w with the mean of squares accumulated in
+ * f64 and rounded once to f32.  h_out (nullable, device fp32 [M][K]) receives h. */
+int rt_act_rmsnorm_quantize(rt_ctx* ctx, const float* x, const float* norm_w, float eps, int M, rt_act* act,
+                            float* h_out);
+
+/* act <- quantise(relu(gate)^2 * up), elementwise on fp32 [M][K] (device); a_out
+ * (nullable) receives the fp32 product. */
+int rt_act_relu2_mul_quantize(rt_ctx* ctx, const float* gate, const float* up, int M, rt_act* act, float* a_out);
+
+/* Natural-order int8 q [M][K] and scales s [M] (device) of the tokens held. */
+int rt_act_export(rt_ctx* ctx, const rt_act* act, int8_t* q, float* s);
+
+/* y fp32 [M][N] = ternary linear of the activations held (M = tokens held). */
+int rt_linear_act_f32(rt_ctx* ctx, const rt_weights* w, const rt_act* act, float* y);
+
+/* A plan over caller-filled activations: problem g reads act[g] (which must hold M
+ * tokens when the plan runs) and writes y[g] fp32 [M][N_g]; rt_plan_quantize is then a
+ * no-op and rt_plan_gemv / rt_plan_run launch the matrix kernels only. */
+int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_act* const* act, int M,
+                       float* const* y, rt_plan** out);
 
 #ifdef __cplusplus
 }

@@ -216,6 +216,43 @@ def rms_norm(x, weight, eps=1e-6):
     return ((x / norm) * np.asarray(weight, np.float32)).astype(np.float32)
 
 
+def rms_norm_f64acc(x, weight, eps=1e-6):
+    """RMSNorm with the mean of squares accumulated in float64 and rounded once to
+    float32: norm = sqrt(f32(sum(x^2) / K) + eps) in f32, h = (x / norm) * w in f32.
+
+    The formula of src/rotor/transformer.py:24-36; the accumulation precision is the
+    build's choice (order independent), the reference's fp32 pairwise mean agrees to
+    about one ulp.
+    """
+    x = np.asarray(x, dtype=np.float32)
+    K = x.shape[-1]
+    ss = np.sum(x.astype(np.float64) ** 2, axis=-1, keepdims=True)
+    ms = (ss / np.float64(K)).astype(np.float32)
+    norm = np.sqrt(ms + np.float32(eps)).astype(np.float32)
+    return ((x / norm) * np.asarray(weight, np.float32)).astype(np.float32)
+
+
+def w2a8_linear_from_q(q, s, W, scale):
+    """Epilogue of the W2A8 linear on given quantised activations:
+    y = (f32(acc) * s_x) * s_w, acc exact."""
+    acc = linear_i64_fast(q, W)
+    return (acc.astype(np.float32) * np.asarray(s, np.float32).reshape(-1, 1)) * np.float32(scale), acc
+
+
+def ffn_block_w2a8(x, norm_w, Wg, sg, Wu, su, Wd, sd, eps=1e-6):
+    """cfg 1 exactly as the device computes it: h = rms_norm_f64acc(x); q_h = quant(h);
+    g, u = W2A8 linears; a = relu(g)^2 * u; q_a = quant(a); y = W2A8 linear(q_a, Wd).
+    Every intermediate is reproducible bit for bit, so the device result must match."""
+    h = rms_norm_f64acc(x, norm_w, eps)
+    qh, sh = quant_rows(h)
+    g, acc_g = w2a8_linear_from_q(qh, sh, Wg, sg)
+    u, acc_u = w2a8_linear_from_q(qh, sh, Wu, su)
+    a = relu2_gate(g, u)
+    qa, sa = quant_rows(a)
+    y, acc_d = w2a8_linear_from_q(qa, sa, Wd, sd)
+    return y, dict(h=h, qh=qh, sh=sh, g=g, u=u, a=a, qa=qa, sa=sa, acc_g=acc_g, acc_u=acc_u, acc_d=acc_d)
+
+
 def relu2_gate(g, u):
     """relu(g)^2 * u in float32 (the configuration's FFN activation)."""
     g = np.asarray(g, np.float32)
@@ -270,4 +307,6 @@ PINNED = {
     "linear_i64": "brute-force loops on tiny shapes; linear_i64 == linear_i64_fast; linearity in q",
     "linear_ref_f32/ternary_linear": "float64 closed form on the same quantised inputs (|diff| << 3e-4)",
     "rms_norm/relu2_gate/ffn_block": "closed forms: constant rows, unit weight, sign cases",
+    "rms_norm_f64acc": "closed forms (constant rows -> +-w); agrees with rms_norm within 1 ulp",
+    "ffn_block_w2a8": "composition of pinned functions; equals ffn_block when intermediates agree",
 }

@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -100,7 +101,22 @@ struct rt_plan {
     void* act = nullptr;             // quantised activations of the U distinct inputs
     std::vector<GemvProb> probs;
     std::vector<QuantProb> quant;
+    std::vector<GemmArgs> gemms;     // M > kGemvMaxM: one MFMA GEMM launch per problem
+    std::vector<const rt_act*> acts; // plans over caller-quantised activations
 };
+
+struct rt_act {
+    int device = 0;
+    int Mcap = 0, K = 0, Kp = 0, Mpad_cap = 0;
+    int M = 0;      // tokens held (set by the last quantise call)
+    int Mpad = 0;   // rows valid for the GEMV/GEMM of M tokens (zero-filled past M)
+    int8_t* qx = nullptr;
+    float* sx = nullptr;
+    void* mem = nullptr;
+};
+
+// Rows the matrix kernels read for M tokens: GEMV tokens per workgroup, or GEMM tile rows.
+static int act_rows(int M) { return M > kGemvMaxM ? round_up(M, gemm_bm(M)) : round_up(M, gemv_mt(M)); }
 
 extern "C" {
 
@@ -268,7 +284,7 @@ static int stage_activations(rt_ctx* ctx, const float* x, const int8_t* q_in, in
     a.U = 1;
     a.M = M;
     a.Mpad = Mpad;
-    a.p = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp};
+    a.p = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp, q_in ? kPermute : kQuant, nullptr, 0.0f, nullptr};
     RT_HIP(launch_quant(a, ctx->stream));
     if (s_out) RT_HIP(hipMemcpyAsync(s_out, *sx, (size_t)M * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
     return RT_OK;
@@ -284,19 +300,15 @@ int rt_quantize_rows(rt_ctx* ctx, const float* x, int M, int K, int8_t* q, float
     return stage_activations(ctx, x, nullptr, M, K, M, q, s, &qx, &sx);
 }
 
-static int run_linear(rt_ctx* ctx, const rt_weights* w, const float* x, const int8_t* q, int M,
-                      const float* row_scale, void* out, bool out_i32, const char* who) {
-    if (!w) return fail(RT_EINVAL, std::string(who) + ": weights are NULL");
-    int rc = check_act(ctx, M, w->K, who);
-    if (rc) return rc;
-    if ((!x && !q) || !out) return fail(RT_EINVAL, std::string(who) + ": NULL pointer");
-    if (w->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": weights live on another device");
-    DeviceGuard g(ctx->device);
+// GEMV (M <= kGemvMaxM) or MFMA GEMM on activations already in the qx layout.
+static int launch_matrix(rt_ctx* ctx, const rt_weights* w, const int8_t* qx, const float* sx, int M,
+                         const float* row_scale, void* out, bool out_i32) {
+    if (M > kGemvMaxM) {
+        GemmArgs a{w->tiles, qx, sx, row_scale, out, w->scale, M, w->N, w->Np, w->C, w->N, out_i32 ? 1 : 0};
+        RT_HIP(launch_gemm(a, ctx->stream));
+        return RT_OK;
+    }
     const int mt = gemv_mt(M);
-    int8_t* qx;
-    float* sx;
-    rc = stage_activations(ctx, x, q, M, w->K, round_up(M, mt), nullptr, nullptr, &qx, &sx);
-    if (rc) return rc;
     GemvArgs a{};
     a.dev = nullptr;
     a.rb2p = nullptr;
@@ -308,6 +320,21 @@ static int run_linear(rt_ctx* ctx, const rt_weights* w, const float* x, const in
     const GemvShape shape = gemv_shape(a.total_rb, (M + mt - 1) / mt, w->C);
     RT_HIP(launch_gemv(a, mt, shape, ctx->stream));
     return RT_OK;
+}
+
+static int run_linear(rt_ctx* ctx, const rt_weights* w, const float* x, const int8_t* q, int M,
+                      const float* row_scale, void* out, bool out_i32, const char* who) {
+    if (!w) return fail(RT_EINVAL, std::string(who) + ": weights are NULL");
+    int rc = check_act(ctx, M, w->K, who);
+    if (rc) return rc;
+    if ((!x && !q) || !out) return fail(RT_EINVAL, std::string(who) + ": NULL pointer");
+    if (w->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": weights live on another device");
+    DeviceGuard g(ctx->device);
+    int8_t* qx;
+    float* sx;
+    rc = stage_activations(ctx, x, q, M, w->K, act_rows(M), nullptr, nullptr, &qx, &sx);
+    if (rc) return rc;
+    return launch_matrix(ctx, w, qx, sx, M, row_scale, out, out_i32);
 }
 
 int rt_linear_i32(rt_ctx* ctx, const rt_weights* w, const int8_t* q, int M, int32_t* acc) {
@@ -355,7 +382,7 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
     p->G = G;
     p->M = M;
     p->mt = gemv_mt(M);
-    p->Mpad = round_up(M, p->mt);
+    p->Mpad = M > kGemvMaxM ? round_up(M, gemm_bm(M)) : round_up(M, p->mt);
     // distinct inputs (same pointer => same quantisation; their K must agree)
     std::unordered_map<const float*, int> uid;
     std::vector<int> which(G);
@@ -397,7 +424,8 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
     for (int g = 0; g < G; ++g) {
         const int u = which[g];
         p->quant[u] = QuantProb{x[g], nullptr, reinterpret_cast<int8_t*>(base + qoff[u]),
-                                reinterpret_cast<float*>(base + soff[u]), nullptr, Ku[u], round_up(Ku[u], kChunk)};
+                                reinterpret_cast<float*>(base + soff[u]), nullptr, Ku[u], round_up(Ku[u], kChunk),
+                                kQuant, nullptr, 0.0f, nullptr};
     }
     int wg = 0, minC = 1 << 30;
     p->probs.resize(G);
@@ -410,6 +438,10 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
     }
     p->total_rb = wg;
     p->shape = gemv_shape(wg, (M + p->mt - 1) / p->mt, minC);
+    if (M > kGemvMaxM)
+        for (int g = 0; g < G; ++g)
+            p->gemms.push_back(GemmArgs{w[g]->tiles, p->probs[g].qx, p->probs[g].sx, nullptr, y[g], w[g]->scale, M,
+                                        w[g]->N, w[g]->Np, w[g]->C, w[g]->N, 0});
     std::vector<int> rb2p(wg);
     for (int g = 0; g < G; ++g)
         for (int r = 0; r < w[g]->Np / kRowBlock; ++r) rb2p[p->probs[g].wg_begin + r] = g;
@@ -450,6 +482,8 @@ int rt_plan_run(rt_ctx* ctx, const rt_plan* plan) {
 int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
     if (!ctx || !plan) return fail(RT_EINVAL, "rt_plan_gemv: NULL argument");
     if (plan->device != ctx->device) return fail(RT_EINVAL, "rt_plan_gemv: plan belongs to another device");
+    for (const rt_act* act : plan->acts)
+        if (act->M != plan->M) return fail(RT_EINVAL, "rt_plan_gemv: an input activation does not hold the plan's M tokens");
     DeviceGuard g(ctx->device);
     GemvArgs a{};
     a.dev = plan->dev_probs;
@@ -458,7 +492,146 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
     a.M = plan->M;
     a.out_i32 = 0;
     a.total_rb = plan->total_rb;
+    if (!plan->gemms.empty()) {
+        for (const GemmArgs& ga : plan->gemms) RT_HIP(launch_gemm(ga, ctx->stream));
+        return RT_OK;
+    }
     RT_HIP(launch_gemv(a, plan->mt, plan->shape, ctx->stream));
+    return RT_OK;
+}
+
+// --- reusable quantised activations ------------------------------------------------
+
+int rt_act_create(rt_ctx* ctx, int M, int K, rt_act** out) {
+    if (!ctx || !out) return fail(RT_EINVAL, "rt_act_create: NULL argument");
+    *out = nullptr;
+    if (M <= 0 || K <= 0 || M > (1 << 24) || K > (1 << 24)) return fail(RT_EINVAL, "rt_act_create: M or K out of range");
+    DeviceGuard g(ctx->device);
+    rt_act* a = new rt_act();
+    a->device = ctx->device;
+    a->Mcap = M;
+    a->K = K;
+    a->Kp = round_up(K, kChunk);
+    a->Mpad_cap = act_rows(M);
+    for (int m = 1; m <= M; ++m) a->Mpad_cap = std::max(a->Mpad_cap, act_rows(m));
+    const size_t qbytes = (size_t)a->Mpad_cap * a->Kp;
+    hipError_t e = hipMalloc(&a->mem, qbytes + (size_t)a->Mpad_cap * sizeof(float));
+    if (e != hipSuccess) {
+        delete a;
+        return fail(RT_ENOMEM, "rt_act_create: allocation failed");
+    }
+    a->qx = static_cast<int8_t*>(a->mem);
+    a->sx = reinterpret_cast<float*>(static_cast<char*>(a->mem) + qbytes);
+    *out = a;
+    return RT_OK;
+}
+
+int rt_act_free(rt_act* act) {
+    if (!act) return RT_OK;
+    DeviceGuard g(act->device);
+    if (act->mem) (void)hipFree(act->mem);
+    delete act;
+    return RT_OK;
+}
+
+static int act_fill(rt_ctx* ctx, rt_act* act, int M, int mode, const float* x, const float* aux, float eps,
+                    float* v_out, const char* who) {
+    if (!ctx || !act || !x) return fail(RT_EINVAL, std::string(who) + ": NULL argument");
+    if (M <= 0 || M > act->Mcap) return fail(RT_EINVAL, std::string(who) + ": M exceeds the activation capacity");
+    if (act->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": activations live on another device");
+    DeviceGuard g(ctx->device);
+    QuantArgs q{};
+    q.dev = nullptr;
+    q.U = 1;
+    q.M = M;
+    q.Mpad = act_rows(M);
+    q.p = QuantProb{x, nullptr, act->qx, act->sx, nullptr, act->K, act->Kp, mode, aux, eps, v_out};
+    RT_HIP(launch_quant(q, ctx->stream));
+    act->M = M;
+    act->Mpad = q.Mpad;
+    return RT_OK;
+}
+
+int rt_act_quantize(rt_ctx* ctx, const float* x, int M, rt_act* act) {
+    return act_fill(ctx, act, M, kQuant, x, nullptr, 0.0f, nullptr, "rt_act_quantize");
+}
+
+int rt_act_rmsnorm_quantize(rt_ctx* ctx, const float* x, const float* norm_w, float eps, int M, rt_act* act,
+                            float* h_out) {
+    if (!norm_w) return fail(RT_EINVAL, "rt_act_rmsnorm_quantize: norm weight is NULL");
+    return act_fill(ctx, act, M, kRmsNorm, x, norm_w, eps, h_out, "rt_act_rmsnorm_quantize");
+}
+
+int rt_act_relu2_mul_quantize(rt_ctx* ctx, const float* gate, const float* up, int M, rt_act* act, float* a_out) {
+    if (!up) return fail(RT_EINVAL, "rt_act_relu2_mul_quantize: up is NULL");
+    return act_fill(ctx, act, M, kRelu2Mul, gate, up, 0.0f, a_out, "rt_act_relu2_mul_quantize");
+}
+
+int rt_act_export(rt_ctx* ctx, const rt_act* act, int8_t* q, float* s) {
+    if (!ctx || !act || !q || !s) return fail(RT_EINVAL, "rt_act_export: NULL argument");
+    if (act->M <= 0) return fail(RT_EINVAL, "rt_act_export: activations are empty");
+    DeviceGuard g(ctx->device);
+    RT_HIP(launch_unpermute(act->qx, act->M, act->K, act->Kp, q, ctx->stream));
+    RT_HIP(hipMemcpyAsync(s, act->sx, (size_t)act->M * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+    return RT_OK;
+}
+
+int rt_linear_act_f32(rt_ctx* ctx, const rt_weights* w, const rt_act* act, float* y) {
+    if (!ctx || !w || !act || !y) return fail(RT_EINVAL, "rt_linear_act_f32: NULL argument");
+    if (act->M <= 0) return fail(RT_EINVAL, "rt_linear_act_f32: activations are empty");
+    if (act->K != w->K) return fail(RT_EINVAL, "rt_linear_act_f32: activation K differs from the weights' K");
+    if (w->device != ctx->device || act->device != ctx->device)
+        return fail(RT_EINVAL, "rt_linear_act_f32: operands live on another device");
+    DeviceGuard g(ctx->device);
+    return launch_matrix(ctx, w, act->qx, act->sx, act->M, nullptr, y, false);
+}
+
+int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_act* const* act, int M,
+                       float* const* y, rt_plan** out) {
+    if (!ctx || !w || !act || !y || !out) return fail(RT_EINVAL, "rt_plan_create_act: NULL argument");
+    *out = nullptr;
+    if (G <= 0 || G > (1 << 16)) return fail(RT_EINVAL, "rt_plan_create_act: G out of range");
+    for (int g = 0; g < G; ++g) {
+        if (!w[g] || !act[g] || !y[g]) return fail(RT_EINVAL, "rt_plan_create_act: NULL entry in a pointer array");
+        if (act[g]->K != w[g]->K) return fail(RT_EINVAL, "rt_plan_create_act: activation K differs from weights");
+        if (M <= 0 || M > act[g]->Mcap) return fail(RT_EINVAL, "rt_plan_create_act: M exceeds an activation capacity");
+        if (w[g]->device != ctx->device || act[g]->device != ctx->device)
+            return fail(RT_EINVAL, "rt_plan_create_act: operands live on another device");
+    }
+    DeviceGuard guard(ctx->device);
+    rt_plan* p = new rt_plan();
+    p->device = ctx->device;
+    p->G = G;
+    p->M = M;
+    p->mt = gemv_mt(M);
+    p->Mpad = act_rows(M);
+    p->U = 0;  // inputs are quantised by the caller
+    p->acts.assign(act, act + G);
+    int wg = 0, minC = 1 << 30;
+    p->probs.resize(G);
+    for (int g = 0; g < G; ++g) {
+        p->probs[g] = GemvProb{w[g]->tiles, act[g]->qx, act[g]->sx, nullptr, y[g], w[g]->scale,
+                               w[g]->N, w[g]->C, w[g]->N, wg};
+        wg += w[g]->Np / kRowBlock;
+        if (w[g]->C < minC) minC = w[g]->C;
+        if (M > kGemvMaxM)
+            p->gemms.push_back(GemmArgs{w[g]->tiles, act[g]->qx, act[g]->sx, nullptr, y[g], w[g]->scale, M,
+                                        w[g]->N, w[g]->Np, w[g]->C, w[g]->N, 0});
+    }
+    p->total_rb = wg;
+    p->shape = gemv_shape(wg, (M + p->mt - 1) / p->mt, minC);
+    std::vector<int> rb2p(wg);
+    for (int g = 0; g < G; ++g)
+        for (int r = 0; r < w[g]->Np / kRowBlock; ++r) rb2p[p->probs[g].wg_begin + r] = g;
+    hipError_t e = hipMalloc(&p->dev_probs, sizeof(GemvProb) * G);
+    if (e == hipSuccess) e = hipMalloc(&p->dev_rb2p, sizeof(int) * wg);
+    if (e == hipSuccess) e = hipMemcpy(p->dev_rb2p, rb2p.data(), sizeof(int) * wg, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(p->dev_probs, p->probs.data(), sizeof(GemvProb) * G, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        rt_plan_free(p);
+        return hip_fail(e, "rt_plan_create_act");
+    }
+    *out = p;
     return RT_OK;
 }
 

@@ -63,14 +63,25 @@ struct GemvShape {
     int nw;       // waves per workgroup
 };
 
-// ---- one quantisation problem (x fp32 [M][K] -> qx, sx) -------------------------
+// ---- one quantisation problem (-> qx, sx) -----------------------------------------
+// The value quantised for element k of a row depends on `mode`:
+//   kQuant    v = x[k]
+//   kPermute  q = q_in[k] taken as is (no quantisation, s = 1)
+//   kRmsNorm  v = (x[k] / sqrt(mean_k x^2 + eps)) * norm_w[k], mean accumulated in f64
+//   kRelu2Mul v = x[k] > 0 ? (x[k] * x[k]) * u[k] : 0        (x = gate, u = up)
+enum QuantMode { kQuant = 0, kPermute = 1, kRmsNorm = 2, kRelu2Mul = 3 };
+
 struct QuantProb {
-    const float* x;      // fp32 [M][K]           (quantise mode)
-    const int8_t* q_in;  // int8 [M][K]           (permute mode: no quantisation)
+    const float* x;      // fp32 [M][K] (gate in kRelu2Mul)
+    const int8_t* q_in;  // int8 [M][K] (kPermute)
     int8_t* qx;          // [Mpad][Kp]
     float* sx;           // [Mpad]
     int8_t* q_nat;       // optional natural-order q [M][K]
     int K, Kp;
+    int mode;
+    const float* aux;    // norm_w [K] (kRmsNorm) or up [M][K] (kRelu2Mul)
+    float eps;
+    float* v_out;        // optional fp32 [M][K]: the values that were quantised
 };
 
 struct QuantArgs {
@@ -79,12 +90,29 @@ struct QuantArgs {
     QuantProb p;
 };
 
+// ---- one GEMM problem (int8 MFMA path, M > kGemvMaxM) ---------------------------
+struct GemmArgs {
+    const v4u* w;        // weight tiles (Np rows, C chunks)
+    const int8_t* qx;    // [Mpad][Kp], Mpad a multiple of gemm_bm(M)
+    const float* sx;     // [Mpad]
+    const float* rs;     // [N] per-row scales or nullptr (then s_w)
+    void* out;           // float y[M][ldo] or int32 acc[M][ldo]
+    float s_w;
+    int M, N, Np, C, ldo, out_i32;
+};
+
+constexpr int kGemvMaxM = 8;  // up to this many tokens: VALU GEMV; beyond: MFMA GEMM
+inline int gemm_bm(int M) { return M <= 64 ? 64 : 128; }
+
 // Launchers (return hipSuccess or the launch error).
 hipError_t launch_relayout(const uint8_t* src, int N, int K, v4u* tiles, hipStream_t s);
 hipError_t launch_unrelayout(const v4u* tiles, int N, int K, uint8_t* dst, hipStream_t s);
 hipError_t launch_quant(const QuantArgs& a, hipStream_t s);
+// qx rows [M][Kp] (permuted) -> natural-order int8 [M][K]
+hipError_t launch_unpermute(const int8_t* qx, int M, int K, int Kp, int8_t* q, hipStream_t s);
 // mt = tokens per workgroup (1, 2, 4 or 8).
 hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s);
+hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 
 // Host policy: tokens per workgroup for M tokens.
 inline int gemv_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }

@@ -43,6 +43,15 @@ SIGNATURES = {
     "rt_plan_quantize": (_I, [_P, _P]),
     "rt_plan_gemv": (_I, [_P, _P]),
     "rt_plan_free": (_I, [_P]),
+    "rt_act_create": (_I, [_P, _I, _I, ctypes.POINTER(_P)]),
+    "rt_act_free": (_I, [_P]),
+    "rt_act_quantize": (_I, [_P, _P, _I, _P]),
+    "rt_act_rmsnorm_quantize": (_I, [_P, _P, _P, _F, _I, _P, _P]),
+    "rt_act_relu2_mul_quantize": (_I, [_P, _P, _P, _I, _P, _P]),
+    "rt_act_export": (_I, [_P, _P, _P, _P]),
+    "rt_linear_act_f32": (_I, [_P, _P, _P, _P]),
+    "rt_plan_create_act": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, ctypes.POINTER(_P),
+                                ctypes.POINTER(_P)]),
 }
 
 _lib = None

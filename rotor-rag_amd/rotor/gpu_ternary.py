@@ -101,6 +101,39 @@ class LinearPlan:
             pass
 
 
+class DeviceActivations:
+    """Reusable quantised activations (opaque ``rt_act``): up to ``capacity`` tokens of
+    ``in_features`` int8 values in the device layout, plus per-token scales."""
+
+    def __init__(self, backend, handle, capacity: int, K: int):
+        self._backend = backend
+        self.handle = handle
+        self.capacity = capacity
+        self.in_features = K
+        self.tokens = 0
+
+    def export(self):
+        """(q int8 [M, K], s fp32 [M]) device tensors of the tokens held, natural order."""
+        torch = _torch()
+        b = self._backend
+        q = torch.empty((self.tokens, self.in_features), dtype=torch.int8, device=b.device)
+        s = torch.empty((self.tokens,), dtype=torch.float32, device=b.device)
+        b._bind_stream()
+        _hip.check(_hip.load().rt_act_export(b.ctx, self.handle, q.data_ptr(), s.data_ptr()), "rt_act_export")
+        return q, s
+
+    def free(self) -> None:
+        if self.handle:
+            _hip.load().rt_act_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class HIPTernaryOps:
     """GPUTernaryOps-compatible HIP backend bound to one device."""
 
@@ -249,6 +282,83 @@ class HIPTernaryOps:
         _hip.check(self.lib.rt_plan_create(self.ctx, G, wa, xa, M, ya, ctypes.byref(h)), "rt_plan_create")
         return LinearPlan(self, h, (list(weights), list(xs), list(ys)))
 
+    # -- reusable quantised activations ------------------------------------------
+    def activations(self, capacity: int, in_features: int) -> DeviceActivations:
+        h = ctypes.c_void_p()
+        _hip.check(self.lib.rt_act_create(self.ctx, int(capacity), int(in_features), ctypes.byref(h)), "rt_act_create")
+        return DeviceActivations(self, h, int(capacity), int(in_features))
+
+    def _check_rows(self, t, act, name):
+        if t.ndim != 2 or t.shape[1] != act.in_features or t.shape[0] > act.capacity:
+            raise ValueError(f"{name} of shape {tuple(t.shape)} does not fit activations "
+                             f"[{act.capacity}, {act.in_features}]")
+
+    def act_quantize(self, x, act: DeviceActivations):
+        """act <- per-token int8 of x [M, K] (device)."""
+        xt = self._dev(x, _torch().float32)
+        self._check_rows(xt, act, "x")
+        self._bind_stream()
+        _hip.check(self.lib.rt_act_quantize(self.ctx, xt.data_ptr(), xt.shape[0], act.handle), "rt_act_quantize")
+        act.tokens = xt.shape[0]
+        return act
+
+    def act_rmsnorm_quantize(self, x, norm_w, act: DeviceActivations, eps: float = 1e-6, h_out=None):
+        """act <- int8 of RMSNorm(x) * norm_w (fused); optional fp32 h_out [M, K]."""
+        torch = _torch()
+        xt = self._dev(x, torch.float32)
+        wt = self._dev(norm_w, torch.float32).reshape(-1)
+        self._check_rows(xt, act, "x")
+        if wt.numel() != act.in_features:
+            raise ValueError("norm weight must have in_features entries")
+        self._bind_stream()
+        _hip.check(self.lib.rt_act_rmsnorm_quantize(self.ctx, xt.data_ptr(), wt.data_ptr(), float(eps), xt.shape[0],
+                                                    act.handle, h_out.data_ptr() if h_out is not None else None),
+                   "rt_act_rmsnorm_quantize")
+        act.tokens = xt.shape[0]
+        return act
+
+    def act_relu2_mul_quantize(self, gate, up, act: DeviceActivations, a_out=None):
+        """act <- int8 of relu(gate)^2 * up (fused); optional fp32 a_out [M, K]."""
+        torch = _torch()
+        g = self._dev(gate, torch.float32)
+        u = self._dev(up, torch.float32)
+        self._check_rows(g, act, "gate")
+        if u.shape != g.shape:
+            raise ValueError("gate and up must have the same shape")
+        self._bind_stream()
+        _hip.check(self.lib.rt_act_relu2_mul_quantize(self.ctx, g.data_ptr(), u.data_ptr(), g.shape[0], act.handle,
+                                                      a_out.data_ptr() if a_out is not None else None),
+                   "rt_act_relu2_mul_quantize")
+        act.tokens = g.shape[0]
+        return act
+
+    def linear_act(self, w: DeviceTernaryWeights, act: DeviceActivations, out=None):
+        """y [M, N] fp32 = W2A8 linear of the activations held."""
+        torch = _torch()
+        if act.in_features != w.in_features:
+            raise ValueError("activations and weights disagree on in_features")
+        y = out if out is not None else torch.empty((act.tokens, w.out_features), dtype=torch.float32,
+                                                    device=self.device)
+        self._bind_stream()
+        _hip.check(self.lib.rt_linear_act_f32(self.ctx, w.handle, act.handle, y.data_ptr()), "rt_linear_act_f32")
+        return y
+
+    def plan_act(self, weights, acts, M: int, ys) -> LinearPlan:
+        """One launch of len(weights) linears over caller-filled activations."""
+        G = len(weights)
+        if not (G == len(acts) == len(ys)) or G == 0:
+            raise ValueError("plan_act needs equal, non-zero numbers of weights, activations and outputs")
+        for w, a, y in zip(weights, acts, ys):
+            if a.in_features != w.in_features or tuple(y.shape) != (M, w.out_features) or not y.is_contiguous():
+                raise ValueError("plan_act: shapes do not match")
+        P = ctypes.c_void_p
+        wa = (P * G)(*[w.handle for w in weights])
+        aa = (P * G)(*[a.handle for a in acts])
+        ya = (P * G)(*[y.data_ptr() for y in ys])
+        h = ctypes.c_void_p()
+        _hip.check(self.lib.rt_plan_create_act(self.ctx, G, wa, aa, int(M), ya, ctypes.byref(h)), "rt_plan_create_act")
+        return LinearPlan(self, h, (list(weights), list(acts), list(ys)))
+
     def __del__(self):
         try:
             if getattr(self, "ctx", None):
@@ -258,4 +368,4 @@ class HIPTernaryOps:
             pass
 
 
-__all__ = ["HIPTernaryOps", "DeviceTernaryWeights", "LinearPlan", "unpack_rotor_rows"]
+__all__ = ["HIPTernaryOps", "DeviceTernaryWeights", "DeviceActivations", "LinearPlan", "unpack_rotor_rows"]

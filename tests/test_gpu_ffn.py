@@ -1,0 +1,141 @@
+"""GPU parity of the fused activation producers and of the cfg-1 FFN block.
+
+The device computes every intermediate exactly as oracle.ffn_block_w2a8 defines it
+(RMSNorm mean of squares accumulated in f64, IEEE fp32 elementwise, absmax int8,
+exact int32 accumulation), so intermediates and the block output are compared bit for
+bit; the output is also checked against the reference-formula chain (fp32 RMSNorm,
+np.dot on dequantised activations) within the quantisation error.
+"""
+import numpy as np
+import pytest
+
+from oracle import rotor_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,K", [(1, 2560), (7, 6912), (64, 2560), (3, 100), (2, 20000)])
+def test_act_quantize_matches_quantize_rows(hip, M, K):
+    import torch
+
+    x = np.random.default_rng(K + M).standard_normal((M, K), dtype=np.float32) * 4
+    act = hip.activations(M, K)
+    hip.act_quantize(torch.from_numpy(x), act)
+    q, s = act.export()
+    qo, so = O.quant_rows(x)
+    assert np.array_equal(_np(q), qo) and np.array_equal(_np(s), so)
+
+
+@pytest.mark.parametrize("M,K", [(1, 2560), (5, 2560), (64, 2560), (2, 6912), (3, 17), (2, 20000)])
+def test_act_rmsnorm_quantize_bit_exact(hip, M, K):
+    import torch
+
+    rng = np.random.default_rng(3 * K + M)
+    x = rng.standard_normal((M, K), dtype=np.float32) * rng.uniform(0.1, 10, (M, 1)).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    act = hip.activations(M, K)
+    h = torch.empty((M, K), dtype=torch.float32, device="cuda")
+    hip.act_rmsnorm_quantize(torch.from_numpy(x), torch.from_numpy(w), act, 1e-6, h_out=h)
+    ho = O.rms_norm_f64acc(x, w, 1e-6)
+    assert np.array_equal(_np(h), ho)
+    q, s = act.export()
+    qo, so = O.quant_rows(ho)
+    assert np.array_equal(_np(s), so) and np.array_equal(_np(q), qo)
+    # the reference's fp32 RMSNorm is within a few ulp
+    assert np.abs(_np(h) - O.rms_norm(x, w, 1e-6)).max() <= 4 * np.spacing(np.abs(ho).max())
+
+
+@pytest.mark.parametrize("M,K", [(1, 6912), (4, 6912), (64, 6912), (2, 33)])
+def test_act_relu2_mul_quantize_bit_exact(hip, M, K):
+    import torch
+
+    rng = np.random.default_rng(K * 7 + M)
+    g = rng.standard_normal((M, K), dtype=np.float32) * 2
+    u = rng.standard_normal((M, K), dtype=np.float32) * 2
+    g[0, :5] = [0.0, -0.0, -1.0, 1.0, 3.0]
+    act = hip.activations(M, K)
+    a = torch.empty((M, K), dtype=torch.float32, device="cuda")
+    hip.act_relu2_mul_quantize(torch.from_numpy(g), torch.from_numpy(u), act, a_out=a)
+    ao = O.relu2_gate(g, u)
+    assert np.array_equal(_np(a), ao)
+    q, s = act.export()
+    qo, so = O.quant_rows(ao)
+    assert np.array_equal(_np(s), so) and np.array_equal(_np(q), qo)
+
+
+@pytest.mark.parametrize("M", [1, 4, 64, 130])
+def test_linear_act_equals_linear(hip, M):
+    import torch
+
+    x, W, scale = O.make_linear_case(M, M, 640, 2560)
+    w = hip.upload(O.pack_rotor(W), 2560, scale)
+    act = hip.activations(M, 2560)
+    xt = torch.from_numpy(x).cuda()
+    hip.act_quantize(xt, act)
+    assert torch.equal(hip.linear_act(w, act), hip.linear_device(w, xt))
+
+
+@pytest.mark.parametrize("M", [1, 3, 64])
+def test_ffn_block_cfg1_bit_exact(hip, M):
+    import torch
+
+    from rotor import gpu_layers
+    from rotor.ffn import TernaryFFNBlock
+
+    D, F = 2560, 6912
+    rng = np.random.default_rng(100 + M)
+    Wg, sg = O.make_ternary(rng, F, D)
+    Wu, su = O.make_ternary(rng, F, D)
+    Wd, sd = O.make_ternary(rng, D, F)
+    nw = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    x = rng.standard_normal((M, D), dtype=np.float32)
+    gpu_layers._gpu_instance = hip
+    try:
+        blk = TernaryFFNBlock(D, F, use_gpu=True, max_tokens=64)
+        blk.load(nw, (O.pack_rotor(Wg), sg), (O.pack_rotor(Wu), su), (O.pack_rotor(Wd), sd))
+        y = blk.forward(x)
+        y2 = blk.forward(x)  # buffers and plans are reused
+    finally:
+        gpu_layers._gpu_instance = None
+    yo, it = O.ffn_block_w2a8(x, nw, Wg, sg, Wu, su, Wd, sd)
+    assert np.array_equal(y, yo) and np.array_equal(y2, yo)
+    y_ref, _ = O.ffn_block(x, nw, Wg, sg, Wu, su, Wd, sd)
+    assert np.abs(y - y_ref).max() < 0.05 * max(1.0, np.abs(y_ref).max())
+
+
+def test_ffn_block_graph_replay(hip):
+    """A captured forward replays with the same result (no allocation in the path)."""
+    import torch
+
+    from rotor import gpu_layers
+    from rotor.ffn import TernaryFFNBlock
+
+    D, F = 256, 512
+    rng = np.random.default_rng(7)
+    Wg, sg = O.make_ternary(rng, F, D)
+    Wu, su = O.make_ternary(rng, F, D)
+    Wd, sd = O.make_ternary(rng, D, F)
+    nw = np.ones(D, np.float32)
+    gpu_layers._gpu_instance = hip
+    try:
+        blk = TernaryFFNBlock(D, F, use_gpu=True, max_tokens=4)
+        blk.load(nw, (O.pack_rotor(Wg), sg), (O.pack_rotor(Wu), su), (O.pack_rotor(Wd), sd))
+        x = torch.zeros((1, D), device="cuda")
+        blk.forward_device(x)  # allocate buffers and plans outside the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            y = blk.forward_device(x)
+        for i in range(3):
+            xi = rng.standard_normal((1, D), dtype=np.float32)
+            x.copy_(torch.from_numpy(xi))
+            g.replay()
+            torch.cuda.synchronize()
+            yo, _ = O.ffn_block_w2a8(xi, nw, Wg, sg, Wu, su, Wd, sd)
+            assert np.array_equal(_np(y), yo), f"replay {i}"
+    finally:
+        gpu_layers._gpu_instance = None

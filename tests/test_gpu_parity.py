@@ -31,6 +31,13 @@ LINEAR_CASES = [
     (3, 77, 130),
     (9, 65, 63),
     (2, 129, 1000),
+    # int8-MFMA GEMM path (M > 8)
+    (16, 640, 2560),
+    (100, 300, 256),
+    (129, 2560, 2560),
+    (256, 6912, 2560),
+    (512, 2560, 6912),
+    (2048, 6912, 2560),  # cfg 3 (gate/up)
 ]
 
 

@@ -271,3 +271,34 @@ def test_c_oracle_matches_numpy_oracle(corc):
     acc2 = np.zeros((M, N), np.int64)
     corc.orc_linear_i64_packed(q.ctypes.data, p.ctypes.data, M, N, K, acc2.ctypes.data)
     assert np.array_equal(acc2, acc)
+
+
+def test_rms_norm_f64acc():
+    x = np.full((3, 64), -2.0, np.float32)
+    w = np.linspace(0.5, 1.5, 64).astype(np.float32)
+    assert np.allclose(O.rms_norm_f64acc(x, w, eps=0.0), -w, atol=0, rtol=1e-7)
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((5, 2560), dtype=np.float32) * 3
+    a, b = O.rms_norm_f64acc(x, w[:1].repeat(2560)), O.rms_norm(x, w[:1].repeat(2560))
+    assert np.abs(a - b).max() <= 2 * np.spacing(np.abs(b).max())
+
+
+def test_ffn_block_w2a8_composes_pinned_parts():
+    rng = np.random.default_rng(10)
+    D, F = 64, 96
+    x = rng.standard_normal((2, D), dtype=np.float32)
+    nw = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    Wg, sg = O.make_ternary(rng, F, D)
+    Wu, su = O.make_ternary(rng, F, D)
+    Wd, sd = O.make_ternary(rng, D, F)
+    y, it = O.ffn_block_w2a8(x, nw, Wg, sg, Wu, su, Wd, sd)
+    assert y.shape == (2, D)
+    # each stage is the pinned function applied to the previous stage
+    assert np.array_equal(it["acc_g"], O.linear_i64(it["qh"], Wg))
+    assert np.array_equal(it["a"], O.relu2_gate(it["g"], it["u"]))
+    q, s = O.quant_rows(it["a"])
+    assert np.array_equal(q, it["qa"]) and np.array_equal(s, it["sa"])
+    assert np.array_equal(it["acc_d"], O.linear_i64(q, Wd))
+    # and agrees with the reference-formula chain within the quantisation error
+    y_ref, _ = O.ffn_block(x, nw, Wg, sg, Wu, su, Wd, sd)
+    assert np.abs(y - y_ref).max() < 0.05 * max(1.0, np.abs(y_ref).max())

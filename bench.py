@@ -168,6 +168,45 @@ def prefill_and_layer(torch, hip, gen, dev, reps=20):
     return out
 
 
+def ffn_block_cfg1(torch, hip, gen, dev, reps=200):
+    """cfg 1: RMSNorm -> gate & up -> relu^2(gate)*up -> down at batch 1, captured in a
+    HIP graph (4 launches) and replayed; reports the per-block latency."""
+    from rotor import gpu_layers
+    from rotor.ffn import TernaryFFNBlock
+
+    D, F = 2560, 6912
+    gpu_layers._gpu_instance = hip
+    try:
+        blk = TernaryFFNBlock(D, F, use_gpu=True, max_tokens=1)
+        to_np = lambda t: t.cpu().numpy()
+        blk.load(torch.rand(D, generator=gen, device=dev).add(0.5).cpu().numpy(),
+                 (to_np(make_weights_device(torch, gen, F, D, dev)), 0.03),
+                 (to_np(make_weights_device(torch, gen, F, D, dev)), 0.03),
+                 (to_np(make_weights_device(torch, gen, D, F, dev)), 0.03))
+    finally:
+        gpu_layers._gpu_instance = None
+    x = torch.randn((1, D), generator=gen, device=dev)
+    blk.forward_device(x)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        blk.forward_device(x)
+    for _ in range(10):
+        graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) / reps * 1e3
+    wbytes = 3 * D * F // 4
+    return {"us_per_block": round(us, 2), "weight_GB_per_s": round(wbytes / (us * 1e-6) / 1e9, 1),
+            "launches": 4, "note": "batch 1, graph-replayed back to back, weights 13.3 MB (L2/MALL-resident "
+                                   "when replayed on one block)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -256,6 +295,8 @@ def main():
     single_ms = float(np.median(lat_ms))
 
     extra = prefill_and_layer(torch, hip, gen, dev) if not args.no_extra else None
+    if extra is not None:
+        extra["cfg1_ffn_block_m1"] = ffn_block_cfg1(torch, hip, gen, dev)
 
     # re-run the plan so ys[0] holds the plan's output for the parity check
     plan.run()

@@ -142,17 +142,55 @@ int rt_act_rmsnorm_quantize(rt_ctx* ctx, const float* x, const float* norm_w, fl
  * (nullable) receives the fp32 product. */
 int rt_act_relu2_mul_quantize(rt_ctx* ctx, const float* gate, const float* up, int M, rt_act* act, float* a_out);
 
+/* act <- quantise(RMSNorm(relu(gate)^2 * up) * norm_w): the FFN activation followed
+ * by BitNet's FFN sub-norm (src/rotor/transformer.py:336-337 applies ffn_norm before
+ * down_proj); a_out (nullable) receives the normalised fp32 values. */
+int rt_act_relu2_mul_norm_quantize(rt_ctx* ctx, const float* gate, const float* up, const float* norm_w, float eps,
+                                   int M, rt_act* act, float* a_out);
+
 /* Natural-order int8 q [M][K] and scales s [M] (device) of the tokens held. */
 int rt_act_export(rt_ctx* ctx, const rt_act* act, int8_t* q, float* s);
 
-/* y fp32 [M][N] = ternary linear of the activations held (M = tokens held). */
-int rt_linear_act_f32(rt_ctx* ctx, const rt_weights* w, const rt_act* act, float* y);
+/* y fp32 [M][N] = ternary linear of the activations held (M = tokens held), plus
+ * residual fp32 [M][N] when non-NULL (the residual adds of
+ * src/rotor/transformer.py:396-411); y may alias residual. */
+int rt_linear_act_f32(rt_ctx* ctx, const rt_weights* w, const rt_act* act, const float* residual, float* y);
 
 /* A plan over caller-filled activations: problem g reads act[g] (which must hold M
  * tokens when the plan runs) and writes y[g] fp32 [M][N_g]; rt_plan_quantize is then a
  * no-op and rt_plan_gemv / rt_plan_run launch the matrix kernels only. */
 int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_act* const* act, int M,
                        float* const* y, rt_plan** out);
+
+/* ---- kernels around the linears for BitNet-2B-shape inference ----------------------
+ * Positions are read from device memory (`pos`: position of the first of the M tokens)
+ * so that a decode step does not depend on host values and can be replayed as a graph.
+ * The KV cache of one layer is k_cache fp32 [Hkv][hd][Lmax] (dimension-major) and
+ * v_cache fp32 [Hkv][Lmax][hd]; rope is fp32 [Lmax][hd/2][2] = (cos, sin). */
+
+/* h fp32 [M][D] = emb bf16 [V][D] rows ids[0..M) (src/rotor/bitnet_model.py:220). */
+int rt_embed(rt_ctx* ctx, const uint16_t* emb, int V, int D, const int* ids, int M, float* h);
+
+/* RoPE (rotate-half) on q [M][H*hd] and k [M][Hkv*hd] in place, then k and v
+ * [M][Hkv*hd] into the caches at positions *pos .. *pos+M-1 (replaces the KV concat of
+ * src/rotor/transformer.py:250-252 with an in-place cache). */
+int rt_rope_kv_append(rt_ctx* ctx, float* q, float* k, const float* v, float* k_cache, float* v_cache,
+                      const float* rope, int M, int H, int Hkv, int hd, int Lmax, const int* pos);
+
+/* Causal GQA attention: out [M][H*hd] for queries at *pos+m over keys 0..*pos+m,
+ * scale 1/sqrt(hd) (src/rotor/transformer.py:260-281 plus the causal mask). */
+int rt_attention(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, float* out, int M, int H,
+                 int Hkv, int hd, int Lmax, const int* pos);
+
+/* Final RMSNorm of x fp32 [D] with norm_w, tied bf16 LM head logits [V]
+ * (src/rotor/bitnet_model.py:231-235) and greedy argmax (src/rotor/generation.py:42;
+ * first index of the maximum).  `best` (device u64, zero before first use) is left
+ * zero.  token <- argmax; when non-NULL: next_ids[0] <- token and, with
+ * p = *pos + advance, out_tokens[p - 1 - pos_base] <- token (if in [0, out_cap)) and
+ * *pos <- p (advance = tokens consumed by this forward). */
+int rt_lm_head_argmax(rt_ctx* ctx, const uint16_t* emb, const float* x, const float* norm_w, float eps, int V, int D,
+                      float* logits, unsigned long long* best, int* token, int* pos, int advance, int* next_ids,
+                      int* out_tokens, int pos_base, int out_cap);
 
 #ifdef __cplusplus
 }

@@ -277,6 +277,146 @@ def ffn_block(x, norm_w, Wg, sg, Wu, su, Wd, sd, eps=1e-6):
 
 
 # ---------------------------------------------------------------------------
+# a11: the decode model of the benchmark configuration (cfg 4), restated in NumPy
+# ---------------------------------------------------------------------------
+
+
+def bf16_to_f32(b):
+    """uint16 bf16 bit patterns -> float32 (exact)."""
+    return (np.asarray(b, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16(x):
+    """float32 -> bf16 bit patterns, round to nearest even."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return r.astype(np.uint16)
+
+
+def rope_table(max_len, head_dim, theta):
+    """(cos, sin) of pos * theta^(-2i/head_dim) [max_len, head_dim/2, 2], f64 then f32."""
+    i = np.arange(head_dim // 2, dtype=np.float64)
+    inv = theta ** (-(2.0 * i) / head_dim)
+    ang = np.arange(max_len, dtype=np.float64)[:, None] * inv[None, :]
+    return np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+
+
+def apply_rope(x, table, pos0):
+    """Rotate-half RoPE on x [M, heads, hd] for positions pos0.. in float32:
+    x1' = x1*c - x2*s, x2' = x2*c + x1*s (two roundings per product, then the add)."""
+    M, _, hd = x.shape
+    half = hd // 2
+    cs = table[pos0:pos0 + M]  # [M, half, 2]
+    c, s = cs[:, None, :, 0], cs[:, None, :, 1]
+    x1, x2 = x[..., :half], x[..., half:]
+    return np.concatenate([x1 * c - x2 * s, x2 * c + x1 * s], axis=-1).astype(np.float32)
+
+
+def causal_gqa_attention(q, K, V, pos0):
+    """q [M, H, hd] (queries at pos0..), K/V [Hkv, L, hd] (all cached keys) ->
+    out [M, H, hd]; scale 1/sqrt(hd); query m sees keys 0..pos0+m.  Computed in f64
+    (src/rotor/transformer.py:260-281 plus the causal mask of the configuration)."""
+    M, H, hd = q.shape
+    Hkv = K.shape[0]
+    rep = H // Hkv
+    out = np.zeros((M, H, hd), np.float64)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    for m in range(M):
+        L = pos0 + m + 1
+        for h in range(H):
+            kk = K[h // rep, :L].astype(np.float64)
+            sc = (kk @ q[m, h].astype(np.float64)) * np.float64(scale)
+            p = np.exp(sc - sc.max())
+            out[m, h] = (p / p.sum()) @ V[h // rep, :L].astype(np.float64)
+    return out.astype(np.float32)
+
+
+def bitnet_forward(params, cfg, ids, cache):
+    """One forward of the cfg-4 model on token ids [M] at position len(cache)
+    (cache: dict with per-layer K/V lists, updated in place).  Returns the final-normed
+    hidden states [M, D] and the logits of the last token [V] (f64 accumulation).
+
+    Layer: x += Wo(subnorm(attn(rope(Wq a), rope(Wk a), Wv a))), a = norm(x);
+           x += Wd(subnorm(relu(Wg f)^2 * Wu f)), f = norm(x)  -- every linear W2A8.
+    """
+    H, Hkv, eps = cfg["n_heads"], cfg["n_kv_heads"], cfg.get("rms_norm_eps", 1e-6)
+    D = cfg["d_model"]
+    hd = D // H
+    pos0 = cache.get("len", 0)
+    emb = bf16_to_f32(params["embed"])
+    x = emb[np.asarray(ids)].astype(np.float32)
+    M = x.shape[0]
+    table = params["rope"]
+    for li, L in enumerate(params["layers"]):
+        a = rms_norm_f64acc(x, L["input_norm"], eps)
+        qa, sa = quant_rows(a)
+        q = w2a8_linear_from_q(qa, sa, L["q_proj"][0], L["q_proj"][1])[0]
+        k = w2a8_linear_from_q(qa, sa, L["k_proj"][0], L["k_proj"][1])[0]
+        v = w2a8_linear_from_q(qa, sa, L["v_proj"][0], L["v_proj"][1])[0]
+        q = apply_rope(q.reshape(M, H, hd), table, pos0)
+        k = apply_rope(k.reshape(M, Hkv, hd), table, pos0)
+        kv = cache.setdefault(li, {"k": np.zeros((Hkv, 0, hd), np.float32), "v": np.zeros((Hkv, 0, hd), np.float32)})
+        kv["k"] = np.concatenate([kv["k"], k.transpose(1, 0, 2)], axis=1)
+        kv["v"] = np.concatenate([kv["v"], v.reshape(M, Hkv, hd).transpose(1, 0, 2)], axis=1)
+        o = causal_gqa_attention(q, kv["k"], kv["v"], pos0).reshape(M, H * hd)
+        on = rms_norm_f64acc(o, L["attn_sub_norm"], eps) if L.get("attn_sub_norm") is not None else o
+        qo, so = quant_rows(on)
+        x = x + w2a8_linear_from_q(qo, so, L["o_proj"][0], L["o_proj"][1])[0]
+        f = rms_norm_f64acc(x, L["post_norm"], eps)
+        qf, sf = quant_rows(f)
+        g = w2a8_linear_from_q(qf, sf, L["gate_proj"][0], L["gate_proj"][1])[0]
+        u = w2a8_linear_from_q(qf, sf, L["up_proj"][0], L["up_proj"][1])[0]
+        act = relu2_gate(g, u)
+        if L.get("ffn_sub_norm") is not None:
+            act = rms_norm_f64acc(act, L["ffn_sub_norm"], eps)
+        qd, sd = quant_rows(act)
+        x = x + w2a8_linear_from_q(qd, sd, L["down_proj"][0], L["down_proj"][1])[0]
+    cache["len"] = pos0 + M
+    hn = rms_norm_f64acc(x, params["final_norm"], eps)
+    logits = emb.astype(np.float64) @ hn[-1].astype(np.float64)
+    return hn, logits
+
+
+def bitnet_greedy(params, cfg, prompt, n):
+    """Greedy decode (src/rotor/generation.py:244-279 protocol): prompt, then one token
+    per step; returns the n generated ids and the per-step top-2 logit gaps."""
+    cache = {}
+    _, logits = bitnet_forward(params, cfg, prompt, cache)
+    toks, gaps = [], []
+    for i in range(n):
+        t = int(np.argmax(logits))
+        srt = np.sort(logits)
+        toks.append(t)
+        gaps.append(float(srt[-1] - srt[-2]))
+        if i + 1 < n:
+            _, logits = bitnet_forward(params, cfg, [t], cache)
+    return np.array(toks), np.array(gaps)
+
+
+def make_bitnet_params(seed, cfg, max_len, sub_norms=True):
+    """Seeded random-init cfg-4 weights: ternary matrices and scales as in cfg 0,
+    norm weights ~U(0.5, 1.5), bf16 embedding ~N(0, 1)."""
+    rng = np.random.default_rng(seed)
+    D, F, H, Hkv, V = cfg["d_model"], cfg["d_ff"], cfg["n_heads"], cfg["n_kv_heads"], cfg["vocab_size"]
+    hd = D // H
+    shapes = {"q_proj": (H * hd, D), "k_proj": (Hkv * hd, D), "v_proj": (Hkv * hd, D), "o_proj": (D, H * hd),
+              "gate_proj": (F, D), "up_proj": (F, D), "down_proj": (D, F)}
+    layers = []
+    for _ in range(cfg["n_layers"]):
+        L = {"input_norm": rng.uniform(0.5, 1.5, D).astype(np.float32),
+             "post_norm": rng.uniform(0.5, 1.5, D).astype(np.float32)}
+        for name, (n, k) in shapes.items():
+            L[name] = make_ternary(rng, n, k)
+        L["attn_sub_norm"] = rng.uniform(0.5, 1.5, D).astype(np.float32) if sub_norms else None
+        L["ffn_sub_norm"] = rng.uniform(0.5, 1.5, F).astype(np.float32) if sub_norms else None
+        layers.append(L)
+    embed = f32_to_bf16(rng.standard_normal((V, D), dtype=np.float32))
+    final_norm = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    return {"layers": layers, "embed": embed, "final_norm": final_norm,
+            "rope": rope_table(max_len, hd, cfg.get("rope_theta", 500000.0))}
+
+
+# ---------------------------------------------------------------------------
 # Seeded synthetic inputs (the generators of the benchmark configurations)
 # ---------------------------------------------------------------------------
 
@@ -309,4 +449,7 @@ PINNED = {
     "rms_norm/relu2_gate/ffn_block": "closed forms: constant rows, unit weight, sign cases",
     "rms_norm_f64acc": "closed forms (constant rows -> +-w); agrees with rms_norm within 1 ulp",
     "ffn_block_w2a8": "composition of pinned functions; equals ffn_block when intermediates agree",
+    "bf16/rope/attention/bitnet_forward": "bf16 round trip; RoPE norm preservation and pos-0 identity; attention "
+                                          "closed forms (one key -> V, equal keys -> mean of V, causal prefix); "
+                                          "incremental decode == full-sequence forward",
 }

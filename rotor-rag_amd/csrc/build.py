@@ -20,7 +20,7 @@ PKG = CSRC.parent
 LIB_DIR = PKG / "rotor" / "lib"
 LIB = LIB_DIR / "librotor_hip.so"
 OBJ_DIR = PKG / "build" / "obj"
-SOURCES = ["rt_layout.hip", "rt_quant.hip", "rt_gemv.hip", "rt_gemm.hip", "rt_api.hip"]
+SOURCES = ["rt_layout.hip", "rt_quant.hip", "rt_gemv.hip", "rt_gemm.hip", "rt_model.hip", "rt_api.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

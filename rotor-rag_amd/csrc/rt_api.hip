@@ -8,6 +8,7 @@
 
 #include <cstdio>
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <string>
 #include <unordered_map>
@@ -284,7 +285,7 @@ static int stage_activations(rt_ctx* ctx, const float* x, const int8_t* q_in, in
     a.U = 1;
     a.M = M;
     a.Mpad = Mpad;
-    a.p = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp, q_in ? kPermute : kQuant, nullptr, 0.0f, nullptr};
+    a.p = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp, q_in ? kPermute : kQuant, nullptr, 0.0f, nullptr, nullptr};
     RT_HIP(launch_quant(a, ctx->stream));
     if (s_out) RT_HIP(hipMemcpyAsync(s_out, *sx, (size_t)M * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
     return RT_OK;
@@ -302,9 +303,9 @@ int rt_quantize_rows(rt_ctx* ctx, const float* x, int M, int K, int8_t* q, float
 
 // GEMV (M <= kGemvMaxM) or MFMA GEMM on activations already in the qx layout.
 static int launch_matrix(rt_ctx* ctx, const rt_weights* w, const int8_t* qx, const float* sx, int M,
-                         const float* row_scale, void* out, bool out_i32) {
+                         const float* row_scale, void* out, bool out_i32, const float* res = nullptr) {
     if (M > kGemvMaxM) {
-        GemmArgs a{w->tiles, qx, sx, row_scale, out, w->scale, M, w->N, w->Np, w->C, w->N, out_i32 ? 1 : 0};
+        GemmArgs a{w->tiles, qx, sx, row_scale, out, w->scale, M, w->N, w->Np, w->C, w->N, out_i32 ? 1 : 0, res};
         RT_HIP(launch_gemm(a, ctx->stream));
         return RT_OK;
     }
@@ -316,7 +317,7 @@ static int launch_matrix(rt_ctx* ctx, const rt_weights* w, const int8_t* qx, con
     a.M = M;
     a.out_i32 = out_i32 ? 1 : 0;
     a.total_rb = w->Np / kRowBlock;
-    a.p = GemvProb{w->tiles, qx, sx, row_scale, out, w->scale, w->N, w->C, w->N, 0};
+    a.p = GemvProb{w->tiles, qx, sx, row_scale, out, w->scale, w->N, w->C, w->N, 0, res};
     const GemvShape shape = gemv_shape(a.total_rb, (M + mt - 1) / mt, w->C);
     RT_HIP(launch_gemv(a, mt, shape, ctx->stream));
     return RT_OK;
@@ -425,7 +426,7 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
         const int u = which[g];
         p->quant[u] = QuantProb{x[g], nullptr, reinterpret_cast<int8_t*>(base + qoff[u]),
                                 reinterpret_cast<float*>(base + soff[u]), nullptr, Ku[u], round_up(Ku[u], kChunk),
-                                kQuant, nullptr, 0.0f, nullptr};
+                                kQuant, nullptr, 0.0f, nullptr, nullptr};
     }
     int wg = 0, minC = 1 << 30;
     p->probs.resize(G);
@@ -535,7 +536,7 @@ int rt_act_free(rt_act* act) {
 }
 
 static int act_fill(rt_ctx* ctx, rt_act* act, int M, int mode, const float* x, const float* aux, float eps,
-                    float* v_out, const char* who) {
+                    float* v_out, const char* who, const float* aux2 = nullptr) {
     if (!ctx || !act || !x) return fail(RT_EINVAL, std::string(who) + ": NULL argument");
     if (M <= 0 || M > act->Mcap) return fail(RT_EINVAL, std::string(who) + ": M exceeds the activation capacity");
     if (act->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": activations live on another device");
@@ -545,7 +546,7 @@ static int act_fill(rt_ctx* ctx, rt_act* act, int M, int mode, const float* x, c
     q.U = 1;
     q.M = M;
     q.Mpad = act_rows(M);
-    q.p = QuantProb{x, nullptr, act->qx, act->sx, nullptr, act->K, act->Kp, mode, aux, eps, v_out};
+    q.p = QuantProb{x, nullptr, act->qx, act->sx, nullptr, act->K, act->Kp, mode, aux, eps, v_out, aux2};
     RT_HIP(launch_quant(q, ctx->stream));
     act->M = M;
     act->Mpad = q.Mpad;
@@ -567,6 +568,12 @@ int rt_act_relu2_mul_quantize(rt_ctx* ctx, const float* gate, const float* up, i
     return act_fill(ctx, act, M, kRelu2Mul, gate, up, 0.0f, a_out, "rt_act_relu2_mul_quantize");
 }
 
+int rt_act_relu2_mul_norm_quantize(rt_ctx* ctx, const float* gate, const float* up, const float* norm_w, float eps,
+                                   int M, rt_act* act, float* a_out) {
+    if (!up || !norm_w) return fail(RT_EINVAL, "rt_act_relu2_mul_norm_quantize: NULL argument");
+    return act_fill(ctx, act, M, kRelu2MulNorm, gate, up, eps, a_out, "rt_act_relu2_mul_norm_quantize", norm_w);
+}
+
 int rt_act_export(rt_ctx* ctx, const rt_act* act, int8_t* q, float* s) {
     if (!ctx || !act || !q || !s) return fail(RT_EINVAL, "rt_act_export: NULL argument");
     if (act->M <= 0) return fail(RT_EINVAL, "rt_act_export: activations are empty");
@@ -576,14 +583,14 @@ int rt_act_export(rt_ctx* ctx, const rt_act* act, int8_t* q, float* s) {
     return RT_OK;
 }
 
-int rt_linear_act_f32(rt_ctx* ctx, const rt_weights* w, const rt_act* act, float* y) {
+int rt_linear_act_f32(rt_ctx* ctx, const rt_weights* w, const rt_act* act, const float* residual, float* y) {
     if (!ctx || !w || !act || !y) return fail(RT_EINVAL, "rt_linear_act_f32: NULL argument");
     if (act->M <= 0) return fail(RT_EINVAL, "rt_linear_act_f32: activations are empty");
     if (act->K != w->K) return fail(RT_EINVAL, "rt_linear_act_f32: activation K differs from the weights' K");
     if (w->device != ctx->device || act->device != ctx->device)
         return fail(RT_EINVAL, "rt_linear_act_f32: operands live on another device");
     DeviceGuard g(ctx->device);
-    return launch_matrix(ctx, w, act->qx, act->sx, act->M, nullptr, y, false);
+    return launch_matrix(ctx, w, act->qx, act->sx, act->M, nullptr, y, false, residual);
 }
 
 int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_act* const* act, int M,
@@ -632,6 +639,62 @@ int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_
         return hip_fail(e, "rt_plan_create_act");
     }
     *out = p;
+    return RT_OK;
+}
+
+// --- model kernels --------------------------------------------------------------------
+
+int rt_embed(rt_ctx* ctx, const uint16_t* emb, int V, int D, const int* ids, int M, float* h) {
+    if (!ctx || !emb || !ids || !h) return fail(RT_EINVAL, "rt_embed: NULL argument");
+    if (V <= 0 || D <= 0 || M <= 0) return fail(RT_EINVAL, "rt_embed: sizes must be positive");
+    DeviceGuard g(ctx->device);
+    RT_HIP(launch_embed(emb, ids, M, V, D, h, ctx->stream));
+    return RT_OK;
+}
+
+static int check_heads(int H, int Hkv, int hd, int Lmax, const char* who) {
+    if (H <= 0 || Hkv <= 0 || H % Hkv || hd <= 0 || hd % 2 || 256 % hd || Lmax <= 0 || Lmax > (1 << 16))
+        return fail(RT_EINVAL, std::string(who) + ": unsupported head layout (H % Hkv == 0, even hd dividing 256, "
+                                                  "Lmax <= 65536)");
+    return RT_OK;
+}
+
+int rt_rope_kv_append(rt_ctx* ctx, float* q, float* k, const float* v, float* k_cache, float* v_cache,
+                      const float* rope, int M, int H, int Hkv, int hd, int Lmax, const int* pos) {
+    if (!ctx || !q || !k || !v || !k_cache || !v_cache || !rope || !pos)
+        return fail(RT_EINVAL, "rt_rope_kv_append: NULL argument");
+    int rc = check_heads(H, Hkv, hd, Lmax, "rt_rope_kv_append");
+    if (rc) return rc;
+    if (M <= 0 || M > Lmax) return fail(RT_EINVAL, "rt_rope_kv_append: M out of range");
+    DeviceGuard g(ctx->device);
+    RT_HIP(launch_rope_append(q, k, v, k_cache, v_cache, rope, M, H, Hkv, hd, Lmax, pos, ctx->stream));
+    return RT_OK;
+}
+
+int rt_attention(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, float* out, int M, int H,
+                 int Hkv, int hd, int Lmax, const int* pos) {
+    if (!ctx || !q || !k_cache || !v_cache || !out || !pos) return fail(RT_EINVAL, "rt_attention: NULL argument");
+    int rc = check_heads(H, Hkv, hd, Lmax, "rt_attention");
+    if (rc) return rc;
+    if (M <= 0 || M > Lmax) return fail(RT_EINVAL, "rt_attention: M out of range");
+    if ((size_t)(hd + Lmax + 256) * sizeof(float) > 160 * 1024)
+        return fail(RT_EINVAL, "rt_attention: Lmax too large for the scores buffer");
+    DeviceGuard g(ctx->device);
+    RT_HIP(launch_attention(q, k_cache, v_cache, out, M, H, Hkv, hd, Lmax, pos, 1.0f / sqrtf((float)hd),
+                            ctx->stream));
+    return RT_OK;
+}
+
+int rt_lm_head_argmax(rt_ctx* ctx, const uint16_t* emb, const float* x, const float* norm_w, float eps, int V, int D,
+                      float* logits, unsigned long long* best, int* token, int* pos, int advance, int* next_ids,
+                      int* out_tokens, int pos_base, int out_cap) {
+    if (!ctx || !emb || !x || !norm_w || !logits || !best || !token)
+        return fail(RT_EINVAL, "rt_lm_head_argmax: NULL argument");
+    if (V <= 0 || D <= 0 || D % 512 || (D / 512 != 1 && D / 512 != 2 && D / 512 != 4 && D / 512 != 5 && D / 512 != 8))
+        return fail(RT_EINVAL, "rt_lm_head_argmax: D must be 512, 1024, 2048, 2560 or 4096");
+    DeviceGuard g(ctx->device);
+    RT_HIP(launch_lm_head(emb, x, norm_w, eps, V, D, logits, best, token, pos, advance, next_ids, out_tokens, pos_base,
+                          out_cap, ctx->stream));
     return RT_OK;
 }
 

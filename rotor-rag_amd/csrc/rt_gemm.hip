@@ -123,7 +123,9 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
                     static_cast<int*>(a.out)[(size_t)m * a.ldo + n] = v;
                 } else {
                     const float sw = a.rs ? a.rs[n] : a.s_w;
-                    static_cast<float*>(a.out)[(size_t)m * a.ldo + n] = ((float)v * a.sx[m]) * sw;
+                    const size_t o = (size_t)m * a.ldo + n;
+                    const float y = ((float)v * a.sx[m]) * sw;
+                    static_cast<float*>(a.out)[o] = a.res ? a.res[o] + y : y;
                 }
             }
 }

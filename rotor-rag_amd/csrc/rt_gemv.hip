@@ -110,7 +110,9 @@ __device__ __forceinline__ void emit(const GemvArgs& a, const GemvProb& P, int r
         static_cast<int*>(P.out)[(size_t)mg * P.ldo + n] = acc;
     } else {
         const float sw = P.rs ? P.rs[n] : P.s_w;
-        static_cast<float*>(P.out)[(size_t)mg * P.ldo + n] = ((float)acc * P.sx[mg]) * sw;
+        const size_t o = (size_t)mg * P.ldo + n;
+        const float y = ((float)acc * P.sx[mg]) * sw;
+        static_cast<float*>(P.out)[o] = P.res ? P.res[o] + y : y;
     }
 }
 

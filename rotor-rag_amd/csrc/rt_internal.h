@@ -48,6 +48,7 @@ struct GemvProb {
     float s_w;
     int N, C, ldo;
     int wg_begin;        // first global row block of this problem (prefix sum over problems)
+    const float* res;    // optional fp32 [M][ldo] added to y (may alias out)
 };
 
 struct GemvArgs {
@@ -69,7 +70,8 @@ struct GemvShape {
 //   kPermute  q = q_in[k] taken as is (no quantisation, s = 1)
 //   kRmsNorm  v = (x[k] / sqrt(mean_k x^2 + eps)) * norm_w[k], mean accumulated in f64
 //   kRelu2Mul v = x[k] > 0 ? (x[k] * x[k]) * u[k] : 0        (x = gate, u = up)
-enum QuantMode { kQuant = 0, kPermute = 1, kRmsNorm = 2, kRelu2Mul = 3 };
+//   kRelu2MulNorm  v = RMSNorm(relu2mul(x, u)) * norm_w       (norm_w = aux2)
+enum QuantMode { kQuant = 0, kPermute = 1, kRmsNorm = 2, kRelu2Mul = 3, kRelu2MulNorm = 4 };
 
 struct QuantProb {
     const float* x;      // fp32 [M][K] (gate in kRelu2Mul)
@@ -82,6 +84,7 @@ struct QuantProb {
     const float* aux;    // norm_w [K] (kRmsNorm) or up [M][K] (kRelu2Mul)
     float eps;
     float* v_out;        // optional fp32 [M][K]: the values that were quantised
+    const float* aux2;   // norm_w [K] (kRelu2MulNorm)
 };
 
 struct QuantArgs {
@@ -99,6 +102,7 @@ struct GemmArgs {
     void* out;           // float y[M][ldo] or int32 acc[M][ldo]
     float s_w;
     int M, N, Np, C, ldo, out_i32;
+    const float* res;    // optional fp32 [M][ldo] added to y (may alias out)
 };
 
 constexpr int kGemvMaxM = 8;  // up to this many tokens: VALU GEMV; beyond: MFMA GEMM
@@ -113,6 +117,16 @@ hipError_t launch_unpermute(const int8_t* qx, int M, int K, int Kp, int8_t* q, h
 // mt = tokens per workgroup (1, 2, 4 or 8).
 hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+
+// model kernels (rt_model.hip)
+hipError_t launch_embed(const uint16_t* E, const int* ids, int M, int V, int D, float* h, hipStream_t s);
+hipError_t launch_rope_append(float* q, float* k, const float* v, float* Kc, float* Vc, const float* rope, int M,
+                              int H, int Hkv, int hd, int Lmax, const int* pos, hipStream_t s);
+hipError_t launch_attention(const float* q, const float* Kc, const float* Vc, float* out, int M, int H, int Hkv,
+                            int hd, int Lmax, const int* pos, float scale, hipStream_t s);
+hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w, float eps, int V, int D,
+                          float* logits, unsigned long long* best, int* token, int* pos, int advance,
+                          int* next_ids, int* out_tokens, int pos_base, int out_cap, hipStream_t s);
 
 // Host policy: tokens per workgroup for M tokens.
 inline int gemv_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }

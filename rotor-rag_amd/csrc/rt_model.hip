@@ -1,0 +1,234 @@
+// Device kernels around the ternary linears for BitNet-2B-shape inference:
+// embedding gather, RoPE + KV-cache append, causal GQA attention over the cache,
+// bf16 LM head (fused final RMSNorm) with greedy argmax.
+//
+// Callers in the reference: BitNetModel.forward (src/rotor/bitnet_model.py:190-244:
+// embedding :220, blocks :224-228, final norm :231, tied LM head :235),
+// MultiHeadAttention.forward (src/rotor/transformer.py:206-292: KV concat :250-252,
+// GQA repeat :260-263, scores/softmax/AV :267-281) and GreedySampling
+// (src/rotor/generation.py:28-42).  This build's model adds RoPE and a causal mask (the
+// benchmark configuration); the reference has neither.
+//
+// Floating-point contraction is off in this file so that a*b+c rounds twice, as the
+// NumPy model of the tests computes it.
+#include "rt_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace rt {
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((unsigned)b << 16); }
+
+// h[m][:] = E[ids[m]][:] (bf16 -> fp32)
+__global__ void __launch_bounds__(256) embed_kernel(const uint16_t* __restrict__ E, const int* __restrict__ ids, int V,
+                                                    int D, float* __restrict__ h) {
+    const int m = blockIdx.x;
+    int id = ids[m];
+    if (id < 0 || id >= V) id = 0;  // the host validates ids; never read out of range
+    const uint16_t* row = E + (size_t)id * D;
+    for (int k = threadIdx.x; k < D; k += blockDim.x) h[(size_t)m * D + k] = bf16_to_f32(row[k]);
+}
+
+// RoPE (rotate-half convention) on q [M][H*hd] and k [M][Hkv*hd] in place for positions
+// *pos_p + m, then k -> Kc [Hkv][hd][Lmax] (dimension-major), v -> Vc [Hkv][Lmax][hd].
+// rope: [Lmax][hd/2][2] = (cos, sin) of position * theta_i.
+__global__ void __launch_bounds__(256) rope_append_kernel(float* __restrict__ q, float* __restrict__ k,
+                                                          const float* __restrict__ v, float* __restrict__ Kc,
+                                                          float* __restrict__ Vc, const float* __restrict__ rope,
+                                                          int H, int Hkv, int hd, int Lmax,
+                                                          const int* __restrict__ pos_p) {
+    const int m = blockIdx.x, pos = *pos_p + m, half = hd / 2;
+    const float* cs = rope + (size_t)pos * half * 2;
+    for (int idx = threadIdx.x; idx < (H + Hkv) * half; idx += blockDim.x) {
+        const int head = idx / half, i = idx % half;
+        float* base = head < H ? q + (size_t)m * H * hd + (size_t)head * hd
+                               : k + (size_t)m * Hkv * hd + (size_t)(head - H) * hd;
+        const float c = cs[2 * i], s = cs[2 * i + 1];
+        const float x1 = base[i], x2 = base[i + half];
+        base[i] = x1 * c - x2 * s;
+        base[i + half] = x2 * c + x1 * s;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < Hkv * hd; idx += blockDim.x) {
+        const int kh = idx / hd, d = idx % hd;
+        Kc[((size_t)kh * hd + d) * Lmax + pos] = k[(size_t)m * Hkv * hd + idx];
+        Vc[((size_t)kh * Lmax + pos) * hd + d] = v[(size_t)m * Hkv * hd + idx];
+    }
+}
+
+// out[m][h*hd + d] = sum_j softmax_j(q.K_j * scale) V_j[d] over keys j <= *pos_p + m.
+// One 256-thread workgroup per (head, query); scores live in LDS (Lmax floats).
+__global__ void __launch_bounds__(256) attention_kernel(const float* __restrict__ q, const float* __restrict__ Kc,
+                                                        const float* __restrict__ Vc, float* __restrict__ out, int H,
+                                                        int Hkv, int hd, int Lmax, const int* __restrict__ pos_p,
+                                                        float scale) {
+    extern __shared__ float smem[];  // [hd] q, [Lmax] scores, [256] reduction
+    float* qs = smem;
+    float* sc = smem + hd;
+    float* red = sc + Lmax;
+    const int h = blockIdx.x, m = blockIdx.y, t = threadIdx.x;
+    const int kh = h / (H / Hkv), L = *pos_p + m + 1;
+    for (int d = t; d < hd; d += 256) qs[d] = q[(size_t)m * H * hd + (size_t)h * hd + d];
+    __syncthreads();
+    const float* K = Kc + (size_t)kh * hd * Lmax;
+    float mx = -INFINITY;
+    for (int j = t; j < L; j += 256) {
+        float dot = 0.0f;
+        for (int d = 0; d < hd; ++d) dot += qs[d] * K[(size_t)d * Lmax + j];
+        const float s = dot * scale;
+        sc[j] = s;
+        mx = fmaxf(mx, s);
+    }
+    red[t] = mx;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (t < w) red[t] = fmaxf(red[t], red[t + w]);
+        __syncthreads();
+    }
+    mx = red[0];
+    __syncthreads();
+    float z = 0.0f;
+    for (int j = t; j < L; j += 256) {
+        const float p = expf(sc[j] - mx);
+        sc[j] = p;
+        z += p;
+    }
+    red[t] = z;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (t < w) red[t] += red[t + w];
+        __syncthreads();
+    }
+    z = red[0];
+    __syncthreads();
+    // two halves of the workgroup take alternate keys, then combine
+    const float* V = Vc + (size_t)kh * Lmax * hd;
+    const int groups = 256 / hd;  // hd divides 256 (checked on the host)
+    const int d = t % hd, gsub = t / hd;
+    float acc = 0.0f;
+    for (int j = gsub; j < L; j += groups) acc += sc[j] * V[(size_t)j * hd + d];
+    red[t] = acc;
+    __syncthreads();
+    if (gsub == 0) {
+        for (int g = 1; g < groups; ++g) acc += red[g * hd + d];
+        out[(size_t)m * H * hd + (size_t)h * hd + d] = acc / z;
+    }
+}
+
+// Final RMSNorm (f64 mean of squares, as the quantiser's) fused into the tied bf16 LM
+// head: logits[r] = sum_k E[r][k] * xn[k]; the greedy token is the first index of the
+// largest logit, accumulated as a 64-bit key (ordered value << 32 | ~index) with an
+// atomic max.  Each wave owns `rows_per_wave` consecutive rows; lane l owns elements
+// [512 s + 8 l, 512 s + 8 l + 8) of every row (D a multiple of 512).
+__device__ __forceinline__ unsigned long long argmax_key(float v, unsigned idx) {
+    unsigned b = __float_as_uint(v);
+    b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((unsigned long long)b << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+
+template <int SLICES>
+__global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict__ E, const float* __restrict__ x,
+                                                      const float* __restrict__ norm_w, float eps, int V,
+                                                      int rows_per_wave, float* __restrict__ logits,
+                                                      unsigned long long* __restrict__ best) {
+    constexpr int D = SLICES * 512;
+    __shared__ double redd[4];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // RMSNorm statistics of x over D (every workgroup recomputes them)
+    double ss = 0.0;
+    for (int k = t; k < D; k += 256) ss += (double)x[k] * (double)x[k];
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    if (lane == 0) redd[wave] = ss;
+    __syncthreads();
+    ss = (redd[0] + redd[1]) + (redd[2] + redd[3]);
+    const float norm = sqrtf((float)(ss / (double)D) + eps);
+    float xn[SLICES][8];
+#pragma unroll
+    for (int s = 0; s < SLICES; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int k = s * 512 + lane * 8 + e;
+            xn[s][e] = (x[k] / norm) * norm_w[k];
+        }
+    const int r0 = (blockIdx.x * 4 + wave) * rows_per_wave;
+    unsigned long long key = 0ull;
+    for (int r = r0; r < r0 + rows_per_wave && r < V; ++r) {
+        const v4u* row = reinterpret_cast<const v4u*>(E + (size_t)r * D);
+        float acc = 0.0f;
+#pragma unroll
+        for (int s = 0; s < SLICES; ++s) {
+            const v4u w = __builtin_nontemporal_load(row + s * 64 + lane);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc += __uint_as_float(w[e] << 16) * xn[s][2 * e];
+                acc += __uint_as_float(w[e] & 0xFFFF0000u) * xn[s][2 * e + 1];
+            }
+        }
+        for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        if (lane == 0) {
+            logits[r] = acc;
+            const unsigned long long kk = argmax_key(acc, (unsigned)r);
+            key = kk > key ? kk : key;
+        }
+    }
+    if (lane == 0 && key) atomicMax(best, key);
+}
+
+// token = argmax; optionally also written to next_ids[0] (the next step's input) and,
+// with p = *pos_p + advance, to out_tokens[p - 1 - pos_base]; then *pos_p = p.
+__global__ void argmax_finalize_kernel(unsigned long long* best, int* token, int* pos_p, int advance, int* next_ids,
+                                       int* out_tokens, int pos_base, int out_cap) {
+    const unsigned long long k = *best;
+    const int tok = (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull));
+    *token = tok;
+    *best = 0ull;  // ready for the next step
+    if (next_ids) next_ids[0] = tok;
+    if (pos_p) {
+        const int p = *pos_p + advance;
+        const int i = p - 1 - pos_base;
+        if (out_tokens && i >= 0 && i < out_cap) out_tokens[i] = tok;
+        *pos_p = p;
+    }
+}
+
+hipError_t launch_embed(const uint16_t* E, const int* ids, int M, int V, int D, float* h, hipStream_t s) {
+    hipLaunchKernelGGL(embed_kernel, dim3((unsigned)M), dim3(256), 0, s, E, ids, V, D, h);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_append(float* q, float* k, const float* v, float* Kc, float* Vc, const float* rope, int M,
+                              int H, int Hkv, int hd, int Lmax, const int* pos, hipStream_t s) {
+    hipLaunchKernelGGL(rope_append_kernel, dim3((unsigned)M), dim3(256), 0, s, q, k, v, Kc, Vc, rope, H, Hkv, hd,
+                       Lmax, pos);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const float* q, const float* Kc, const float* Vc, float* out, int M, int H, int Hkv,
+                            int hd, int Lmax, const int* pos, float scale, hipStream_t s) {
+    const size_t lds = (size_t)(hd + Lmax + 256) * sizeof(float);
+    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)H, (unsigned)M), dim3(256), lds, s, q, Kc, Vc, out, H, Hkv,
+                       hd, Lmax, pos, scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w, float eps, int V, int D,
+                          float* logits, unsigned long long* best, int* token, int* pos, int advance,
+                          int* next_ids, int* out_tokens, int pos_base, int out_cap, hipStream_t s) {
+    const int rpw = 16;
+    const unsigned blocks = (unsigned)((V + 4 * rpw - 1) / (4 * rpw));
+    switch (D / 512) {
+        case 1: hipLaunchKernelGGL(lm_head_kernel<1>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;
+        case 2: hipLaunchKernelGGL(lm_head_kernel<2>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;
+        case 4: hipLaunchKernelGGL(lm_head_kernel<4>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;
+        case 5: hipLaunchKernelGGL(lm_head_kernel<5>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;
+        case 8: hipLaunchKernelGGL(lm_head_kernel<8>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;
+        default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(1), 0, s, best, token, pos, advance, next_ids,
+                       out_tokens, pos_base, out_cap);
+    return hipGetLastError();
+}
+
+}  // namespace rt

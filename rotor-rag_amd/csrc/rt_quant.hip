@@ -10,7 +10,8 @@
 // RMSNorm: src/rotor/transformer.py:24-36 (x / sqrt(mean(x^2) + eps) * w); the mean of
 // squares is accumulated in f64 and rounded once to f32, so its value does not depend
 // on the summation order (the reference's fp32 pairwise mean agrees to ~1 ulp).
-// relu^2(gate) * up: the FFN activation of the benchmark configuration.
+// relu^2(gate) * up: the FFN activation of the benchmark configuration, optionally
+// followed by the FFN sub-norm (BitNet's ffn_sub_norm, src/rotor/transformer.py:336-337).
 //
 // One 256-thread workgroup per token row.  Each thread holds groups of 16 elements in
 // registers (rows up to 16384 elements; longer rows recompute from memory), reduces
@@ -76,7 +77,7 @@ __device__ __forceinline__ void load_group(const float* __restrict__ xr, int g, 
 __device__ __forceinline__ void source_group(const QuantProb& P, const float* xr, const float* ur, int g, bool vec,
                                              float (&v)[16]) {
     load_group(xr, g, P.K, vec, v);
-    if (P.mode == kRelu2Mul) {
+    if (P.mode == kRelu2Mul || P.mode == kRelu2MulNorm) {
         float u[16];
         load_group(ur, g, P.K, vec, u);
 #pragma unroll
@@ -84,10 +85,13 @@ __device__ __forceinline__ void source_group(const QuantProb& P, const float* xr
     }
 }
 
-// kRmsNorm: h = (x / norm) * w for group g
+__device__ __forceinline__ bool has_norm(const QuantProb& P) { return P.mode == kRmsNorm || P.mode == kRelu2MulNorm; }
+__device__ __forceinline__ const float* norm_weight(const QuantProb& P) { return P.mode == kRmsNorm ? P.aux : P.aux2; }
+
+// kRmsNorm / kRelu2MulNorm: h = (v / norm) * w for group g
 __device__ __forceinline__ void rmsnorm_group(const QuantProb& P, float norm, int g, bool vec, float (&v)[16]) {
     float w[16];
-    load_group(P.aux, g, P.K, vec, w);
+    load_group(norm_weight(P), g, P.K, vec, w);
 #pragma unroll
     for (int e = 0; e < 16; ++e) v[e] = (v[e] / norm) * w[e];
 }
@@ -156,12 +160,12 @@ __global__ void __launch_bounds__(256) quant_kernel(QuantArgs a) {
         return;
     }
     const float* xr = P.x + (size_t)m * K;
-    const float* ur = P.mode == kRelu2Mul ? P.aux + (size_t)m * K : nullptr;
+    const float* ur = (P.mode == kRelu2Mul || P.mode == kRelu2MulNorm) ? P.aux + (size_t)m * K : nullptr;
     int8_t* qn = P.q_nat ? P.q_nat + (size_t)m * K : nullptr;
     float* vo = P.v_out ? P.v_out + (size_t)m * K : nullptr;
     bool vec = (K & 15) == 0 && ((uintptr_t)xr & 15u) == 0;
     if (ur) vec = vec && ((uintptr_t)ur & 15u) == 0;
-    if (P.mode == kRmsNorm) vec = vec && ((uintptr_t)P.aux & 15u) == 0;
+    if (has_norm(P)) vec = vec && ((uintptr_t)norm_weight(P) & 15u) == 0;
     auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
     auto dadd_op = [](double x, double y) { return x + y; };
 
@@ -169,7 +173,7 @@ __global__ void __launch_bounds__(256) quant_kernel(QuantArgs a) {
         float v[kRegGroups][16];
 #pragma unroll
         for (int r = 0; r < kRegGroups; ++r) source_group(P, xr, ur, threadIdx.x + r * 256, vec, v[r]);
-        if (P.mode == kRmsNorm) {
+        if (has_norm(P)) {
             double ss = 0.0;
 #pragma unroll
             for (int r = 0; r < kRegGroups; ++r) ss = sumsq_group(v[r], ss);
@@ -193,7 +197,7 @@ __global__ void __launch_bounds__(256) quant_kernel(QuantArgs a) {
     }
     // long rows: recompute the source values on every pass
     float norm = 1.0f;
-    if (P.mode == kRmsNorm) {
+    if (has_norm(P)) {
         double ss = 0.0;
         for (int g = threadIdx.x; g < groups; g += blockDim.x) {
             float v[16];
@@ -207,7 +211,7 @@ __global__ void __launch_bounds__(256) quant_kernel(QuantArgs a) {
     for (int g = threadIdx.x; g < groups; g += blockDim.x) {
         float v[16];
         source_group(P, xr, ur, g, vec, v);
-        if (P.mode == kRmsNorm) rmsnorm_group(P, norm, g, vec, v);
+        if (has_norm(P)) rmsnorm_group(P, norm, g, vec, v);
         amax = amax_group(v, amax);
     }
     amax = block_reduce_256(amax, redf, fmax_op);
@@ -215,7 +219,7 @@ __global__ void __launch_bounds__(256) quant_kernel(QuantArgs a) {
     for (int g = threadIdx.x; g < groups; g += blockDim.x) {
         float v[16];
         source_group(P, xr, ur, g, vec, v);
-        if (P.mode == kRmsNorm) rmsnorm_group(P, norm, g, vec, v);
+        if (has_norm(P)) rmsnorm_group(P, norm, g, vec, v);
         emit_group(v, s, g, K, qrow, qn, vo);
     }
     if (threadIdx.x == 0 && P.sx) P.sx[m] = s;

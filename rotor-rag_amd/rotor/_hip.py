@@ -48,10 +48,15 @@ SIGNATURES = {
     "rt_act_quantize": (_I, [_P, _P, _I, _P]),
     "rt_act_rmsnorm_quantize": (_I, [_P, _P, _P, _F, _I, _P, _P]),
     "rt_act_relu2_mul_quantize": (_I, [_P, _P, _P, _I, _P, _P]),
+    "rt_act_relu2_mul_norm_quantize": (_I, [_P, _P, _P, _P, _F, _I, _P, _P]),
     "rt_act_export": (_I, [_P, _P, _P, _P]),
-    "rt_linear_act_f32": (_I, [_P, _P, _P, _P]),
+    "rt_linear_act_f32": (_I, [_P, _P, _P, _P, _P]),
     "rt_plan_create_act": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, ctypes.POINTER(_P),
                                 ctypes.POINTER(_P)]),
+    "rt_embed": (_I, [_P, _P, _I, _I, _P, _I, _P]),
+    "rt_rope_kv_append": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "rt_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "rt_lm_head_argmax": (_I, [_P, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I]),
 }
 
 _lib = None

@@ -1,0 +1,343 @@
+"""BitNet-b1.58-2B-shape language model on MI355X, with the reference's loading and
+forward surface (src/rotor/bitnet_model.py):
+
+    model = load_bitnet_model(model_dir, use_gpu=True)          # :349
+    logits, cache = model.forward(ids, past_kv_cache=cache, use_cache=True)   # :190
+    tokens = model.generate_greedy(prompt_ids, max_new_tokens)
+
+Checkpoint: ``model_dir/config.json`` (HF keys vocab_size, hidden_size,
+num_hidden_layers, num_attention_heads, num_key_value_heads, intermediate_size; optional
+rope_theta, rms_norm_eps, max_position_embeddings) and ``model_dir/model.safetensors`` with
+the tensor names the reference reads (src/rotor/bitnet_model.py:100-188): ternary weights
+as rotor/BitNet bytes ``[out, in/4]`` uint8 with a per-tensor ``weight_scale`` that
+multiplies (the reference's convention, :179-188), bf16/fp32 norms and a bf16 embedding
+tied to the LM head (:235).
+
+Layer semantics of this build (the benchmark configuration, BitNet b1.58 structure):
+    a = RMSNorm(x);  q, k, v = W2A8(a);  RoPE(q, k);  o = causal GQA attention
+    x = x + Wo(RMSNorm_sub(o))
+    f = RMSNorm(x);  x = x + Wd(RMSNorm_sub(relu(Wg f)^2 * Wu f))
+The reference differs (no RoPE, no mask, SiLU gate, sub-norm after o_proj; see its
+src/rotor/transformer.py:206-341); logits are therefore not comparable with it, only
+the per-linear arithmetic is.  Every ternary linear runs in the HIP library; attention,
+RoPE, norms and the LM head are HIP kernels of the same library.  The model runs on the
+GPU only: ``use_gpu=False`` raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+from pathlib import Path
+from typing import Dict, Optional
+
+import numpy as np
+
+from . import _hip
+
+TERNARY = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+
+
+def rope_table(max_len: int, head_dim: int, theta: float) -> np.ndarray:
+    """(cos, sin) of pos * theta^(-2i/head_dim), [max_len, head_dim/2, 2] fp32 (computed in f64)."""
+    i = np.arange(head_dim // 2, dtype=np.float64)
+    inv = theta ** (-(2.0 * i) / head_dim)
+    ang = np.arange(max_len, dtype=np.float64)[:, None] * inv[None, :]
+    return np.stack([np.cos(ang), np.sin(ang)], axis=-1).astype(np.float32)
+
+
+class KVCache:
+    """Handle to the device KV cache of a model: `length` tokens are cached."""
+
+    def __init__(self, model: "BitNetModel", length: int):
+        self.model = model
+        self.length = length
+
+    def __len__(self):
+        return self.length
+
+
+class BitNetModel:
+    def __init__(self, config: Dict, use_gpu: bool = False):
+        if not use_gpu:
+            raise NotImplementedError("this build runs BitNetModel on the GPU only: pass use_gpu=True")
+        self.config = dict(config)
+        self.vocab_size = config["vocab_size"]
+        self.d_model = config["d_model"]
+        self.n_layers = config["n_layers"]
+        self.n_heads = config.get("n_heads", 20)
+        self.n_kv_heads = config.get("n_kv_heads", 4)   # reference default, src/rotor/bitnet_model.py:60
+        self.d_ff = config.get("d_ff", 6912)
+        self.head_dim = self.d_model // self.n_heads
+        self.rope_theta = float(config.get("rope_theta", 500000.0))
+        self.eps = float(config.get("rms_norm_eps", 1e-6))
+        self.max_seq_len = int(config.get("max_seq_len", 2048))
+        self.max_tokens = int(config.get("max_batch_tokens", 512))
+        self.use_gpu = True
+        from .gpu_layers import get_gpu, last_error
+
+        self.gpu = get_gpu()
+        if self.gpu is None:
+            raise RuntimeError(f"BitNetModel(use_gpu=True): HIP backend unavailable: {last_error()}")
+        self._dev = None
+
+    # ------------------------------------------------------------------ loading
+    def load_weights_from_safetensors(self, model_path: str):
+        """Read the reference's tensor names (src/rotor/bitnet_model.py:92-188)."""
+        import torch
+        from safetensors import safe_open
+
+        state = {}
+        with safe_open(model_path, framework="pt") as f:
+            for k in f.keys():
+                state[k] = f.get_tensor(k)
+        self.load_state(state)
+
+    def load_state(self, state: Dict):
+        """state: name -> torch tensor / numpy array, with the reference's names."""
+        import torch
+
+        def t(name):
+            v = state[name]
+            return v if isinstance(v, torch.Tensor) else torch.from_numpy(np.asarray(v))
+
+        def f32(name):
+            return t(name).to(torch.float32).contiguous()
+
+        L = []
+        for i in range(self.n_layers):
+            p = f"model.layers.{i}"
+            lw = {"input_norm": f32(f"{p}.input_layernorm.weight"),
+                  "post_norm": f32(f"{p}.post_attention_layernorm.weight")}
+            for name in TERNARY:
+                grp = "self_attn" if name in ("q_proj", "k_proj", "v_proj", "o_proj") else "mlp"
+                w = t(f"{p}.{grp}.{name}.weight")
+                scale = float(t(f"{p}.{grp}.{name}.weight_scale").to(torch.float32).reshape(-1)[0])
+                lw[name] = (w.to(torch.uint8).cpu().numpy(), scale)
+            sub_a, sub_f = f"{p}.self_attn.attn_sub_norm.weight", f"{p}.mlp.ffn_sub_norm.weight"
+            lw["attn_sub_norm"] = f32(sub_a) if sub_a in state else None
+            lw["ffn_sub_norm"] = f32(sub_f) if sub_f in state else None
+            L.append(lw)
+        emb = t("model.embed_tokens.weight")
+        if emb.dtype != torch.bfloat16:
+            emb = emb.to(torch.bfloat16)
+        self._dev = _DeviceModel(self, L, emb.contiguous(), f32("model.norm.weight"))
+
+    # ------------------------------------------------------------------ inference
+    def forward(self, input_ids, return_logits: bool = True, past_kv_cache: Optional[KVCache] = None,
+                use_cache: bool = False):
+        """Same contract as src/rotor/bitnet_model.py:190-244: ids [seq] or [1, seq] ->
+        (logits [seq, vocab] (or [1, seq, vocab]), cache or None).  The KV cache stays on the
+        device; pass back the returned handle to continue a sequence."""
+        ids = np.asarray(input_ids)
+        squeeze = ids.ndim == 1
+        if ids.ndim == 2:
+            if ids.shape[0] != 1:
+                raise ValueError("batch size 1 only")
+            ids = ids[0]
+        start = past_kv_cache.length if past_kv_cache is not None else 0
+        out = self._dev.forward(ids.astype(np.int32), start, return_logits)
+        cache = KVCache(self, start + len(ids)) if use_cache else None
+        if not squeeze:
+            out = out[None]
+        return out, cache
+
+    def generate_greedy(self, prompt_ids, max_new_tokens: int, graph: bool = True) -> np.ndarray:
+        """Greedy decoding with the KV cache, the protocol of TextGenerator
+        (src/rotor/generation.py:244-279: the whole prompt first, then one token per step,
+        argmax sampling :42).  The decode step is captured once as a HIP graph and replayed."""
+        return self._dev.generate(np.asarray(prompt_ids, dtype=np.int32), int(max_new_tokens), graph)
+
+
+class _DeviceModel:
+    """Device-resident weights, KV cache and buffers, and the launch sequence."""
+
+    def __init__(self, model: BitNetModel, layers, emb, final_norm):
+        import torch
+
+        self.m = model
+        hip = self.hip = model.gpu
+        dev = self.device = hip.device
+        D, F, H, Hkv, hd = model.d_model, model.d_ff, model.n_heads, model.n_kv_heads, model.head_dim
+        self.D, self.F, self.H, self.Hkv, self.hd = D, F, H, Hkv, hd
+        self.Lmax = model.max_seq_len
+        if H * hd != D or H % Hkv:
+            raise ValueError("unsupported head layout")
+        self.layers = []
+        for lw in layers:
+            d = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in lw.items()
+                 if k in ("input_norm", "post_norm", "attn_sub_norm", "ffn_sub_norm")}
+            for name in TERNARY:
+                wb, scale = lw[name]
+                K = D if name != "down_proj" else F
+                if name == "o_proj":
+                    K = H * hd
+                d[name] = hip.upload(wb, K, scale)
+            d["kc"] = torch.zeros((Hkv, hd, self.Lmax), dtype=torch.float32, device=dev)
+            d["vc"] = torch.zeros((Hkv, self.Lmax, hd), dtype=torch.float32, device=dev)
+            self.layers.append(d)
+        self.emb = emb.to(dev)
+        self.final_norm = final_norm.to(dev)
+        self.rope = torch.from_numpy(rope_table(self.Lmax, hd, model.rope_theta)).to(dev)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.ids = torch.zeros(max(self.Lmax, 1), dtype=torch.int32, device=dev)
+        self.token = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.best = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.logits = torch.empty(model.vocab_size, dtype=torch.float32, device=dev)
+        self.out_tokens = torch.zeros(self.Lmax, dtype=torch.int32, device=dev)
+        cap = model.max_tokens
+        self.act_d = hip.activations(cap, D)
+        self.act_f = hip.activations(cap, F)
+        self.state = {}
+
+    def _state(self, M):
+        st = self.state.get(M)
+        if st is not None:
+            return st
+        import torch
+
+        dev, D, F, H, Hkv, hd = self.device, self.D, self.F, self.H, self.Hkv, self.hd
+        e = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)
+        st = {"h": e(M, D), "q": e(M, H * hd), "k": e(M, Hkv * hd), "v": e(M, Hkv * hd), "o": e(M, H * hd),
+              "g": e(M, F), "u": e(M, F)}
+        st["qkv"], st["gu"] = [], []
+        for L in self.layers:
+            st["qkv"].append(self.hip.plan_act([L["q_proj"], L["k_proj"], L["v_proj"]], [self.act_d] * 3, M,
+                                               [st["q"], st["k"], st["v"]]))
+            st["gu"].append(self.hip.plan_act([L["gate_proj"], L["up_proj"]], [self.act_d] * 2, M, [st["g"], st["u"]]))
+        self.state[M] = st
+        return st
+
+    def _enqueue(self, M, pos_base, out_cap):
+        """Forward of the M tokens in ids[0:M] at position *pos; LM head + argmax of the last."""
+        hip, lib, ctx = self.hip, _hip.load(), self.hip.ctx
+        st = self._state(M)
+        h, q, k, v, o, g, u = st["h"], st["q"], st["k"], st["v"], st["o"], st["g"], st["u"]
+        hip._bind_stream()
+        chk = _hip.check
+        chk(lib.rt_embed(ctx, self.emb.data_ptr(), self.m.vocab_size, self.D, self.ids.data_ptr(), M, h.data_ptr()),
+            "rt_embed")
+        eps = self.m.eps
+        for li, L in enumerate(self.layers):
+            hip.act_rmsnorm_quantize(h, L["input_norm"], self.act_d, eps)
+            st["qkv"][li].gemv()
+            chk(lib.rt_rope_kv_append(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
+                                      L["vc"].data_ptr(), self.rope.data_ptr(), M, self.H, self.Hkv, self.hd,
+                                      self.Lmax, self.pos.data_ptr()), "rt_rope_kv_append")
+            chk(lib.rt_attention(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), o.data_ptr(), M, self.H,
+                                 self.Hkv, self.hd, self.Lmax, self.pos.data_ptr()), "rt_attention")
+            if L["attn_sub_norm"] is not None:
+                hip.act_rmsnorm_quantize(o, L["attn_sub_norm"], self.act_d, eps)
+            else:
+                hip.act_quantize(o, self.act_d)
+            hip.linear_act(L["o_proj"], self.act_d, out=h, residual=h)
+            hip.act_rmsnorm_quantize(h, L["post_norm"], self.act_d, eps)
+            st["gu"][li].gemv()
+            if L["ffn_sub_norm"] is not None:
+                hip.act_relu2_mul_norm_quantize(g, u, L["ffn_sub_norm"], self.act_f, eps)
+            else:
+                hip.act_relu2_mul_quantize(g, u, self.act_f)
+            hip.linear_act(L["down_proj"], self.act_f, out=h, residual=h)
+        chk(lib.rt_lm_head_argmax(ctx, self.emb.data_ptr(), h[M - 1].data_ptr(), self.final_norm.data_ptr(), eps,
+                                  self.m.vocab_size, self.D, self.logits.data_ptr(), self.best.data_ptr(),
+                                  self.token.data_ptr(), self.pos.data_ptr(), M, self.ids.data_ptr(),
+                                  self.out_tokens.data_ptr(), pos_base, out_cap), "rt_lm_head_argmax")
+        return st
+
+    def _check_ids(self, ids, start):
+        if len(ids) == 0:
+            raise ValueError("empty input")
+        if start + len(ids) > self.Lmax:
+            raise ValueError(f"sequence of {start + len(ids)} tokens exceeds max_seq_len={self.Lmax}")
+        if len(ids) > self.m.max_tokens:
+            raise ValueError(f"{len(ids)} tokens in one forward exceed max_batch_tokens={self.m.max_tokens}")
+        if ids.min() < 0 or ids.max() >= self.m.vocab_size:
+            raise ValueError("token id out of range")
+
+    def forward(self, ids, start, return_logits):
+        import torch
+
+        self._check_ids(ids, start)
+        M = len(ids)
+        self.ids[:M].copy_(torch.from_numpy(ids))
+        self.pos.fill_(start)
+        st = self._enqueue(M, pos_base=1 << 30, out_cap=0)
+        h = st["h"]
+        if M == 1:
+            out = self.logits[None] if return_logits else self._final_norm(h)
+        else:
+            hn = self._final_norm(h)
+            out = self._lm_head_all(hn) if return_logits else hn
+        return out.cpu().numpy()
+
+    def _final_norm(self, h):
+        import torch
+
+        ss = (h.double() ** 2).sum(-1, keepdim=True)
+        norm = torch.sqrt((ss / h.shape[-1]).float() + self.m.eps)
+        return (h / norm) * self.final_norm
+
+    def _lm_head_all(self, hn, chunk=16384):
+        # every position's logits (reference semantics); the hot decode path uses the
+        # fused LM-head kernel for the last position only
+        import torch
+
+        out = torch.empty((hn.shape[0], self.m.vocab_size), dtype=torch.float32, device=self.device)
+        for v0 in range(0, self.m.vocab_size, chunk):
+            out[:, v0:v0 + chunk] = hn @ self.emb[v0:v0 + chunk].float().T
+        return out
+
+    def generate(self, prompt, n, graph):
+        import torch
+
+        self._check_ids(prompt, 0)
+        P = len(prompt)
+        if P + n > self.Lmax:
+            raise ValueError("prompt + new tokens exceed max_seq_len")
+        self.ids[:P].copy_(torch.from_numpy(prompt))
+        self.pos.fill_(0)
+        self.best.zero_()
+        self._enqueue(P, pos_base=P - 1, out_cap=n)            # prefill; out_tokens[0]
+        if n > 1:
+            if graph:
+                self._state(1)
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                saved_pos = self.pos.clone()
+                saved_ids = self.ids[:1].clone()
+                with torch.cuda.graph(g):
+                    self._enqueue(1, pos_base=P - 1, out_cap=n)
+                # capture does not execute; restore in case it touched nothing anyway
+                self.pos.copy_(saved_pos)
+                self.ids[:1].copy_(saved_ids)
+                for _ in range(n - 1):
+                    g.replay()
+            else:
+                for _ in range(n - 1):
+                    self._enqueue(1, pos_base=P - 1, out_cap=n)
+        torch.cuda.synchronize()
+        return self.out_tokens[:n].cpu().numpy().copy()
+
+
+def config_from_hf(cfg: Dict) -> Dict:
+    """HF config.json -> the model config dict (src/rotor/bitnet_model.py:368-375)."""
+    return {
+        "vocab_size": cfg["vocab_size"],
+        "d_model": cfg["hidden_size"],
+        "n_layers": cfg["num_hidden_layers"],
+        "n_heads": cfg["num_attention_heads"],
+        "n_kv_heads": cfg.get("num_key_value_heads", cfg["num_attention_heads"]),
+        "d_ff": cfg["intermediate_size"],
+        "rope_theta": cfg.get("rope_theta", 500000.0),
+        "rms_norm_eps": cfg.get("rms_norm_eps", 1e-6),
+        "max_seq_len": cfg.get("max_position_embeddings", 2048),
+    }
+
+
+def load_bitnet_model(model_dir: str, use_gpu: bool = False) -> BitNetModel:
+    """src/rotor/bitnet_model.py:349-394: config.json + model.safetensors -> BitNetModel."""
+    model_dir = Path(model_dir)
+    with open(model_dir / "config.json") as f:
+        cfg = json.load(f)
+    model = BitNetModel(config_from_hf(cfg), use_gpu=use_gpu)
+    model.load_weights_from_safetensors(str(model_dir / "model.safetensors"))
+    return model

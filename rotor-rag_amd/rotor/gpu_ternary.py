@@ -332,15 +332,33 @@ class HIPTernaryOps:
         act.tokens = g.shape[0]
         return act
 
-    def linear_act(self, w: DeviceTernaryWeights, act: DeviceActivations, out=None):
-        """y [M, N] fp32 = W2A8 linear of the activations held."""
+    def act_relu2_mul_norm_quantize(self, gate, up, norm_w, act: DeviceActivations, eps: float = 1e-6, a_out=None):
+        """act <- int8 of RMSNorm(relu(gate)^2 * up) * norm_w (fused)."""
+        torch = _torch()
+        g = self._dev(gate, torch.float32)
+        u = self._dev(up, torch.float32)
+        wt = self._dev(norm_w, torch.float32).reshape(-1)
+        self._check_rows(g, act, "gate")
+        if u.shape != g.shape or wt.numel() != act.in_features:
+            raise ValueError("gate, up and norm weight shapes do not match")
+        self._bind_stream()
+        _hip.check(self.lib.rt_act_relu2_mul_norm_quantize(self.ctx, g.data_ptr(), u.data_ptr(), wt.data_ptr(),
+                                                           float(eps), g.shape[0], act.handle,
+                                                           a_out.data_ptr() if a_out is not None else None),
+                   "rt_act_relu2_mul_norm_quantize")
+        act.tokens = g.shape[0]
+        return act
+
+    def linear_act(self, w: DeviceTernaryWeights, act: DeviceActivations, out=None, residual=None):
+        """y [M, N] fp32 = W2A8 linear of the activations held (+ residual [M, N])."""
         torch = _torch()
         if act.in_features != w.in_features:
             raise ValueError("activations and weights disagree on in_features")
         y = out if out is not None else torch.empty((act.tokens, w.out_features), dtype=torch.float32,
                                                     device=self.device)
         self._bind_stream()
-        _hip.check(self.lib.rt_linear_act_f32(self.ctx, w.handle, act.handle, y.data_ptr()), "rt_linear_act_f32")
+        res = residual.data_ptr() if residual is not None else None
+        _hip.check(self.lib.rt_linear_act_f32(self.ctx, w.handle, act.handle, res, y.data_ptr()), "rt_linear_act_f32")
         return y
 
     def plan_act(self, weights, acts, M: int, ys) -> LinearPlan:

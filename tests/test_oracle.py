@@ -302,3 +302,54 @@ def test_ffn_block_w2a8_composes_pinned_parts():
     # and agrees with the reference-formula chain within the quantisation error
     y_ref, _ = O.ffn_block(x, nw, Wg, sg, Wu, su, Wd, sd)
     assert np.abs(y - y_ref).max() < 0.05 * max(1.0, np.abs(y_ref).max())
+
+
+def test_bf16_roundtrip_and_rounding():
+    x = np.array([1.0, -2.5, 3.1415927, 1e-3, 65504.0], np.float32)
+    b = O.f32_to_bf16(x)
+    y = O.bf16_to_f32(b)
+    assert np.abs(y - x).max() <= np.abs(x).max() * 2 ** -8
+    assert np.array_equal(O.f32_to_bf16(y), b)  # bf16 values are fixed points
+    # round half to even on the 16 dropped bits
+    assert O.f32_to_bf16(np.array([np.uint32(0x3F808000)], np.uint32).view(np.float32))[0] == 0x3F80
+    assert O.f32_to_bf16(np.array([np.uint32(0x3F818000)], np.uint32).view(np.float32))[0] == 0x3F82
+
+
+def test_rope_properties():
+    tab = O.rope_table(16, 8, 10000.0)
+    x = np.random.default_rng(0).standard_normal((3, 2, 8)).astype(np.float32)
+    assert np.array_equal(O.apply_rope(x, tab, 0)[0], x[0])  # position 0 is the identity
+    r = O.apply_rope(x, tab, 5)
+    assert np.allclose(np.linalg.norm(r, axis=-1), np.linalg.norm(x, axis=-1), rtol=1e-5)  # rotation
+    # relative-position property: <rope(q, p), rope(k, p')> depends on p - p' only
+    q, k = x[:1, :1], x[1:2, :1]
+    a = (O.apply_rope(q, tab, 7) * O.apply_rope(k, tab, 4)).sum()
+    b = (O.apply_rope(q, tab, 10) * O.apply_rope(k, tab, 7)).sum()
+    assert abs(a - b) < 1e-4
+
+
+def test_attention_closed_forms():
+    rng = np.random.default_rng(1)
+    hd = 8
+    q = rng.standard_normal((2, 4, hd)).astype(np.float32)
+    K = rng.standard_normal((2, 2, hd)).astype(np.float32)
+    V = rng.standard_normal((2, 2, hd)).astype(np.float32)
+    out = O.causal_gqa_attention(q, K, V, 0)
+    # query 0 sees only key 0: output = V[kv head][0]; GQA maps heads 0,1 -> kv 0, 2,3 -> kv 1
+    assert np.allclose(out[0, 0], V[0, 0]) and np.allclose(out[0, 3], V[1, 0])
+    # equal keys -> uniform weights -> mean of the visible values
+    Ke = np.repeat(K[:, :1], 2, axis=1)
+    out2 = O.causal_gqa_attention(q, Ke, V, 0)
+    assert np.allclose(out2[1, 0], V[0, :2].mean(0), atol=1e-6)
+
+
+def test_bitnet_incremental_equals_full():
+    cfg = dict(vocab_size=50, d_model=32, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=48)
+    p = O.make_bitnet_params(3, cfg, 16)
+    ids = [3, 17, 42, 5]
+    full_cache, inc_cache = {}, {}
+    h_full, _ = O.bitnet_forward(p, cfg, ids, full_cache)
+    h_a, _ = O.bitnet_forward(p, cfg, ids[:3], inc_cache)
+    h_b, logits = O.bitnet_forward(p, cfg, ids[3:], inc_cache)
+    assert np.allclose(h_full[:3], h_a, atol=1e-5) and np.allclose(h_full[3], h_b[0], atol=1e-5)
+    assert full_cache["len"] == inc_cache["len"] == 4

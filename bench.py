@@ -207,6 +207,60 @@ def ffn_block_cfg1(torch, hip, gen, dev, reps=200):
                                    "when replayed on one block)"}
 
 
+def decode_cfg4(torch, hip, gen, dev, n_layers=30, prompt_len=512, new_tokens=128):
+    """cfg 4: 30-layer BitNet-2B-shape random-init model (hidden 2560, ffn 6912, 20/5 heads
+    x 128, RoPE, RMSNorm, bf16 tied embedding/LM head over 128256 tokens), 512 random
+    prompt ids, greedy decode of 128 tokens with the KV cache, batch 1."""
+    import numpy as np
+
+    from rotor import gpu_layers
+    from rotor.bitnet_model import BitNetModel
+
+    D, F, H, Hkv, V = 2560, 6912, 20, 5, 128256
+    cfg = dict(vocab_size=V, d_model=D, n_layers=n_layers, n_heads=H, n_kv_heads=Hkv, d_ff=F,
+               rope_theta=500000.0, rms_norm_eps=1e-6, max_seq_len=prompt_len + new_tokens, max_batch_tokens=prompt_len)
+    state = {"model.embed_tokens.weight": torch.randn((V, D), generator=gen, device=dev).to(torch.bfloat16),
+             "model.norm.weight": torch.rand(D, generator=gen, device=dev) + 0.5}
+    shapes = {"q_proj": (D, D), "k_proj": (Hkv * 128, D), "v_proj": (Hkv * 128, D), "o_proj": (D, D),
+              "gate_proj": (F, D), "up_proj": (F, D), "down_proj": (D, F)}
+    for i in range(n_layers):
+        p = f"model.layers.{i}"
+        state[f"{p}.input_layernorm.weight"] = torch.rand(D, generator=gen, device=dev) + 0.5
+        state[f"{p}.post_attention_layernorm.weight"] = torch.rand(D, generator=gen, device=dev) + 0.5
+        state[f"{p}.self_attn.attn_sub_norm.weight"] = torch.rand(D, generator=gen, device=dev) + 0.5
+        state[f"{p}.mlp.ffn_sub_norm.weight"] = torch.rand(F, generator=gen, device=dev) + 0.5
+        for name, (n, k) in shapes.items():
+            grp = "self_attn" if name in ("q_proj", "k_proj", "v_proj", "o_proj") else "mlp"
+            state[f"{p}.{grp}.{name}.weight"] = make_weights_device(torch, gen, n, k, dev)
+            state[f"{p}.{grp}.{name}.weight_scale"] = torch.rand(1, generator=gen, device=dev) * 0.04 + 0.01
+    gpu_layers._gpu_instance = hip
+    try:
+        model = BitNetModel(cfg, use_gpu=True)
+        model.load_state(state)
+    finally:
+        gpu_layers._gpu_instance = None
+    del state
+    prompt = np.random.default_rng(4).integers(0, V, prompt_len).astype(np.int32)
+    model.generate_greedy(prompt, 8)  # warm-up (kernels, plans, graph)
+    t = {}
+    toks = model.generate_greedy(prompt, new_tokens, timings=t)
+    decode_tok_s = (new_tokens - 1) / (t["decode_ms"] * 1e-3)
+    ternary_bytes = n_layers * sum(n * k // 4 for n, k in shapes.values())
+    per_tok_bytes = ternary_bytes + V * D * 2
+    return {
+        "prefill_ms": round(t["prefill_ms"], 3),
+        "prefill_tok_s": round(prompt_len / (t["prefill_ms"] * 1e-3), 1),
+        "decode_ms_per_token": round(t["decode_ms"] / (new_tokens - 1), 4),
+        "decode_tok_s": round(decode_tok_s, 1),
+        "decode_weight_GB_per_s": round(per_tok_bytes * decode_tok_s / 1e9, 1),
+        "prompt": prompt_len, "new_tokens": new_tokens, "layers": n_layers,
+        "first_tokens": [int(x) for x in toks[:8]],
+        "note": "random-init weights; decode step = one HIP graph replay (embedding, 30 x (norm+quant, qkv, "
+                "rope+kv, attention, sub-norm+quant, o+residual, norm+quant, gate/up, relu2+sub-norm+quant, "
+                "down+residual), fused final-norm LM head + argmax)",
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -215,6 +269,7 @@ def main():
     ap.add_argument("--groups", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill / M=64 layer measurements")
+    ap.add_argument("--no-model", action="store_true", help="skip the cfg-4 decode measurement")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (reference point for HBM counters)")
     args = ap.parse_args()
@@ -297,6 +352,10 @@ def main():
     extra = prefill_and_layer(torch, hip, gen, dev) if not args.no_extra else None
     if extra is not None:
         extra["cfg1_ffn_block_m1"] = ffn_block_cfg1(torch, hip, gen, dev)
+    cfg4 = None
+    if not args.no_model:
+        print("bench: cfg-4 decode (30 layers, 512 prompt + 128 greedy tokens)", file=sys.stderr, flush=True)
+        cfg4 = decode_cfg4(torch, hip, gen, dev)
 
     # re-run the plan so ys[0] holds the plan's output for the parity check
     plan.run()
@@ -346,6 +405,7 @@ def main():
             "note": "one rt_linear_f32 (quantise + GEMV launch) per matrix, rotating over the G matrices",
         },
         "cfg3_prefill_and_cfg2_layer": extra,
+        "cfg4_decode": cfg4,
         "cpu_baseline": cpu,
         "parity_checked": parity,
         "wall_s": round(wall, 3),

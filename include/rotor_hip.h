@@ -182,6 +182,16 @@ int rt_rope_kv_append(rt_ctx* ctx, float* q, float* k, const float* v, float* k_
 int rt_attention(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, float* out, int M, int H,
                  int Hkv, int hd, int Lmax, const int* pos);
 
+/* Decode form of rt_attention for one query (M = 1): the keys are split over
+ * workgroups of 64 and the partial softmax sums are combined by the last workgroup of
+ * each head (flash-decoding).  workspace: device memory of at least
+ * rt_attention_decode_workspace(H, hd, Lmax) bytes, ZEROED before its first use and left
+ * reusable (its counters are reset by the kernel); calls sharing one workspace must not
+ * overlap.  head_dim 64 or 128. */
+size_t rt_attention_decode_workspace(int H, int hd, int Lmax);
+int rt_attention_decode(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, float* out, int H,
+                        int Hkv, int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes);
+
 /* Final RMSNorm of x fp32 [D] with norm_w, tied bf16 LM head logits [V]
  * (src/rotor/bitnet_model.py:231-235) and greedy argmax (src/rotor/generation.py:42;
  * first index of the maximum).  `best` (device u64, zero before first use) is left

@@ -685,6 +685,27 @@ int rt_attention(rt_ctx* ctx, const float* q, const float* k_cache, const float*
     return RT_OK;
 }
 
+size_t rt_attention_decode_workspace(int H, int hd, int Lmax) {
+    return (size_t)H * ((Lmax + 63) / 64) * (hd + 2) * sizeof(float) + (size_t)H * sizeof(int);
+}
+
+int rt_attention_decode(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, float* out, int H,
+                        int Hkv, int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes) {
+    if (!ctx || !q || !k_cache || !v_cache || !out || !pos || !workspace)
+        return fail(RT_EINVAL, "rt_attention_decode: NULL argument");
+    int rc = check_heads(H, Hkv, hd, Lmax, "rt_attention_decode");
+    if (rc) return rc;
+    if (hd != 64 && hd != 128) return fail(RT_EINVAL, "rt_attention_decode: head_dim must be 64 or 128");
+    const size_t need = rt_attention_decode_workspace(H, hd, Lmax);
+    if (workspace_bytes < need) return fail(RT_EINVAL, "rt_attention_decode: workspace too small");
+    float* work = static_cast<float*>(workspace);
+    int* counters = reinterpret_cast<int*>(static_cast<char*>(workspace) + need - (size_t)H * sizeof(int));
+    DeviceGuard g(ctx->device);
+    RT_HIP(launch_attn_decode(q, k_cache, v_cache, out, H, Hkv, hd, Lmax, pos, 1.0f / sqrtf((float)hd), work, counters,
+                              ctx->stream));
+    return RT_OK;
+}
+
 int rt_lm_head_argmax(rt_ctx* ctx, const uint16_t* emb, const float* x, const float* norm_w, float eps, int V, int D,
                       float* logits, unsigned long long* best, int* token, int* pos, int advance, int* next_ids,
                       int* out_tokens, int pos_base, int out_cap) {

@@ -124,6 +124,8 @@ hipError_t launch_rope_append(float* q, float* k, const float* v, float* Kc, flo
                               int H, int Hkv, int hd, int Lmax, const int* pos, hipStream_t s);
 hipError_t launch_attention(const float* q, const float* Kc, const float* Vc, float* out, int M, int H, int Hkv,
                             int hd, int Lmax, const int* pos, float scale, hipStream_t s);
+hipError_t launch_attn_decode(const float* q, const float* Kc, const float* Vc, float* out, int H, int Hkv, int hd,
+                              int Lmax, const int* pos, float scale, float* work, int* counters, hipStream_t s);
 hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w, float eps, int V, int D,
                           float* logits, unsigned long long* best, int* token, int* pos, int advance,
                           int* next_ids, int* out_tokens, int pos_base, int out_cap, hipStream_t s);

@@ -56,6 +56,8 @@ SIGNATURES = {
     "rt_embed": (_I, [_P, _P, _I, _I, _P, _I, _P]),
     "rt_rope_kv_append": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "rt_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "rt_attention_decode_workspace": (ctypes.c_size_t, [_I, _I, _I]),
+    "rt_attention_decode": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t]),
     "rt_lm_head_argmax": (_I, [_P, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I]),
 }
 

@@ -110,9 +110,9 @@ class BitNetModel:
                   "post_norm": f32(f"{p}.post_attention_layernorm.weight")}
             for name in TERNARY:
                 grp = "self_attn" if name in ("q_proj", "k_proj", "v_proj", "o_proj") else "mlp"
-                w = t(f"{p}.{grp}.{name}.weight")
+                w = t(f"{p}.{grp}.{name}.weight").to(torch.uint8)
                 scale = float(t(f"{p}.{grp}.{name}.weight_scale").to(torch.float32).reshape(-1)[0])
-                lw[name] = (w.to(torch.uint8).cpu().numpy(), scale)
+                lw[name] = (w if w.is_cuda else w.cpu().numpy(), scale)
             sub_a, sub_f = f"{p}.self_attn.attn_sub_norm.weight", f"{p}.mlp.ffn_sub_norm.weight"
             lw["attn_sub_norm"] = f32(sub_a) if sub_a in state else None
             lw["ffn_sub_norm"] = f32(sub_f) if sub_f in state else None
@@ -141,11 +141,13 @@ class BitNetModel:
             out = out[None]
         return out, cache
 
-    def generate_greedy(self, prompt_ids, max_new_tokens: int, graph: bool = True) -> np.ndarray:
+    def generate_greedy(self, prompt_ids, max_new_tokens: int, graph: bool = True, timings: Optional[dict] = None):
         """Greedy decoding with the KV cache, the protocol of TextGenerator
         (src/rotor/generation.py:244-279: the whole prompt first, then one token per step,
-        argmax sampling :42).  The decode step is captured once as a HIP graph and replayed."""
-        return self._dev.generate(np.asarray(prompt_ids, dtype=np.int32), int(max_new_tokens), graph)
+        argmax sampling :42).  The decode step is captured once as a HIP graph and replayed.
+        When `timings` is a dict it receives prefill_ms and decode_ms (HIP events; graph
+        capture excluded)."""
+        return self._dev.generate(np.asarray(prompt_ids, dtype=np.int32), int(max_new_tokens), graph, timings)
 
 
 class _DeviceModel:
@@ -171,7 +173,10 @@ class _DeviceModel:
                 K = D if name != "down_proj" else F
                 if name == "o_proj":
                     K = H * hd
-                d[name] = hip.upload(wb, K, scale)
+                if isinstance(wb, torch.Tensor) and wb.is_cuda:
+                    d[name] = hip.upload_device(wb, K, scale)
+                else:
+                    d[name] = hip.upload(np.asarray(wb), K, scale)
             d["kc"] = torch.zeros((Hkv, hd, self.Lmax), dtype=torch.float32, device=dev)
             d["vc"] = torch.zeros((Hkv, self.Lmax, hd), dtype=torch.float32, device=dev)
             self.layers.append(d)
@@ -184,6 +189,9 @@ class _DeviceModel:
         self.best = torch.zeros(1, dtype=torch.int64, device=dev)
         self.logits = torch.empty(model.vocab_size, dtype=torch.float32, device=dev)
         self.out_tokens = torch.zeros(self.Lmax, dtype=torch.int32, device=dev)
+        lib = _hip.load()
+        self.attn_ws_bytes = int(lib.rt_attention_decode_workspace(H, hd, self.Lmax))
+        self.attn_ws = torch.zeros(self.attn_ws_bytes, dtype=torch.uint8, device=dev)
         cap = model.max_tokens
         self.act_d = hip.activations(cap, D)
         self.act_f = hip.activations(cap, F)
@@ -223,8 +231,13 @@ class _DeviceModel:
             chk(lib.rt_rope_kv_append(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
                                       L["vc"].data_ptr(), self.rope.data_ptr(), M, self.H, self.Hkv, self.hd,
                                       self.Lmax, self.pos.data_ptr()), "rt_rope_kv_append")
-            chk(lib.rt_attention(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), o.data_ptr(), M, self.H,
-                                 self.Hkv, self.hd, self.Lmax, self.pos.data_ptr()), "rt_attention")
+            if M == 1:
+                chk(lib.rt_attention_decode(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), o.data_ptr(),
+                                            self.H, self.Hkv, self.hd, self.Lmax, self.pos.data_ptr(),
+                                            self.attn_ws.data_ptr(), self.attn_ws_bytes), "rt_attention_decode")
+            else:
+                chk(lib.rt_attention(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), o.data_ptr(), M,
+                                     self.H, self.Hkv, self.hd, self.Lmax, self.pos.data_ptr()), "rt_attention")
             if L["attn_sub_norm"] is not None:
                 hip.act_rmsnorm_quantize(o, L["attn_sub_norm"], self.act_d, eps)
             else:
@@ -286,35 +299,38 @@ class _DeviceModel:
             out[:, v0:v0 + chunk] = hn @ self.emb[v0:v0 + chunk].float().T
         return out
 
-    def generate(self, prompt, n, graph):
+    def generate(self, prompt, n, graph, timings=None):
         import torch
 
         self._check_ids(prompt, 0)
         P = len(prompt)
         if P + n > self.Lmax:
             raise ValueError("prompt + new tokens exceed max_seq_len")
+        self._state(P)
+        g = None
+        if n > 1 and graph:  # capture the decode step first (capture does not execute it)
+            self._state(1)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self._enqueue(1, pos_base=P - 1, out_cap=n)
         self.ids[:P].copy_(torch.from_numpy(prompt))
         self.pos.fill_(0)
         self.best.zero_()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        ev[0].record()
         self._enqueue(P, pos_base=P - 1, out_cap=n)            # prefill; out_tokens[0]
-        if n > 1:
-            if graph:
-                self._state(1)
-                torch.cuda.synchronize()
-                g = torch.cuda.CUDAGraph()
-                saved_pos = self.pos.clone()
-                saved_ids = self.ids[:1].clone()
-                with torch.cuda.graph(g):
-                    self._enqueue(1, pos_base=P - 1, out_cap=n)
-                # capture does not execute; restore in case it touched nothing anyway
-                self.pos.copy_(saved_pos)
-                self.ids[:1].copy_(saved_ids)
-                for _ in range(n - 1):
-                    g.replay()
+        ev[1].record()
+        for _ in range(n - 1):
+            if g is not None:
+                g.replay()
             else:
-                for _ in range(n - 1):
-                    self._enqueue(1, pos_base=P - 1, out_cap=n)
+                self._enqueue(1, pos_base=P - 1, out_cap=n)
+        ev[2].record()
         torch.cuda.synchronize()
+        if timings is not None:
+            timings["prefill_ms"] = ev[0].elapsed_time(ev[1])
+            timings["decode_ms"] = ev[1].elapsed_time(ev[2])
         return self.out_tokens[:n].cpu().numpy().copy()
 
 

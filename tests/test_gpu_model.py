@@ -79,6 +79,38 @@ def test_rope_append_and_attention(hip, M, pos0, H, Hkv, hd):
     np.testing.assert_allclose(out.cpu().numpy(), ref, atol=2e-5, rtol=1e-4)
 
 
+@pytest.mark.parametrize("pos0,H,Hkv,hd,Lmax", [(0, 20, 5, 128, 640), (63, 20, 5, 128, 640), (64, 8, 2, 64, 200),
+                                                (511, 20, 5, 128, 640), (639, 20, 5, 128, 640), (100, 4, 4, 64, 130)])
+def test_attention_decode_split(hip, pos0, H, Hkv, hd, Lmax):
+    """Flash-decoding form equals the single-workgroup form; the workspace is reusable."""
+    import torch
+
+    lib, chk = _lib()
+    rng = np.random.default_rng(pos0 + H + Lmax)
+    kc = torch.from_numpy(rng.standard_normal((Hkv, hd, Lmax)).astype(np.float32)).cuda()
+    vc = torch.from_numpy(rng.standard_normal((Hkv, Lmax, hd)).astype(np.float32)).cuda()
+    q = torch.from_numpy(rng.standard_normal((1, H * hd)).astype(np.float32) * 2).cuda()
+    pos = torch.tensor([pos0], dtype=torch.int32, device="cuda")
+    ref = torch.empty((1, H * hd), device="cuda")
+    out = torch.empty((1, H * hd), device="cuda")
+    nbytes = lib.rt_attention_decode_workspace(H, hd, Lmax)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    hip._bind_stream()
+    chk(lib.rt_attention(hip.ctx, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), ref.data_ptr(), 1, H, Hkv, hd, Lmax,
+                         pos.data_ptr()))
+    for _ in range(3):
+        out.zero_()
+        chk(lib.rt_attention_decode(hip.ctx, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(), H, Hkv, hd,
+                                    Lmax, pos.data_ptr(), ws.data_ptr(), nbytes))
+        np.testing.assert_allclose(out.cpu().numpy(), ref.cpu().numpy(), atol=2e-6, rtol=2e-5)
+    K = kc.cpu().numpy().transpose(0, 2, 1)[:, :pos0 + 1]
+    V = vc.cpu().numpy()[:, :pos0 + 1]
+    o = O.causal_gqa_attention(q.cpu().numpy().reshape(1, H, hd), K, V, pos0).reshape(1, H * hd)
+    np.testing.assert_allclose(out.cpu().numpy(), o, atol=2e-5, rtol=1e-4)
+    # counters were reset: the workspace tail is zero again
+    assert int(ws[nbytes - 4 * H:].sum()) == 0
+
+
 @pytest.mark.parametrize("V,D", [(1000, 512), (5000, 2560), (777, 1024)])
 def test_lm_head_argmax(hip, V, D):
     import torch

@@ -43,6 +43,19 @@ typedef struct rt_weights rt_weights; /* one device-resident ternary matrix   */
 typedef struct rt_plan rt_plan;       /* a prepared multi-matrix launch        */
 typedef struct rt_act rt_act;         /* reusable quantised activations        */
 
+/* How the int8 input row of a fused decode plan is produced (one token). */
+#define RT_SRC_QUANT 0          /* q = quant(x)                                   */
+#define RT_SRC_RMSNORM 2        /* q = quant(RMSNorm(x) * aux)                    */
+#define RT_SRC_RELU2MUL 3       /* q = quant(relu(x)^2 * aux)        (x = gate, aux = up) */
+#define RT_SRC_RELU2MUL_NORM 4  /* q = quant(RMSNorm(relu(x)^2 * aux) * aux2)     */
+typedef struct rt_src {
+    int mode;           /* RT_SRC_*                                  */
+    const float* x;     /* fp32 [K] (device)                         */
+    const float* aux;   /* fp32 [K]: norm weight or up (device)      */
+    const float* aux2;  /* fp32 [K]: norm weight (RELU2MUL_NORM)     */
+    float eps;          /* RMSNorm epsilon                           */
+} rt_src;
+
 /* Thread-local text of the last error (never NULL).  Replaces the reference's
  * exception text (src/rotor/gpu_layers.py:21-24). */
 const char* rt_last_error(void);
@@ -161,6 +174,15 @@ int rt_linear_act_f32(rt_ctx* ctx, const rt_weights* w, const rt_act* act, const
  * no-op and rt_plan_gemv / rt_plan_run launch the matrix kernels only. */
 int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_act* const* act, int M,
                        float* const* y, rt_plan** out);
+
+/* Fused decode plan (one token): G linears sharing one input row, in ONE launch whose
+ * workgroups each quantise that row (fused with its producer as `src` says) into LDS
+ * before the GEMV, so no separate quantiser launch is needed; problem g writes
+ * y[g] fp32 [N_g] (+ residual[g] [N_g] when residual and residual[g] are non-NULL;
+ * y[g] may alias residual[g]).  Every weight must have the same K.  The device
+ * buffers named in src/y/residual must outlive the plan.  Run with rt_plan_run. */
+int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_src* src, float* const* y,
+                         const float* const* residual, rt_plan** out);
 
 /* ---- kernels around the linears for BitNet-2B-shape inference ----------------------
  * Positions are read from device memory (`pos`: position of the first of the M tokens)

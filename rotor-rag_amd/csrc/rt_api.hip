@@ -104,6 +104,8 @@ struct rt_plan {
     std::vector<QuantProb> quant;
     std::vector<GemmArgs> gemms;     // M > kGemvMaxM: one MFMA GEMM launch per problem
     std::vector<const rt_act*> acts; // plans over caller-quantised activations
+    bool fused = false;              // M = 1, input quantised in the GEMV prologue
+    QuantProb pro{};
 };
 
 struct rt_act {
@@ -487,6 +489,10 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
         if (act->M != plan->M) return fail(RT_EINVAL, "rt_plan_gemv: an input activation does not hold the plan's M tokens");
     DeviceGuard g(ctx->device);
     GemvArgs a{};
+    if (plan->fused) {
+        a.has_pro = 1;
+        a.pro = plan->pro;
+    }
     a.dev = plan->dev_probs;
     a.rb2p = plan->dev_rb2p;
     a.G = plan->G;
@@ -716,6 +722,63 @@ int rt_lm_head_argmax(rt_ctx* ctx, const uint16_t* emb, const float* x, const fl
     DeviceGuard g(ctx->device);
     RT_HIP(launch_lm_head(emb, x, norm_w, eps, V, D, logits, best, token, pos, advance, next_ids, out_tokens, pos_base,
                           out_cap, ctx->stream));
+    return RT_OK;
+}
+
+// --- fused decode plans ------------------------------------------------------------
+
+int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_src* src, float* const* y,
+                         const float* const* residual, rt_plan** out) {
+    if (!ctx || !w || !src || !y || !out) return fail(RT_EINVAL, "rt_plan_create_fused: NULL argument");
+    *out = nullptr;
+    if (G <= 0 || G > (1 << 16)) return fail(RT_EINVAL, "rt_plan_create_fused: G out of range");
+    if (!src->x) return fail(RT_EINVAL, "rt_plan_create_fused: source x is NULL");
+    if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRelu2Mul && src->mode != kRelu2MulNorm)
+        return fail(RT_EINVAL, "rt_plan_create_fused: unknown source mode");
+    if ((src->mode != kQuant && !src->aux) || (src->mode == kRelu2MulNorm && !src->aux2))
+        return fail(RT_EINVAL, "rt_plan_create_fused: the source mode needs aux/aux2");
+    const int K = w[0] ? w[0]->K : 0;
+    for (int g = 0; g < G; ++g) {
+        if (!w[g] || !y[g]) return fail(RT_EINVAL, "rt_plan_create_fused: NULL entry in a pointer array");
+        if (w[g]->K != K) return fail(RT_EINVAL, "rt_plan_create_fused: all weights must share K (one input)");
+        if (w[g]->device != ctx->device) return fail(RT_EINVAL, "rt_plan_create_fused: weights live on another device");
+    }
+    const int Kp = round_up(K, kChunk);
+    if ((size_t)16 * kRowBlock * sizeof(int) + (size_t)Kp + sizeof(double) * 40 > 64 * 1024)
+        return fail(RT_EINVAL, "rt_plan_create_fused: K too large for the LDS-resident input row");
+    DeviceGuard guard(ctx->device);
+    rt_plan* p = new rt_plan();
+    p->device = ctx->device;
+    p->G = G;
+    p->M = 1;
+    p->mt = 1;
+    p->Mpad = 1;
+    p->U = 0;
+    p->fused = true;
+    p->pro = QuantProb{src->x, nullptr, nullptr, nullptr, nullptr, K, Kp, src->mode, src->aux, src->eps, nullptr,
+                       src->aux2};
+    int wg = 0, minC = 1 << 30;
+    p->probs.resize(G);
+    for (int g = 0; g < G; ++g) {
+        p->probs[g] = GemvProb{w[g]->tiles, nullptr, nullptr, nullptr, y[g], w[g]->scale, w[g]->N, w[g]->C, w[g]->N, wg,
+                               residual ? residual[g] : nullptr};
+        wg += w[g]->Np / kRowBlock;
+        if (w[g]->C < minC) minC = w[g]->C;
+    }
+    p->total_rb = wg;
+    p->shape = gemv_shape_fused(wg, minC);
+    std::vector<int> rb2p(wg);
+    for (int g = 0; g < G; ++g)
+        for (int r = 0; r < w[g]->Np / kRowBlock; ++r) rb2p[p->probs[g].wg_begin + r] = g;
+    hipError_t e = hipMalloc(&p->dev_probs, sizeof(GemvProb) * G);
+    if (e == hipSuccess) e = hipMalloc(&p->dev_rb2p, sizeof(int) * wg);
+    if (e == hipSuccess) e = hipMemcpy(p->dev_rb2p, rb2p.data(), sizeof(int) * wg, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(p->dev_probs, p->probs.data(), sizeof(GemvProb) * G, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        rt_plan_free(p);
+        return hip_fail(e, "rt_plan_create_fused");
+    }
+    *out = p;
     return RT_OK;
 }
 

@@ -27,7 +27,7 @@
 //     t0: sel 0,1,2,3  -> 00, FF, 01, 00  =  w  for f = 00, 01, 10, 11
 //     t1: sel 0,4,8,12 -> 00, 01, FF, 00  = -w  for f = 00, 01, 10, 11
 // so element positions 0/2 accumulate into accP and 1/3 into accN, acc = accP - accN.
-#include "rt_internal.h"
+#include "rt_rowquant.h"
 
 namespace rt {
 
@@ -37,8 +37,9 @@ constexpr int kBufDword3 = 0x00020000;    // buffer resource word 3 for gfx9 raw
 constexpr int kAuxNT = 2;                 // cache policy: non-temporal (streamed once)
 
 // The activations are read-only for the whole launch, so the constant address space
-// lets uniform reads become s_load.
+// lets uniform reads become s_load; a prologue-quantised row is read from LDS.
 typedef __attribute__((address_space(4))) const int cint;
+typedef __attribute__((address_space(3))) const int lint;
 
 // Problem of global row block rbg: two dependent scalar loads (table, descriptor).
 __device__ __forceinline__ GemvProb find_prob(const GemvArgs& a, int rbg) {
@@ -46,8 +47,8 @@ __device__ __forceinline__ GemvProb find_prob(const GemvArgs& a, int rbg) {
     return a.dev[a.rb2p[rbg]];
 }
 
-template <int MT>
-__device__ __forceinline__ void chunk_step(const v4u v, cint* __restrict__ xc, const int ldx,
+template <int MT, typename XP>
+__device__ __forceinline__ void chunk_step(const v4u v, XP* __restrict__ xc, const int ldx,
                                            int (&accP)[MT], int (&accN)[MT]) {
     int d[16];
 #pragma unroll
@@ -61,7 +62,7 @@ __device__ __forceinline__ void chunk_step(const v4u v, cint* __restrict__ xc, c
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-        cint* __restrict__ xm = xc + m * ldx;
+        XP* __restrict__ xm = xc + m * ldx;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             accP[m] = __builtin_amdgcn_sdot4(d[4 * j + 0], xm[4 * j + 0], accP[m], false);
@@ -78,8 +79,8 @@ __device__ __forceinline__ void chunk_step(const v4u v, cint* __restrict__ xc, c
 // that run past the range come back as zeros without touching memory.  That keeps
 // every load unconditional -- two batches of U chunks in flight -- while the math on
 // chunks >= ce is skipped.
-template <int MT, int U>
-__device__ __forceinline__ void gemv_body(__amdgpu_buffer_rsrc_t rsrc, const int lane_off, cint* __restrict__ xq,
+template <int MT, int U, typename XP>
+__device__ __forceinline__ void gemv_body(__amdgpu_buffer_rsrc_t rsrc, const int lane_off, XP* __restrict__ xq,
                                           const int ldx, const int cb, const int ce, int (&accP)[MT],
                                           int (&accN)[MT]) {
     auto ld = [&](int c) {
@@ -93,17 +94,18 @@ __device__ __forceinline__ void gemv_body(__amdgpu_buffer_rsrc_t rsrc, const int
         for (int i = 0; i < U; ++i) B[i] = ld(c + U + i);
 #pragma unroll
         for (int i = 0; i < U; ++i)
-            if (c + i < ce) chunk_step<MT>(A[i], xq + (c + i) * 16, ldx, accP, accN);
+            if (c + i < ce) chunk_step<MT, XP>(A[i], xq + (c + i) * 16, ldx, accP, accN);
 #pragma unroll
         for (int i = 0; i < U; ++i) A[i] = ld(c + 2 * U + i);
 #pragma unroll
         for (int i = 0; i < U; ++i)
-            if (c + U + i < ce) chunk_step<MT>(B[i], xq + (c + U + i) * 16, ldx, accP, accN);
+            if (c + U + i < ce) chunk_step<MT, XP>(B[i], xq + (c + U + i) * 16, ldx, accP, accN);
     }
 }
 
-template <int MT>
-__device__ __forceinline__ void emit(const GemvArgs& a, const GemvProb& P, int rb, int m0, int m, int r, int acc) {
+// sx_pro: the token scale computed by a prologue (used instead of P.sx when >= 0)
+__device__ __forceinline__ void emit(const GemvArgs& a, const GemvProb& P, int rb, int m0, int m, int r, int acc,
+                                     float sx_pro = -1.0f) {
     const int n = rb * kRowBlock + r, mg = m0 + m;
     if (n >= P.N || mg >= a.M) return;
     if (a.out_i32) {
@@ -111,7 +113,8 @@ __device__ __forceinline__ void emit(const GemvArgs& a, const GemvProb& P, int r
     } else {
         const float sw = P.rs ? P.rs[n] : P.s_w;
         const size_t o = (size_t)mg * P.ldo + n;
-        const float y = ((float)acc * P.sx[mg]) * sw;
+        const float sx = sx_pro >= 0.0f ? sx_pro : P.sx[mg];
+        const float y = ((float)acc * sx) * sw;
         static_cast<float*>(P.out)[o] = P.res ? P.res[o] + y : y;
     }
 }
@@ -133,15 +136,17 @@ __global__ void __launch_bounds__(1024) gemv_rows_kernel(GemvArgs a) {
     int accP[MT], accN[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
-    gemv_body<MT, U>(rsrc, lane * 16, xq, ldx, 0, C, accP, accN);
+    gemv_body<MT, U, const __attribute__((address_space(4))) int>(rsrc, lane * 16, xq, ldx, 0, C, accP, accN);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) emit<MT>(a, P, rb, m0, m, lane, accP[m] - accN[m]);
+    for (int m = 0; m < MT; ++m) emit(a, P, rb, m0, m, lane, accP[m] - accN[m]);
 }
 
-template <int MT>
+// LDS of the KSPLIT kernel: [nw][MT][64] int partial sums, then (prologue) the
+// quantised input row (Kp bytes) and the reduction scratch of the prologue.
+template <int MT, bool PRO>
 __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
     constexpr int U = MT == 1 ? 4 : 2;
-    extern __shared__ int red[];  // [nw][MT][64]
+    extern __shared__ __attribute__((aligned(16))) int red[];
     const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const GemvProb P = find_prob(a, blockIdx.x);
@@ -151,11 +156,20 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
     const int cb = (wave * C) / nw, ce = ((wave + 1) * C) / nw;
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, ce * 1024, kBufDword3);
-    cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
     int accP[MT], accN[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
-    gemv_body<MT, U>(rsrc, lane * 16, xq, ldx, cb, ce, accP, accN);
+    float sx_pro = -1.0f;
+    if constexpr (PRO) {
+        v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
+        RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (a.pro.Kp >> 4));
+        sx_pro = row_quantize<1>(a.pro, 0, lq, nullptr, nullptr, sm);
+        __syncthreads();
+        gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accN);
+    } else {
+        cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
+        gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, cb, ce, accP, accN);
+    }
 #pragma unroll
     for (int m = 0; m < MT; ++m) red[(wave * MT + m) * kRowBlock + lane] = accP[m] - accN[m];
     __syncthreads();
@@ -163,8 +177,17 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
         const int m = idx / kRowBlock, r = idx % kRowBlock;
         int s = 0;
         for (int w = 0; w < nw; ++w) s += red[(w * MT + m) * kRowBlock + r];
-        emit<MT>(a, P, rb, m0, m, r, s);
+        emit(a, P, rb, m0, m, r, s, sx_pro);
     }
+}
+
+GemvShape gemv_shape_fused(int total_rb, int min_C) {
+    // the prologue needs one row block per workgroup (KSPLIT), whatever the size
+    int nw = (2048 + total_rb - 1) / total_rb;
+    if (nw > 16) nw = 16;
+    if (nw > min_C / 2) nw = min_C / 2;
+    if (nw < 1) nw = 1;
+    return GemvShape{true, nw};
 }
 
 GemvShape gemv_shape(int total_rb, int m_blocks, int min_C) {
@@ -188,14 +211,19 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
     if (a.total_rb <= 0 || a.M <= 0) return hipSuccess;
     const unsigned mblocks = (unsigned)((a.M + mt - 1) / mt);
     const dim3 block((unsigned)(64 * shape.nw));
-    if (shape.ksplit) {
+    if (a.has_pro) {  // single token, prologue-quantised input: KSPLIT shape only
+        if (mt != 1 || a.M != 1 || !shape.ksplit) return hipErrorInvalidValue;
+        const dim3 grid((unsigned)a.total_rb, 1);
+        const size_t lds = (size_t)shape.nw * kRowBlock * sizeof(int) + (size_t)a.pro.Kp + sizeof(RowSmem);
+        hipLaunchKernelGGL((gemv_ksplit_kernel<1, true>), grid, block, lds, s, a);
+    } else if (shape.ksplit) {
         const dim3 grid((unsigned)a.total_rb, mblocks);
         const size_t lds = (size_t)shape.nw * mt * kRowBlock * sizeof(int);
         switch (mt) {
-            case 1: hipLaunchKernelGGL(gemv_ksplit_kernel<1>, grid, block, lds, s, a); break;
-            case 2: hipLaunchKernelGGL(gemv_ksplit_kernel<2>, grid, block, lds, s, a); break;
-            case 4: hipLaunchKernelGGL(gemv_ksplit_kernel<4>, grid, block, lds, s, a); break;
-            case 8: hipLaunchKernelGGL(gemv_ksplit_kernel<8>, grid, block, lds, s, a); break;
+            case 1: hipLaunchKernelGGL((gemv_ksplit_kernel<1, false>), grid, block, lds, s, a); break;
+            case 2: hipLaunchKernelGGL((gemv_ksplit_kernel<2, false>), grid, block, lds, s, a); break;
+            case 4: hipLaunchKernelGGL((gemv_ksplit_kernel<4, false>), grid, block, lds, s, a); break;
+            case 8: hipLaunchKernelGGL((gemv_ksplit_kernel<8, false>), grid, block, lds, s, a); break;
             default: return hipErrorInvalidValue;
         }
     } else {

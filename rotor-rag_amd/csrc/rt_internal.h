@@ -38,32 +38,6 @@ constexpr size_t kTileSlack = 16384;
 
 inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 
-// ---- one GEMV problem (a ternary matrix applied to M tokens) -------------------
-struct GemvProb {
-    const v4u* w;        // weight tiles
-    const int8_t* qx;    // quantised activations [Mpad][Kp] (layout above)
-    const float* sx;     // [Mpad] per-token scales (unused for int32 output)
-    const float* rs;     // [N] per-row scales or nullptr (then s_w)
-    void* out;           // float y[M][ldo] or int32 acc[M][ldo]
-    float s_w;
-    int N, C, ldo;
-    int wg_begin;        // first global row block of this problem (prefix sum over problems)
-    const float* res;    // optional fp32 [M][ldo] added to y (may alias out)
-};
-
-struct GemvArgs {
-    const GemvProb* dev;  // device descriptor array [G] (plans) or nullptr -> p
-    const int* rb2p;      // [total_rb] problem index of every global row block (plans)
-    int G, M, out_i32;
-    int total_rb;         // row blocks over all problems
-    GemvProb p;           // the problem of a single-problem launch
-};
-
-struct GemvShape {
-    bool ksplit;  // true: one row block per workgroup, waves split K
-    int nw;       // waves per workgroup
-};
-
 // ---- one quantisation problem (-> qx, sx) -----------------------------------------
 // The value quantised for element k of a row depends on `mode`:
 //   kQuant    v = x[k]
@@ -85,6 +59,34 @@ struct QuantProb {
     float eps;
     float* v_out;        // optional fp32 [M][K]: the values that were quantised
     const float* aux2;   // norm_w [K] (kRelu2MulNorm)
+};
+
+// ---- one GEMV problem (a ternary matrix applied to M tokens) -------------------
+struct GemvProb {
+    const v4u* w;        // weight tiles
+    const int8_t* qx;    // quantised activations [Mpad][Kp] (layout above)
+    const float* sx;     // [Mpad] per-token scales (unused for int32 output)
+    const float* rs;     // [N] per-row scales or nullptr (then s_w)
+    void* out;           // float y[M][ldo] or int32 acc[M][ldo]
+    float s_w;
+    int N, C, ldo;
+    int wg_begin;        // first global row block of this problem (prefix sum over problems)
+    const float* res;    // optional fp32 [M][ldo] added to y (may alias out)
+};
+
+struct GemvArgs {
+    const GemvProb* dev;  // device descriptor array [G] (plans) or nullptr -> p
+    const int* rb2p;      // [total_rb] problem index of every global row block (plans)
+    int G, M, out_i32;
+    int total_rb;         // row blocks over all problems
+    GemvProb p;           // the problem of a single-problem launch
+    int has_pro;          // M = 1: every workgroup quantises `pro` (row 0) into LDS first
+    QuantProb pro;        // source row of the prologue (mode, x, aux, aux2, eps, K, Kp)
+};
+
+struct GemvShape {
+    bool ksplit;  // true: one row block per workgroup, waves split K
+    int nw;       // waves per workgroup
 };
 
 struct QuantArgs {
@@ -134,5 +136,7 @@ hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w
 inline int gemv_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 // Host policy: launch shape so that small launches still fill the chip.
 GemvShape gemv_shape(int total_rb, int m_blocks, int min_C);
+// Launch shape of a plan whose GEMV quantises its input in the prologue (M = 1).
+GemvShape gemv_shape_fused(int total_rb, int min_C);
 
 }  // namespace rt

@@ -1,0 +1,207 @@
+// Device helpers that turn one token row into int8 activations in the qx layout:
+// the per-token absmax quantiser, optionally fused with the operation producing the row
+// (RMSNorm, relu^2(gate)*up, relu^2(gate)*up followed by RMSNorm).  Shared by the
+// quantiser kernel (rt_quant.hip, destination global memory) and the decode GEMV
+// prologue (rt_gemv.hip, destination LDS).  Any workgroup size that is a multiple of 64
+// up to 1024 works.
+//
+// Quantiser: src/rotor/quantization.py:137-149 (bits = 8, symmetric) applied per row:
+// s = max|v| / 127 (1 when the row is all zero), q = clip(rint(v / s), -128, 127), with
+// IEEE fp32 division (HIP's default `/`; never built with fast-math) and round-half-even
+// (rintf -> v_rndne_f32); max|v| is order independent.
+// RMSNorm: src/rotor/transformer.py:24-36 (x / sqrt(mean(x^2) + eps) * w); the mean of
+// squares is accumulated in f64 and rounded once to f32, so its value does not depend
+// on the summation order.
+#pragma once
+
+#include "rt_internal.h"
+
+namespace rt {
+
+struct RowSmem {   // reduction scratch in LDS (one slot per wave)
+    float f[16];
+    double d[16];
+};
+
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, T* red, Op op) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    __syncthreads();  // `red` may still be read by a previous reduction
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    T r = red[0];
+    for (int w = 1; w < nw; ++w) r = op(r, red[w]);
+    return r;
+}
+
+// byte p (0..15) of a permuted group holds element 4*(p%4) + p/4 of the group
+__device__ __forceinline__ v4u pack_permuted(const int (&q)[16]) {
+    v4u o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        unsigned d = 0u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) d |= ((unsigned)q[4 * b + i] & 0xffu) << (8 * b);
+        o[i] = d;
+    }
+    return o;
+}
+
+// 16 elements of group g (k = 16g .. 16g+15) of a row; zeros past K.  `vec`: the row is
+// 16-byte aligned with K % 16 == 0; groups wholly inside the row are then read as four
+// float4 (the padding groups of Kp > K are never read).
+__device__ __forceinline__ void load_group(const float* __restrict__ xr, int g, int K, bool vec, float (&v)[16]) {
+    if (vec && (g + 1) * 16 <= K) {
+        const float4* p = reinterpret_cast<const float4*>(xr + g * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 t = p[i];
+            v[4 * i + 0] = t.x;
+            v[4 * i + 1] = t.y;
+            v[4 * i + 2] = t.z;
+            v[4 * i + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int k = g * 16 + e;
+            v[e] = k < K ? xr[k] : 0.0f;
+        }
+    }
+}
+
+__device__ __forceinline__ bool has_norm(const QuantProb& P) { return P.mode == kRmsNorm || P.mode == kRelu2MulNorm; }
+__device__ __forceinline__ bool has_relu2(const QuantProb& P) { return P.mode == kRelu2Mul || P.mode == kRelu2MulNorm; }
+__device__ __forceinline__ const float* norm_weight(const QuantProb& P) { return P.mode == kRmsNorm ? P.aux : P.aux2; }
+
+// The values of group g before any row-wide normalisation:
+// kQuant/kRmsNorm: x; kRelu2Mul(Norm): relu(gate)^2 * up.
+__device__ __forceinline__ void source_group(const QuantProb& P, const float* xr, const float* ur, int g, bool vec,
+                                             float (&v)[16]) {
+    load_group(xr, g, P.K, vec, v);
+    if (has_relu2(P)) {
+        float u[16];
+        load_group(ur, g, P.K, vec, u);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = v[e] > 0.0f ? (v[e] * v[e]) * u[e] : 0.0f;
+    }
+}
+
+// h = (v / norm) * w for group g
+__device__ __forceinline__ void rmsnorm_group(const QuantProb& P, float norm, int g, bool vec, float (&v)[16]) {
+    float w[16];
+    load_group(norm_weight(P), g, P.K, vec, w);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = (v[e] / norm) * w[e];
+}
+
+// q = clip(rint(v / s), -128, 127) for one group; permuted 16-byte store and, when
+// requested, the natural-order bytes and the fp32 values.
+__device__ __forceinline__ void emit_group(const float (&v)[16], float s, int g, int K, v4u* qrow, int8_t* qn,
+                                           float* vo) {
+    int q[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        float r = rintf(v[e] / s);
+        r = fminf(fmaxf(r, -128.0f), 127.0f);
+        q[e] = (int)r;
+    }
+    qrow[g] = pack_permuted(q);
+    if (qn || vo) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int k = g * 16 + e;
+            if (k < K) {
+                if (qn) qn[k] = (int8_t)q[e];
+                if (vo) vo[k] = v[e];
+            }
+        }
+    }
+}
+
+__device__ __forceinline__ float amax_group(const float (&v)[16], float m) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) m = fmaxf(m, fabsf(v[e]));
+    return m;
+}
+
+__device__ __forceinline__ double sumsq_group(const float (&v)[16], double s) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += (double)v[e] * (double)v[e];
+    return s;
+}
+
+// Quantise token row m of P (modes kQuant, kRmsNorm, kRelu2Mul, kRelu2MulNorm) into
+// qrow (Kp/16 permuted groups) and return its scale.  Rows of up to REG groups of 16
+// per thread stay in registers, longer rows are read again on every pass.  Every
+// thread of the workgroup must call it (it synchronises).
+template <int REG>
+__device__ __forceinline__ float row_quantize(const QuantProb& P, int m, v4u* qrow, int8_t* qn, float* vo,
+                                              RowSmem* sm) {
+    const int K = P.K, groups = P.Kp >> 4, T = blockDim.x;
+    const float* xr = P.x + (size_t)m * K;
+    const float* ur = has_relu2(P) ? P.aux + (size_t)m * K : nullptr;
+    bool vec = (K & 15) == 0 && ((uintptr_t)xr & 15u) == 0;
+    if (ur) vec = vec && ((uintptr_t)ur & 15u) == 0;
+    if (has_norm(P)) vec = vec && ((uintptr_t)norm_weight(P) & 15u) == 0;
+    auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
+    auto dadd_op = [](double x, double y) { return x + y; };
+
+    if (groups <= REG * T) {  // the row stays in registers
+        float v[REG][16];
+#pragma unroll
+        for (int r = 0; r < REG; ++r) source_group(P, xr, ur, threadIdx.x + r * T, vec, v[r]);
+        if (has_norm(P)) {
+            double ss = 0.0;
+#pragma unroll
+            for (int r = 0; r < REG; ++r) ss = sumsq_group(v[r], ss);
+            ss = block_reduce(ss, sm->d, dadd_op);
+            const float norm = sqrtf((float)(ss / (double)K) + P.eps);
+#pragma unroll
+            for (int r = 0; r < REG; ++r) rmsnorm_group(P, norm, threadIdx.x + r * T, vec, v[r]);
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int r = 0; r < REG; ++r) amax = amax_group(v[r], amax);
+        amax = block_reduce(amax, sm->f, fmax_op);
+        const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+#pragma unroll
+        for (int r = 0; r < REG; ++r) {
+            const int g = threadIdx.x + r * T;
+            if (g < groups) emit_group(v[r], s, g, K, qrow, qn, vo);
+        }
+        return s;
+    }
+    // long rows: recompute the source values on every pass
+    float norm = 1.0f;
+    if (has_norm(P)) {
+        double ss = 0.0;
+        for (int g = threadIdx.x; g < groups; g += T) {
+            float v[16];
+            source_group(P, xr, ur, g, vec, v);
+            ss = sumsq_group(v, ss);
+        }
+        ss = block_reduce(ss, sm->d, dadd_op);
+        norm = sqrtf((float)(ss / (double)K) + P.eps);
+    }
+    float amax = 0.0f;
+    for (int g = threadIdx.x; g < groups; g += T) {
+        float v[16];
+        source_group(P, xr, ur, g, vec, v);
+        if (has_norm(P)) rmsnorm_group(P, norm, g, vec, v);
+        amax = amax_group(v, amax);
+    }
+    amax = block_reduce(amax, sm->f, fmax_op);
+    const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+    for (int g = threadIdx.x; g < groups; g += T) {
+        float v[16];
+        source_group(P, xr, ur, g, vec, v);
+        if (has_norm(P)) rmsnorm_group(P, norm, g, vec, v);
+        emit_group(v, s, g, K, qrow, qn, vo);
+    }
+    return s;
+}
+
+}  // namespace rt

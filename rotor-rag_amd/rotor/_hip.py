@@ -16,6 +16,14 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "librotor_hip.so"
 
+class RtSrc(ctypes.Structure):
+    """rt_src of include/rotor_hip.h"""
+    _fields_ = [("mode", ctypes.c_int), ("x", ctypes.c_void_p), ("aux", ctypes.c_void_p), ("aux2", ctypes.c_void_p),
+                ("eps", ctypes.c_float)]
+
+
+SRC_QUANT, SRC_RMSNORM, SRC_RELU2MUL, SRC_RELU2MUL_NORM = 0, 2, 3, 4
+
 # name -> (restype, argtypes); every entry point of include/rotor_hip.h
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -53,6 +61,8 @@ SIGNATURES = {
     "rt_linear_act_f32": (_I, [_P, _P, _P, _P, _P]),
     "rt_plan_create_act": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, ctypes.POINTER(_P),
                                 ctypes.POINTER(_P)]),
+    "rt_plan_create_fused": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(RtSrc), ctypes.POINTER(_P),
+                                  ctypes.POINTER(_P), ctypes.POINTER(_P)]),
     "rt_embed": (_I, [_P, _P, _I, _I, _P, _I, _P]),
     "rt_rope_kv_append": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "rt_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),

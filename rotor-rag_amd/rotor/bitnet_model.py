@@ -207,11 +207,30 @@ class _DeviceModel:
         e = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)
         st = {"h": e(M, D), "q": e(M, H * hd), "k": e(M, Hkv * hd), "v": e(M, Hkv * hd), "o": e(M, H * hd),
               "g": e(M, F), "u": e(M, F)}
-        st["qkv"], st["gu"] = [], []
+        st["qkv"], st["gu"], st["o_plan"], st["d_plan"] = [], [], [], []
+        hip, eps = self.hip, self.m.eps
         for L in self.layers:
-            st["qkv"].append(self.hip.plan_act([L["q_proj"], L["k_proj"], L["v_proj"]], [self.act_d] * 3, M,
-                                               [st["q"], st["k"], st["v"]]))
-            st["gu"].append(self.hip.plan_act([L["gate_proj"], L["up_proj"]], [self.act_d] * 2, M, [st["g"], st["u"]]))
+            if M == 1:  # decode: one launch per plan, the input row is quantised in the GEMV prologue
+                h, o, g, u = st["h"][0], st["o"][0], st["g"][0], st["u"][0]
+                st["qkv"].append(hip.plan_fused([L["q_proj"], L["k_proj"], L["v_proj"]], _hip.SRC_RMSNORM, h,
+                                                L["input_norm"], eps=eps, ys=[st["q"][0], st["k"][0], st["v"][0]]))
+                if L["attn_sub_norm"] is not None:
+                    st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_RMSNORM, o, L["attn_sub_norm"], eps=eps,
+                                                       ys=[h], residuals=[h]))
+                else:
+                    st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_QUANT, o, ys=[h], residuals=[h]))
+                st["gu"].append(hip.plan_fused([L["gate_proj"], L["up_proj"]], _hip.SRC_RMSNORM, h, L["post_norm"],
+                                               eps=eps, ys=[g, u]))
+                if L["ffn_sub_norm"] is not None:
+                    st["d_plan"].append(hip.plan_fused([L["down_proj"]], _hip.SRC_RELU2MUL_NORM, g, u,
+                                                       L["ffn_sub_norm"], eps=eps, ys=[h], residuals=[h]))
+                else:
+                    st["d_plan"].append(hip.plan_fused([L["down_proj"]], _hip.SRC_RELU2MUL, g, u, ys=[h],
+                                                       residuals=[h]))
+            else:
+                st["qkv"].append(hip.plan_act([L["q_proj"], L["k_proj"], L["v_proj"]], [self.act_d] * 3, M,
+                                              [st["q"], st["k"], st["v"]]))
+                st["gu"].append(hip.plan_act([L["gate_proj"], L["up_proj"]], [self.act_d] * 2, M, [st["g"], st["u"]]))
         self.state[M] = st
         return st
 
@@ -225,9 +244,13 @@ class _DeviceModel:
         chk(lib.rt_embed(ctx, self.emb.data_ptr(), self.m.vocab_size, self.D, self.ids.data_ptr(), M, h.data_ptr()),
             "rt_embed")
         eps = self.m.eps
+        fused = M == 1
         for li, L in enumerate(self.layers):
-            hip.act_rmsnorm_quantize(h, L["input_norm"], self.act_d, eps)
-            st["qkv"][li].gemv()
+            if fused:
+                st["qkv"][li].run()
+            else:
+                hip.act_rmsnorm_quantize(h, L["input_norm"], self.act_d, eps)
+                st["qkv"][li].gemv()
             chk(lib.rt_rope_kv_append(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
                                       L["vc"].data_ptr(), self.rope.data_ptr(), M, self.H, self.Hkv, self.hd,
                                       self.Lmax, self.pos.data_ptr()), "rt_rope_kv_append")
@@ -238,6 +261,11 @@ class _DeviceModel:
             else:
                 chk(lib.rt_attention(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), o.data_ptr(), M,
                                      self.H, self.Hkv, self.hd, self.Lmax, self.pos.data_ptr()), "rt_attention")
+            if fused:
+                st["o_plan"][li].run()
+                st["gu"][li].run()
+                st["d_plan"][li].run()
+                continue
             if L["attn_sub_norm"] is not None:
                 hip.act_rmsnorm_quantize(o, L["attn_sub_norm"], self.act_d, eps)
             else:

@@ -377,6 +377,31 @@ class HIPTernaryOps:
         _hip.check(self.lib.rt_plan_create_act(self.ctx, G, wa, aa, int(M), ya, ctypes.byref(h)), "rt_plan_create_act")
         return LinearPlan(self, h, (list(weights), list(acts), list(ys)))
 
+    def plan_fused(self, weights, mode: int, x, aux=None, aux2=None, eps: float = 1e-6, ys=None, residuals=None):
+        """One-token plan whose single launch quantises its input row in the prologue:
+        mode = _hip.SRC_QUANT / SRC_RMSNORM / SRC_RELU2MUL / SRC_RELU2MUL_NORM; x, aux, aux2
+        device fp32 [K]; ys[g] fp32 [N_g] outputs (+ residuals[g])."""
+        G = len(weights)
+        if G == 0 or len(ys) != G or (residuals is not None and len(residuals) != G):
+            raise ValueError("plan_fused: mismatched argument lists")
+        K = weights[0].in_features
+        for w, y in zip(weights, ys):
+            if w.in_features != K or y.numel() != w.out_features or not y.is_contiguous():
+                raise ValueError("plan_fused: shapes do not match")
+        for t in (x, aux, aux2):
+            if t is not None and (t.numel() < K or not t.is_contiguous() or t.device != self.device):
+                raise ValueError("plan_fused: source tensors must be contiguous device tensors of >= K elements")
+        src = _hip.RtSrc(int(mode), x.data_ptr(), aux.data_ptr() if aux is not None else None,
+                         aux2.data_ptr() if aux2 is not None else None, float(eps))
+        P = ctypes.c_void_p
+        wa = (P * G)(*[w.handle for w in weights])
+        ya = (P * G)(*[y.data_ptr() for y in ys])
+        ra = (P * G)(*[r.data_ptr() if r is not None else None for r in residuals]) if residuals is not None else None
+        h = ctypes.c_void_p()
+        _hip.check(self.lib.rt_plan_create_fused(self.ctx, G, wa, ctypes.byref(src), ya, ra, ctypes.byref(h)),
+                   "rt_plan_create_fused")
+        return LinearPlan(self, h, (list(weights), [x, aux, aux2], list(ys), list(residuals or [])))
+
     def __del__(self):
         try:
             if getattr(self, "ctx", None):

@@ -139,3 +139,48 @@ def test_ffn_block_graph_replay(hip):
             assert np.array_equal(_np(y), yo), f"replay {i}"
     finally:
         gpu_layers._gpu_instance = None
+
+
+@pytest.mark.parametrize("mode,K,N", [(0, 2560, 640), (2, 2560, 2560), (3, 6912, 2560), (4, 6912, 2560), (2, 100, 77)])
+def test_fused_plan_equals_act_path(hip, mode, K, N):
+    """One-launch decode plans (input quantised in the GEMV prologue) give exactly the
+    result of the separate quantiser + linear path, with and without the residual."""
+    import torch
+
+    from rotor import _hip
+
+    rng = np.random.default_rng(mode * 1000 + K)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    x = d(rng.standard_normal(K) * 2)
+    aux = d(rng.uniform(0.5, 1.5, K) if mode == 2 else rng.standard_normal(K))
+    aux2 = d(rng.uniform(0.5, 1.5, K))
+    Ws = [O.make_ternary(rng, N, K) for _ in range(2)]
+    ws = [hip.upload(O.pack_rotor(W), K, s) for W, s in Ws]
+    res = d(rng.standard_normal(N))
+    ys = [torch.empty(N, device="cuda"), torch.empty(N, device="cuda")]
+    y_res = res.clone()
+    plan = hip.plan_fused(ws, mode, x, aux if mode else None, aux2 if mode == 4 else None, 1e-6, ys=ys)
+    plan2 = hip.plan_fused(ws[:1], mode, x, aux if mode else None, aux2 if mode == 4 else None, 1e-6, ys=[y_res],
+                           residuals=[y_res])
+    plan.run()
+    plan2.run()
+    act = hip.activations(1, K)
+    xr = x[None]
+    if mode == 0:
+        hip.act_quantize(xr, act)
+    elif mode == 2:
+        hip.act_rmsnorm_quantize(xr, aux, act, 1e-6)
+    elif mode == 3:
+        hip.act_relu2_mul_quantize(xr, aux[None], act)
+    else:
+        hip.act_relu2_mul_norm_quantize(xr, aux[None], aux2, act, 1e-6)
+    for w, y in zip(ws, ys):
+        assert torch.equal(hip.linear_act(w, act)[0], y)
+    assert torch.equal(hip.linear_act(ws[0], act, residual=res[None])[0], y_res)
+    # and the int8 input equals the oracle's for that mode
+    q, s = act.export()
+    xn, an, a2n = x.cpu().numpy(), aux.cpu().numpy(), aux2.cpu().numpy()
+    src = {0: xn, 2: O.rms_norm_f64acc(xn[None], an)[0], 3: O.relu2_gate(xn, an),
+           4: O.rms_norm_f64acc(O.relu2_gate(xn, an)[None], a2n)[0]}[mode]
+    qo, so = O.quant_rows(src[None])
+    assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(s.cpu().numpy(), so)

@@ -48,12 +48,16 @@ typedef struct rt_act rt_act;         /* reusable quantised activations        *
 #define RT_SRC_RMSNORM 2        /* q = quant(RMSNorm(x) * aux)                    */
 #define RT_SRC_RELU2MUL 3       /* q = quant(relu(x)^2 * aux)        (x = gate, aux = up) */
 #define RT_SRC_RELU2MUL_NORM 4  /* q = quant(RMSNorm(relu(x)^2 * aux) * aux2)     */
+#define RT_SRC_ATTN_NORM 5      /* q = quant(RMSNorm(attention(x)) * aux): x = the workspace
+                                   of rt_attention_decode_partials, combined per head */
 typedef struct rt_src {
     int mode;           /* RT_SRC_*                                  */
-    const float* x;     /* fp32 [K] (device)                         */
+    const float* x;     /* fp32 [K] (device); partials for ATTN_NORM */
     const float* aux;   /* fp32 [K]: norm weight or up (device)      */
     const float* aux2;  /* fp32 [K]: norm weight (RELU2MUL_NORM)     */
     float eps;          /* RMSNorm epsilon                           */
+    int attn_head_dim;  /* ATTN_NORM: head dimension (K = heads * head_dim) */
+    int attn_max_len;   /* ATTN_NORM: Lmax given to rt_attention_decode_partials */
 } rt_src;
 
 /* Thread-local text of the last error (never NULL).  Replaces the reference's
@@ -204,15 +208,17 @@ int rt_rope_kv_append(rt_ctx* ctx, float* q, float* k, const float* v, float* k_
 int rt_attention(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, float* out, int M, int H,
                  int Hkv, int hd, int Lmax, const int* pos);
 
-/* Decode form of rt_attention for one query (M = 1): the keys are split over
- * workgroups of 64 and the partial softmax sums are combined by the last workgroup of
- * each head (flash-decoding).  workspace: device memory of at least
- * rt_attention_decode_workspace(H, hd, Lmax) bytes, ZEROED before its first use and left
- * reusable (its counters are reset by the kernel); calls sharing one workspace must not
- * overlap.  head_dim 64 or 128. */
+/* Decode form of rt_attention for one query (M = 1, flash-decoding): the keys are split
+ * over workgroups of 64; each writes a partial softmax result to `workspace` (at least
+ * rt_attention_decode_workspace(H, hd, Lmax) bytes of device memory, no initialisation
+ * needed), then a second launch combines them into out [H*hd].  head_dim 64 or 128.
+ * rt_attention_decode_partials stops after the first launch; a fused plan with source
+ * RT_SRC_ATTN_NORM then combines the partials in its prologue. */
 size_t rt_attention_decode_workspace(int H, int hd, int Lmax);
 int rt_attention_decode(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, float* out, int H,
                         int Hkv, int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes);
+int rt_attention_decode_partials(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, int H,
+                                 int Hkv, int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes);
 
 /* Final RMSNorm of x fp32 [D] with norm_w, tied bf16 LM head logits [V]
  * (src/rotor/bitnet_model.py:231-235) and greedy argmax (src/rotor/generation.py:42;

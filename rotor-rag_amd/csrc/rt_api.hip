@@ -287,7 +287,7 @@ static int stage_activations(rt_ctx* ctx, const float* x, const int8_t* q_in, in
     a.U = 1;
     a.M = M;
     a.Mpad = Mpad;
-    a.p = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp, q_in ? kPermute : kQuant, nullptr, 0.0f, nullptr, nullptr};
+    a.p = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp, q_in ? kPermute : kQuant, nullptr, 0.0f, nullptr, nullptr, 0, 0};
     RT_HIP(launch_quant(a, ctx->stream));
     if (s_out) RT_HIP(hipMemcpyAsync(s_out, *sx, (size_t)M * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
     return RT_OK;
@@ -428,7 +428,7 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
         const int u = which[g];
         p->quant[u] = QuantProb{x[g], nullptr, reinterpret_cast<int8_t*>(base + qoff[u]),
                                 reinterpret_cast<float*>(base + soff[u]), nullptr, Ku[u], round_up(Ku[u], kChunk),
-                                kQuant, nullptr, 0.0f, nullptr, nullptr};
+                                kQuant, nullptr, 0.0f, nullptr, nullptr, 0, 0};
     }
     int wg = 0, minC = 1 << 30;
     p->probs.resize(G);
@@ -552,7 +552,7 @@ static int act_fill(rt_ctx* ctx, rt_act* act, int M, int mode, const float* x, c
     q.U = 1;
     q.M = M;
     q.Mpad = act_rows(M);
-    q.p = QuantProb{x, nullptr, act->qx, act->sx, nullptr, act->K, act->Kp, mode, aux, eps, v_out, aux2};
+    q.p = QuantProb{x, nullptr, act->qx, act->sx, nullptr, act->K, act->Kp, mode, aux, eps, v_out, aux2, 0, 0};
     RT_HIP(launch_quant(q, ctx->stream));
     act->M = M;
     act->Mpad = q.Mpad;
@@ -692,23 +692,38 @@ int rt_attention(rt_ctx* ctx, const float* q, const float* k_cache, const float*
 }
 
 size_t rt_attention_decode_workspace(int H, int hd, int Lmax) {
-    return (size_t)H * ((Lmax + 63) / 64) * (hd + 2) * sizeof(float) + (size_t)H * sizeof(int);
+    return (size_t)H * attn_splits(Lmax) * (hd + 2) * sizeof(float);
+}
+
+static int attn_decode_check(rt_ctx* ctx, const float* q, const float* kc, const float* vc, const int* pos, void* ws,
+                             size_t ws_bytes, int H, int Hkv, int hd, int Lmax, const char* who) {
+    if (!ctx || !q || !kc || !vc || !pos || !ws) return fail(RT_EINVAL, std::string(who) + ": NULL argument");
+    int rc = check_heads(H, Hkv, hd, Lmax, who);
+    if (rc) return rc;
+    if (hd != 64 && hd != 128) return fail(RT_EINVAL, std::string(who) + ": head_dim must be 64 or 128");
+    if (ws_bytes < rt_attention_decode_workspace(H, hd, Lmax))
+        return fail(RT_EINVAL, std::string(who) + ": workspace too small");
+    return RT_OK;
+}
+
+int rt_attention_decode_partials(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, int H,
+                                 int Hkv, int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes) {
+    int rc = attn_decode_check(ctx, q, k_cache, v_cache, pos, workspace, workspace_bytes, H, Hkv, hd, Lmax,
+                               "rt_attention_decode_partials");
+    if (rc) return rc;
+    DeviceGuard g(ctx->device);
+    RT_HIP(launch_attn_partial(q, k_cache, v_cache, H, Hkv, hd, Lmax, pos, 1.0f / sqrtf((float)hd),
+                               static_cast<float*>(workspace), ctx->stream));
+    return RT_OK;
 }
 
 int rt_attention_decode(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, float* out, int H,
                         int Hkv, int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes) {
-    if (!ctx || !q || !k_cache || !v_cache || !out || !pos || !workspace)
-        return fail(RT_EINVAL, "rt_attention_decode: NULL argument");
-    int rc = check_heads(H, Hkv, hd, Lmax, "rt_attention_decode");
+    if (!out) return fail(RT_EINVAL, "rt_attention_decode: out is NULL");
+    int rc = rt_attention_decode_partials(ctx, q, k_cache, v_cache, H, Hkv, hd, Lmax, pos, workspace, workspace_bytes);
     if (rc) return rc;
-    if (hd != 64 && hd != 128) return fail(RT_EINVAL, "rt_attention_decode: head_dim must be 64 or 128");
-    const size_t need = rt_attention_decode_workspace(H, hd, Lmax);
-    if (workspace_bytes < need) return fail(RT_EINVAL, "rt_attention_decode: workspace too small");
-    float* work = static_cast<float*>(workspace);
-    int* counters = reinterpret_cast<int*>(static_cast<char*>(workspace) + need - (size_t)H * sizeof(int));
     DeviceGuard g(ctx->device);
-    RT_HIP(launch_attn_decode(q, k_cache, v_cache, out, H, Hkv, hd, Lmax, pos, 1.0f / sqrtf((float)hd), work, counters,
-                              ctx->stream));
+    RT_HIP(launch_attn_combine(static_cast<const float*>(workspace), H, hd, attn_splits(Lmax), out, ctx->stream));
     return RT_OK;
 }
 
@@ -733,8 +748,13 @@ int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const r
     *out = nullptr;
     if (G <= 0 || G > (1 << 16)) return fail(RT_EINVAL, "rt_plan_create_fused: G out of range");
     if (!src->x) return fail(RT_EINVAL, "rt_plan_create_fused: source x is NULL");
-    if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRelu2Mul && src->mode != kRelu2MulNorm)
+    if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRelu2Mul && src->mode != kRelu2MulNorm &&
+        src->mode != kAttnNorm)
         return fail(RT_EINVAL, "rt_plan_create_fused: unknown source mode");
+    if (src->mode == kAttnNorm && (src->attn_head_dim <= 0 || src->attn_head_dim % 16 || src->attn_max_len <= 0 ||
+                                   !w[0] || w[0]->K % src->attn_head_dim))
+        return fail(RT_EINVAL, "rt_plan_create_fused: attention source needs head_dim (multiple of 16) dividing K "
+                               "and max_len");
     if ((src->mode != kQuant && !src->aux) || (src->mode == kRelu2MulNorm && !src->aux2))
         return fail(RT_EINVAL, "rt_plan_create_fused: the source mode needs aux/aux2");
     const int K = w[0] ? w[0]->K : 0;
@@ -756,7 +776,15 @@ int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const r
     p->U = 0;
     p->fused = true;
     p->pro = QuantProb{src->x, nullptr, nullptr, nullptr, nullptr, K, Kp, src->mode, src->aux, src->eps, nullptr,
-                       src->aux2};
+                       src->aux2, 0, 0};
+    if (src->mode == kAttnNorm) {
+        p->pro.attn_S = attn_splits(src->attn_max_len);
+        p->pro.attn_hd = src->attn_head_dim;
+        if ((size_t)(K / src->attn_head_dim) * (p->pro.attn_S + 1) * sizeof(float) > 32 * 1024) {
+            rt_plan_free(p);
+            return fail(RT_EINVAL, "rt_plan_create_fused: heads x splits too large for the LDS factor table");
+        }
+    }
     int wg = 0, minC = 1 << 30;
     p->probs.resize(G);
     for (int g = 0; g < G; ++g) {

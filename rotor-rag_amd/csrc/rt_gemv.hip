@@ -163,6 +163,7 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
     if constexpr (PRO) {
         v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
         RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (a.pro.Kp >> 4));
+        sm->fac = reinterpret_cast<float*>(sm + 1);  // kAttnNorm factors follow
         sx_pro = row_quantize<1>(a.pro, 0, lq, nullptr, nullptr, sm);
         __syncthreads();
         gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accN);
@@ -214,7 +215,8 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
     if (a.has_pro) {  // single token, prologue-quantised input: KSPLIT shape only
         if (mt != 1 || a.M != 1 || !shape.ksplit) return hipErrorInvalidValue;
         const dim3 grid((unsigned)a.total_rb, 1);
-        const size_t lds = (size_t)shape.nw * kRowBlock * sizeof(int) + (size_t)a.pro.Kp + sizeof(RowSmem);
+        size_t lds = (size_t)shape.nw * kRowBlock * sizeof(int) + (size_t)a.pro.Kp + sizeof(RowSmem);
+        if (a.pro.mode == kAttnNorm) lds += (size_t)(a.pro.K / a.pro.attn_hd) * (a.pro.attn_S + 1) * sizeof(float);
         hipLaunchKernelGGL((gemv_ksplit_kernel<1, true>), grid, block, lds, s, a);
     } else if (shape.ksplit) {
         const dim3 grid((unsigned)a.total_rb, mblocks);

@@ -45,7 +45,9 @@ inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 //   kRmsNorm  v = (x[k] / sqrt(mean_k x^2 + eps)) * norm_w[k], mean accumulated in f64
 //   kRelu2Mul v = x[k] > 0 ? (x[k] * x[k]) * u[k] : 0        (x = gate, u = up)
 //   kRelu2MulNorm  v = RMSNorm(relu2mul(x, u)) * norm_w       (norm_w = aux2)
-enum QuantMode { kQuant = 0, kPermute = 1, kRmsNorm = 2, kRelu2Mul = 3, kRelu2MulNorm = 4 };
+//   kAttnNorm v = RMSNorm(combined decode-attention partials x) * norm_w (aux),
+//             partials [K/hd heads][S][hd + 2]  (one token only)
+enum QuantMode { kQuant = 0, kPermute = 1, kRmsNorm = 2, kRelu2Mul = 3, kRelu2MulNorm = 4, kAttnNorm = 5 };
 
 struct QuantProb {
     const float* x;      // fp32 [M][K] (gate in kRelu2Mul)
@@ -59,6 +61,7 @@ struct QuantProb {
     float eps;
     float* v_out;        // optional fp32 [M][K]: the values that were quantised
     const float* aux2;   // norm_w [K] (kRelu2MulNorm)
+    int attn_S, attn_hd; // kAttnNorm: partial blocks per head, head dimension
 };
 
 // ---- one GEMV problem (a ternary matrix applied to M tokens) -------------------
@@ -126,8 +129,11 @@ hipError_t launch_rope_append(float* q, float* k, const float* v, float* Kc, flo
                               int H, int Hkv, int hd, int Lmax, const int* pos, hipStream_t s);
 hipError_t launch_attention(const float* q, const float* Kc, const float* Vc, float* out, int M, int H, int Hkv,
                             int hd, int Lmax, const int* pos, float scale, hipStream_t s);
-hipError_t launch_attn_decode(const float* q, const float* Kc, const float* Vc, float* out, int H, int Hkv, int hd,
-                              int Lmax, const int* pos, float scale, float* work, int* counters, hipStream_t s);
+// decode attention split over blocks of 64 keys: partials [H][S][hd + 2], S = attn_splits(Lmax)
+inline int attn_splits(int Lmax) { return (Lmax + 63) / 64; }
+hipError_t launch_attn_partial(const float* q, const float* Kc, const float* Vc, int H, int Hkv, int hd, int Lmax,
+                               const int* pos, float scale, float* work, hipStream_t s);
+hipError_t launch_attn_combine(const float* work, int H, int hd, int S, float* out, hipStream_t s);
 hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w, float eps, int V, int D,
                           float* logits, unsigned long long* best, int* token, int* pos, int advance,
                           int* next_ids, int* out_tokens, int pos_base, int out_cap, hipStream_t s);

@@ -11,7 +11,7 @@
 //
 // Floating-point contraction is off in this file so that a*b+c rounds twice, as the
 // NumPy model of the tests computes it.
-#include "rt_internal.h"
+#include "rt_rowquant.h"
 
 #pragma clang fp contract(off)
 
@@ -117,103 +117,90 @@ __global__ void __launch_bounds__(256) attention_kernel(const float* __restrict_
 
 // Decode attention, split over the keys: workgroup (h, s) handles keys
 // [64 s, 64 s + 64) of query head h for the single query at *pos_p and writes a partial
-// (running max, sum of exponentials, unnormalised output); the last of the S workgroups
-// of a head (atomic counter, reset afterwards) combines the partials.
-// work: [H][S][HD + 2] floats; counters: [H] ints, zero before the first launch.
+// result to work[h][s][0..HD+2): the unnormalised output sum_j e^(s_j - m) V_j (HD
+// values), the block maximum m and the sum of exponentials z (m = -inf, z = 0 for an
+// empty block).  The partials are combined by attn_combine_kernel or, in the decode
+// layer, by the prologue of the o_proj GEMV (rt_rowquant.h, kAttnNorm); both use
+// attn_combine_element, so the two give identical values.
 template <int HD>
-__global__ void __launch_bounds__(256) attn_decode_kernel(const float* __restrict__ q, const float* __restrict__ Kc,
-                                                          const float* __restrict__ Vc, float* __restrict__ out,
-                                                          int H, int Hkv, int Lmax, const int* __restrict__ pos_p,
-                                                          float scale, float* __restrict__ work,
-                                                          int* __restrict__ counters) {
+__global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restrict__ q, const float* __restrict__ Kc,
+                                                           const float* __restrict__ Vc, int H, int Hkv, int Lmax,
+                                                           const int* __restrict__ pos_p, float scale,
+                                                           float* __restrict__ work) {
     constexpr int BL = 64;
     __shared__ float qs[HD];
     __shared__ float part[4][BL];
     __shared__ float pr[BL];
     __shared__ float ored[256];
-    __shared__ int last;
     const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int kh = h / (H / Hkv), L = *pos_p + 1;
     const int j0 = s * BL, nk = min(BL, L - j0);  // keys of this block (may be <= 0)
     float* wp = work + ((size_t)h * S + s) * (HD + 2);
-    if (nk > 0) {
-        for (int d = t; d < HD; d += 256) qs[d] = q[(size_t)h * HD + d];
-        __syncthreads();
-        // scores: wave w sums dims [w*HD/4, (w+1)*HD/4) for key j0 + lane
-        const float* K = Kc + (size_t)kh * HD * Lmax + j0 + lane;
-        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-        if (lane < nk) {
+    if (nk <= 0) {
+        if (t == 0) {
+            wp[HD] = -INFINITY;
+            wp[HD + 1] = 0.0f;
+        }
+        return;
+    }
+    for (int d = t; d < HD; d += 256) qs[d] = q[(size_t)h * HD + d];
+    __syncthreads();
+    // scores: wave w sums dims [w*HD/4, (w+1)*HD/4) for key j0 + lane
+    const float* K = Kc + (size_t)kh * HD * Lmax + j0 + lane;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    if (lane < nk) {
 #pragma unroll
-            for (int d = wave * (HD / 4); d < (wave + 1) * (HD / 4); d += 4) {
-                a0 += qs[d + 0] * K[(size_t)(d + 0) * Lmax];
-                a1 += qs[d + 1] * K[(size_t)(d + 1) * Lmax];
-                a2 += qs[d + 2] * K[(size_t)(d + 2) * Lmax];
-                a3 += qs[d + 3] * K[(size_t)(d + 3) * Lmax];
-            }
+        for (int d = wave * (HD / 4); d < (wave + 1) * (HD / 4); d += 4) {
+            a0 += qs[d + 0] * K[(size_t)(d + 0) * Lmax];
+            a1 += qs[d + 1] * K[(size_t)(d + 1) * Lmax];
+            a2 += qs[d + 2] * K[(size_t)(d + 2) * Lmax];
+            a3 += qs[d + 3] * K[(size_t)(d + 3) * Lmax];
         }
-        part[wave][lane] = (a0 + a1) + (a2 + a3);
-        __syncthreads();
-        if (wave == 0) {
-            float sc = lane < nk ? (((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane])) * scale)
-                                 : -INFINITY;
-            float mx = sc;
-            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            const float p = lane < nk ? expf(sc - mx) : 0.0f;
-            float z = p;
-            for (int off = 32; off >= 1; off >>= 1) z += __shfl_xor(z, off, 64);
-            pr[lane] = p;
-            if (lane == 0) {
-                wp[HD] = mx;
-                wp[HD + 1] = z;
-            }
-        }
-        __syncthreads();
-        // unnormalised output: thread (d, g) sums keys g, g + G, ... of the block
-        constexpr int G = 256 / HD;
-        const int d = t % HD, g = t / HD;
-        const float* V = Vc + ((size_t)kh * Lmax + j0) * HD + d;
-        float o0 = 0.f, o1 = 0.f;
-        int j = g;
-        for (; j + G < nk; j += 2 * G) {
-            o0 += pr[j] * V[(size_t)j * HD];
-            o1 += pr[j + G] * V[(size_t)(j + G) * HD];
-        }
-        if (j < nk) o0 += pr[j] * V[(size_t)j * HD];
-        ored[t] = o0 + o1;
-        __syncthreads();
-        if (g == 0) {
-            float o = ored[d];
-            for (int gg = 1; gg < G; ++gg) o += ored[gg * HD + d];
-            wp[d] = o;
-        }
-    } else if (t == 0) {
-        wp[HD] = -INFINITY;
-        wp[HD + 1] = 0.0f;
     }
-    // publish the partial; the last workgroup of this head combines
-    __threadfence();
+    part[wave][lane] = (a0 + a1) + (a2 + a3);
     __syncthreads();
-    if (t == 0) last = atomicAdd(&counters[h], 1) == S - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    const float* wh = work + (size_t)h * S * (HD + 2);
-    float mx = -INFINITY;
-    for (int i = 0; i < S; ++i) mx = fmaxf(mx, wh[(size_t)i * (HD + 2) + HD]);
-    for (int d = t; d < HD; d += 256) {
-        float num = 0.0f, den = 0.0f;
-        for (int i = 0; i < S; ++i) {
-            const float* pi = wh + (size_t)i * (HD + 2);
-            const float m_i = pi[HD];
-            if (m_i == -INFINITY) continue;
-            const float f = expf(m_i - mx);
-            num += f * pi[d];
-            den += f * pi[HD + 1];
+    if (wave == 0) {
+        float sc = lane < nk ? (((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane])) * scale)
+                             : -INFINITY;
+        float mx = sc;
+        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        const float p = lane < nk ? expf(sc - mx) : 0.0f;
+        float z = p;
+        for (int off = 32; off >= 1; off >>= 1) z += __shfl_xor(z, off, 64);
+        pr[lane] = p;
+        if (lane == 0) {
+            wp[HD] = mx;
+            wp[HD + 1] = z;
         }
-        out[(size_t)h * HD + d] = num / den;
     }
-    if (t == 0) counters[h] = 0;
+    __syncthreads();
+    // unnormalised output: thread (d, g) sums keys g, g + G, ... of the block
+    constexpr int G = 256 / HD;
+    const int d = t % HD, g = t / HD;
+    const float* V = Vc + ((size_t)kh * Lmax + j0) * HD + d;
+    float o0 = 0.f, o1 = 0.f;
+    int j = g;
+    for (; j + G < nk; j += 2 * G) {
+        o0 += pr[j] * V[(size_t)j * HD];
+        o1 += pr[j + G] * V[(size_t)(j + G) * HD];
+    }
+    if (j < nk) o0 += pr[j] * V[(size_t)j * HD];
+    ored[t] = o0 + o1;
+    __syncthreads();
+    if (g == 0) {
+        float o = ored[d];
+        for (int gg = 1; gg < G; ++gg) o += ored[gg * HD + d];
+        wp[d] = o;
+    }
+}
+
+// out[h*hd + d] from the S partials of head h (one thread per output element)
+__global__ void __launch_bounds__(256) attn_combine_kernel(const float* __restrict__ work, int H, int hd, int S,
+                                                           float* __restrict__ out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H * hd) return;
+    out[i] = attn_combine_element(work, hd, S, i / hd, i % hd);
 }
 
 // Final RMSNorm (f64 mean of squares, as the quantiser's) fused into the tied bf16 LM
@@ -312,14 +299,19 @@ hipError_t launch_attention(const float* q, const float* Kc, const float* Vc, fl
     return hipGetLastError();
 }
 
-hipError_t launch_attn_decode(const float* q, const float* Kc, const float* Vc, float* out, int H, int Hkv, int hd,
-                              int Lmax, const int* pos, float scale, float* work, int* counters, hipStream_t s) {
-    const dim3 grid((unsigned)H, (unsigned)((Lmax + 63) / 64));
+hipError_t launch_attn_partial(const float* q, const float* Kc, const float* Vc, int H, int Hkv, int hd, int Lmax,
+                               const int* pos, float scale, float* work, hipStream_t s) {
+    const dim3 grid((unsigned)H, (unsigned)attn_splits(Lmax));
     switch (hd) {
-        case 64: hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(256), 0, s, q, Kc, Vc, out, H, Hkv, Lmax, pos, scale, work, counters); break;
-        case 128: hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(256), 0, s, q, Kc, Vc, out, H, Hkv, Lmax, pos, scale, work, counters); break;
+        case 64: hipLaunchKernelGGL(attn_partial_kernel<64>, grid, dim3(256), 0, s, q, Kc, Vc, H, Hkv, Lmax, pos, scale, work); break;
+        case 128: hipLaunchKernelGGL(attn_partial_kernel<128>, grid, dim3(256), 0, s, q, Kc, Vc, H, Hkv, Lmax, pos, scale, work); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_combine(const float* work, int H, int hd, int S, float* out, hipStream_t s) {
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)((H * hd + 255) / 256)), dim3(256), 0, s, work, H, hd, S, out);
     return hipGetLastError();
 }
 

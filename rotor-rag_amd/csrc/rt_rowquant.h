@@ -21,6 +21,7 @@ namespace rt {
 struct RowSmem {   // reduction scratch in LDS (one slot per wave)
     float f[16];
     double d[16];
+    float* fac;    // kAttnNorm: [heads][S] combine factors (-1 = empty block), then [heads] denominators
 };
 
 template <typename T, typename Op>
@@ -72,14 +73,91 @@ __device__ __forceinline__ void load_group(const float* __restrict__ xr, int g, 
     }
 }
 
-__device__ __forceinline__ bool has_norm(const QuantProb& P) { return P.mode == kRmsNorm || P.mode == kRelu2MulNorm; }
+__device__ __forceinline__ bool has_norm(const QuantProb& P) {
+    return P.mode == kRmsNorm || P.mode == kRelu2MulNorm || P.mode == kAttnNorm;
+}
 __device__ __forceinline__ bool has_relu2(const QuantProb& P) { return P.mode == kRelu2Mul || P.mode == kRelu2MulNorm; }
-__device__ __forceinline__ const float* norm_weight(const QuantProb& P) { return P.mode == kRmsNorm ? P.aux : P.aux2; }
+__device__ __forceinline__ const float* norm_weight(const QuantProb& P) {
+    return P.mode == kRelu2MulNorm ? P.aux2 : P.aux;
+}
+
+// Output element d of head h from decode-attention partials work[h][s][0..hd+2)
+// (unnormalised sum, block max, block sum of exponentials):
+// o = sum_s e^(m_s - m) o_s[d] / sum_s e^(m_s - m) z_s, m = max_s m_s, empty blocks skipped.
+__device__ __forceinline__ float attn_combine_element(const float* __restrict__ work, int hd, int S, int h, int d) {
+    const float* wh = work + (size_t)h * S * (hd + 2);
+    float mx = -INFINITY;
+    for (int i = 0; i < S; ++i) mx = fmaxf(mx, wh[(size_t)i * (hd + 2) + hd]);
+    float num = 0.0f, den = 0.0f;
+    for (int i = 0; i < S; ++i) {
+        const float* pi = wh + (size_t)i * (hd + 2);
+        const float m_i = pi[hd];
+        if (m_i == -INFINITY) continue;
+        const float f = expf(m_i - mx);
+        num += f * pi[d];
+        den += f * pi[hd + 1];
+    }
+    return num / den;
+}
 
 // The values of group g before any row-wide normalisation:
 // kQuant/kRmsNorm: x; kRelu2Mul(Norm): relu(gate)^2 * up.
+// kAttnNorm, per head h: the factor e^(m_s - m) of every partial block (-1 for an
+// empty block) and the denominator sum_s e^(m_s - m) z_s, in the operation order of
+// attn_combine_element.
+__device__ __forceinline__ void attn_factors(const QuantProb& P, float* fac) {
+    const int hd = P.attn_hd, S = P.attn_S, H = P.K / hd;
+    for (int h = threadIdx.x; h < H; h += blockDim.x) {
+        const float* wh = P.x + (size_t)h * S * (hd + 2);
+        float mx = -INFINITY;
+        for (int i = 0; i < S; ++i) mx = fmaxf(mx, wh[(size_t)i * (hd + 2) + hd]);
+        float den = 0.0f;
+        for (int i = 0; i < S; ++i) {
+            const float m_i = wh[(size_t)i * (hd + 2) + hd];
+            if (m_i == -INFINITY) {
+                fac[h * S + i] = -1.0f;
+                continue;
+            }
+            const float f = expf(m_i - mx);
+            fac[h * S + i] = f;
+            den += f * wh[(size_t)i * (hd + 2) + hd + 1];
+        }
+        fac[H * S + h] = den;
+    }
+}
+
 __device__ __forceinline__ void source_group(const QuantProb& P, const float* xr, const float* ur, int g, bool vec,
-                                             float (&v)[16]) {
+                                             float (&v)[16], const float* fac = nullptr) {
+    if (P.mode == kAttnNorm) {  // 16 consecutive elements of one head (hd % 16 == 0)
+        const int hd = P.attn_hd, S = P.attn_S, H = P.K / hd;
+        const int k0 = g * 16, h = k0 / hd, d0 = k0 % hd;
+        if (k0 >= P.K) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = 0.0f;
+            return;
+        }
+        float num[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) num[e] = 0.0f;
+        const float* wh = P.x + (size_t)h * S * (hd + 2) + d0;
+        for (int i = 0; i < S; ++i) {
+            const float f = fac[h * S + i];
+            if (f < 0.0f) continue;
+            const float4* p = reinterpret_cast<const float4*>(wh + (size_t)i * (hd + 2));
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 t = p[q4];
+                num[4 * q4 + 0] += f * t.x;
+                num[4 * q4 + 1] += f * t.y;
+                num[4 * q4 + 2] += f * t.z;
+                num[4 * q4 + 3] += f * t.w;
+            }
+        }
+        const float den = fac[H * S + h];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = num[e] / den;
+        return;
+    }
     load_group(xr, g, P.K, vec, v);
     if (has_relu2(P)) {
         float u[16];
@@ -143,16 +221,20 @@ __device__ __forceinline__ float row_quantize(const QuantProb& P, int m, v4u* qr
     const int K = P.K, groups = P.Kp >> 4, T = blockDim.x;
     const float* xr = P.x + (size_t)m * K;
     const float* ur = has_relu2(P) ? P.aux + (size_t)m * K : nullptr;
-    bool vec = (K & 15) == 0 && ((uintptr_t)xr & 15u) == 0;
+    bool vec = (K & 15) == 0 && ((uintptr_t)xr & 15u) == 0 && P.mode != kAttnNorm;
     if (ur) vec = vec && ((uintptr_t)ur & 15u) == 0;
     if (has_norm(P)) vec = vec && ((uintptr_t)norm_weight(P) & 15u) == 0;
     auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
     auto dadd_op = [](double x, double y) { return x + y; };
 
+    if (P.mode == kAttnNorm) {
+        attn_factors(P, sm->fac);
+        __syncthreads();
+    }
     if (groups <= REG * T) {  // the row stays in registers
         float v[REG][16];
 #pragma unroll
-        for (int r = 0; r < REG; ++r) source_group(P, xr, ur, threadIdx.x + r * T, vec, v[r]);
+        for (int r = 0; r < REG; ++r) source_group(P, xr, ur, threadIdx.x + r * T, vec, v[r], sm->fac);
         if (has_norm(P)) {
             double ss = 0.0;
 #pragma unroll
@@ -180,7 +262,7 @@ __device__ __forceinline__ float row_quantize(const QuantProb& P, int m, v4u* qr
         double ss = 0.0;
         for (int g = threadIdx.x; g < groups; g += T) {
             float v[16];
-            source_group(P, xr, ur, g, vec, v);
+            source_group(P, xr, ur, g, vec, v, sm->fac);
             ss = sumsq_group(v, ss);
         }
         ss = block_reduce(ss, sm->d, dadd_op);
@@ -189,7 +271,7 @@ __device__ __forceinline__ float row_quantize(const QuantProb& P, int m, v4u* qr
     float amax = 0.0f;
     for (int g = threadIdx.x; g < groups; g += T) {
         float v[16];
-        source_group(P, xr, ur, g, vec, v);
+        source_group(P, xr, ur, g, vec, v, sm->fac);
         if (has_norm(P)) rmsnorm_group(P, norm, g, vec, v);
         amax = amax_group(v, amax);
     }
@@ -197,7 +279,7 @@ __device__ __forceinline__ float row_quantize(const QuantProb& P, int m, v4u* qr
     const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
     for (int g = threadIdx.x; g < groups; g += T) {
         float v[16];
-        source_group(P, xr, ur, g, vec, v);
+        source_group(P, xr, ur, g, vec, v, sm->fac);
         if (has_norm(P)) rmsnorm_group(P, norm, g, vec, v);
         emit_group(v, s, g, K, qrow, qn, vo);
     }

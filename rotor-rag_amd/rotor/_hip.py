@@ -19,10 +19,10 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "librotor_hip.so"
 class RtSrc(ctypes.Structure):
     """rt_src of include/rotor_hip.h"""
     _fields_ = [("mode", ctypes.c_int), ("x", ctypes.c_void_p), ("aux", ctypes.c_void_p), ("aux2", ctypes.c_void_p),
-                ("eps", ctypes.c_float)]
+                ("eps", ctypes.c_float), ("attn_head_dim", ctypes.c_int), ("attn_max_len", ctypes.c_int)]
 
 
-SRC_QUANT, SRC_RMSNORM, SRC_RELU2MUL, SRC_RELU2MUL_NORM = 0, 2, 3, 4
+SRC_QUANT, SRC_RMSNORM, SRC_RELU2MUL, SRC_RELU2MUL_NORM, SRC_ATTN_NORM = 0, 2, 3, 4, 5
 
 # name -> (restype, argtypes); every entry point of include/rotor_hip.h
 _P = ctypes.c_void_p
@@ -68,6 +68,7 @@ SIGNATURES = {
     "rt_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "rt_attention_decode_workspace": (ctypes.c_size_t, [_I, _I, _I]),
     "rt_attention_decode": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t]),
+    "rt_attention_decode_partials": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t]),
     "rt_lm_head_argmax": (_I, [_P, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I]),
 }
 

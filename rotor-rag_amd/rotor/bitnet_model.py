@@ -191,7 +191,7 @@ class _DeviceModel:
         self.out_tokens = torch.zeros(self.Lmax, dtype=torch.int32, device=dev)
         lib = _hip.load()
         self.attn_ws_bytes = int(lib.rt_attention_decode_workspace(H, hd, self.Lmax))
-        self.attn_ws = torch.zeros(self.attn_ws_bytes, dtype=torch.uint8, device=dev)
+        self.attn_ws = torch.zeros(self.attn_ws_bytes, dtype=torch.uint8, device=dev)  # decode partials
         cap = model.max_tokens
         self.act_d = hip.activations(cap, D)
         self.act_f = hip.activations(cap, F)
@@ -214,9 +214,10 @@ class _DeviceModel:
                 h, o, g, u = st["h"][0], st["o"][0], st["g"][0], st["u"][0]
                 st["qkv"].append(hip.plan_fused([L["q_proj"], L["k_proj"], L["v_proj"]], _hip.SRC_RMSNORM, h,
                                                 L["input_norm"], eps=eps, ys=[st["q"][0], st["k"][0], st["v"][0]]))
-                if L["attn_sub_norm"] is not None:
-                    st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_RMSNORM, o, L["attn_sub_norm"], eps=eps,
-                                                       ys=[h], residuals=[h]))
+                if L["attn_sub_norm"] is not None:  # combine the attention partials + sub-norm in the prologue
+                    st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_ATTN_NORM, self.attn_ws,
+                                                       L["attn_sub_norm"], eps=eps, ys=[h], residuals=[h],
+                                                       attn_head_dim=self.hd, attn_max_len=self.Lmax))
                 else:
                     st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_QUANT, o, ys=[h], residuals=[h]))
                 st["gu"].append(hip.plan_fused([L["gate_proj"], L["up_proj"]], _hip.SRC_RMSNORM, h, L["post_norm"],
@@ -254,7 +255,12 @@ class _DeviceModel:
             chk(lib.rt_rope_kv_append(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
                                       L["vc"].data_ptr(), self.rope.data_ptr(), M, self.H, self.Hkv, self.hd,
                                       self.Lmax, self.pos.data_ptr()), "rt_rope_kv_append")
-            if M == 1:
+            if M == 1 and L["attn_sub_norm"] is not None:  # o_proj's prologue combines the partials
+                chk(lib.rt_attention_decode_partials(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(),
+                                                     self.H, self.Hkv, self.hd, self.Lmax, self.pos.data_ptr(),
+                                                     self.attn_ws.data_ptr(), self.attn_ws_bytes),
+                    "rt_attention_decode_partials")
+            elif M == 1:
                 chk(lib.rt_attention_decode(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), o.data_ptr(),
                                             self.H, self.Hkv, self.hd, self.Lmax, self.pos.data_ptr(),
                                             self.attn_ws.data_ptr(), self.attn_ws_bytes), "rt_attention_decode")

@@ -377,7 +377,8 @@ class HIPTernaryOps:
         _hip.check(self.lib.rt_plan_create_act(self.ctx, G, wa, aa, int(M), ya, ctypes.byref(h)), "rt_plan_create_act")
         return LinearPlan(self, h, (list(weights), list(acts), list(ys)))
 
-    def plan_fused(self, weights, mode: int, x, aux=None, aux2=None, eps: float = 1e-6, ys=None, residuals=None):
+    def plan_fused(self, weights, mode: int, x, aux=None, aux2=None, eps: float = 1e-6, ys=None, residuals=None,
+                   attn_head_dim: int = 0, attn_max_len: int = 0):
         """One-token plan whose single launch quantises its input row in the prologue:
         mode = _hip.SRC_QUANT / SRC_RMSNORM / SRC_RELU2MUL / SRC_RELU2MUL_NORM; x, aux, aux2
         device fp32 [K]; ys[g] fp32 [N_g] outputs (+ residuals[g])."""
@@ -388,11 +389,16 @@ class HIPTernaryOps:
         for w, y in zip(weights, ys):
             if w.in_features != K or y.numel() != w.out_features or not y.is_contiguous():
                 raise ValueError("plan_fused: shapes do not match")
-        for t in (x, aux, aux2):
+        for t in ((x if mode != _hip.SRC_ATTN_NORM else None), aux, aux2):
             if t is not None and (t.numel() < K or not t.is_contiguous() or t.device != self.device):
                 raise ValueError("plan_fused: source tensors must be contiguous device tensors of >= K elements")
+        if mode == _hip.SRC_ATTN_NORM:
+            need = self.lib.rt_attention_decode_workspace(K // max(attn_head_dim, 1), attn_head_dim, attn_max_len)
+            if attn_head_dim <= 0 or x.numel() * x.element_size() < need:
+                raise ValueError("plan_fused: attention partials buffer too small")
         src = _hip.RtSrc(int(mode), x.data_ptr(), aux.data_ptr() if aux is not None else None,
-                         aux2.data_ptr() if aux2 is not None else None, float(eps))
+                         aux2.data_ptr() if aux2 is not None else None, float(eps), int(attn_head_dim),
+                         int(attn_max_len))
         P = ctypes.c_void_p
         wa = (P * G)(*[w.handle for w in weights])
         ya = (P * G)(*[y.data_ptr() for y in ys])

@@ -107,8 +107,22 @@ def test_attention_decode_split(hip, pos0, H, Hkv, hd, Lmax):
     V = vc.cpu().numpy()[:, :pos0 + 1]
     o = O.causal_gqa_attention(q.cpu().numpy().reshape(1, H, hd), K, V, pos0).reshape(1, H * hd)
     np.testing.assert_allclose(out.cpu().numpy(), o, atol=2e-5, rtol=1e-4)
-    # counters were reset: the workspace tail is zero again
-    assert int(ws[nbytes - 4 * H:].sum()) == 0
+    # an o_proj plan that combines the partials in its prologue equals combine + norm + linear
+    from rotor import _hip as H_
+
+    W, sw = O.make_ternary(rng, 96, H * hd)
+    w = hip.upload(O.pack_rotor(W), H * hd, sw)
+    nw = torch.from_numpy(rng.uniform(0.5, 1.5, H * hd).astype(np.float32)).cuda()
+    res = torch.from_numpy(rng.standard_normal(96).astype(np.float32)).cuda()
+    y = res.clone()
+    plan = hip.plan_fused([w], H_.SRC_ATTN_NORM, ws, nw, eps=1e-6, ys=[y], residuals=[y], attn_head_dim=hd,
+                          attn_max_len=Lmax)
+    chk(lib.rt_attention_decode_partials(hip.ctx, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), H, Hkv, hd, Lmax,
+                                         pos.data_ptr(), ws.data_ptr(), nbytes))
+    plan.run()
+    act = hip.activations(1, H * hd)
+    hip.act_rmsnorm_quantize(out, nw, act, 1e-6)
+    assert torch.equal(y, hip.linear_act(w, act, residual=res[None])[0])
 
 
 @pytest.mark.parametrize("V,D", [(1000, 512), (5000, 2560), (777, 1024)])

@@ -275,7 +275,7 @@ static int check_act(const rt_ctx* ctx, int M, int K, const char* who) {
 }
 
 // Quantise (x != NULL) or permute (q_in != NULL) M rows of K into the context scratch.
-static int stage_activations(rt_ctx* ctx, const float* x, const int8_t* q_in, int M, int K, int Mpad,
+static int stage_activations(rt_ctx* ctx, const float* x, const int8_t* q_in, int M, int K, int Mpad, bool blocked,
                              int8_t* q_nat, float* s_out, int8_t** qx, float** sx) {
     const int Kp = round_up(K, kChunk);
     const size_t qbytes = (size_t)Mpad * Kp;
@@ -287,7 +287,8 @@ static int stage_activations(rt_ctx* ctx, const float* x, const int8_t* q_in, in
     a.U = 1;
     a.M = M;
     a.Mpad = Mpad;
-    a.p = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp, q_in ? kPermute : kQuant, nullptr, 0.0f, nullptr, nullptr, 0, 0};
+    a.p = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp, q_in ? kPermute : kQuant, nullptr, 0.0f, nullptr, nullptr, 0, 0,
+                    blocked};
     RT_HIP(launch_quant(a, ctx->stream));
     if (s_out) RT_HIP(hipMemcpyAsync(s_out, *sx, (size_t)M * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
     return RT_OK;
@@ -300,7 +301,7 @@ int rt_quantize_rows(rt_ctx* ctx, const float* x, int M, int K, int8_t* q, float
     DeviceGuard g(ctx->device);
     int8_t* qx;
     float* sx;
-    return stage_activations(ctx, x, nullptr, M, K, M, q, s, &qx, &sx);
+    return stage_activations(ctx, x, nullptr, M, K, M, false, q, s, &qx, &sx);
 }
 
 // GEMV (M <= kGemvMaxM) or MFMA GEMM on activations already in the qx layout.
@@ -335,7 +336,7 @@ static int run_linear(rt_ctx* ctx, const rt_weights* w, const float* x, const in
     DeviceGuard g(ctx->device);
     int8_t* qx;
     float* sx;
-    rc = stage_activations(ctx, x, q, M, w->K, act_rows(M), nullptr, nullptr, &qx, &sx);
+    rc = stage_activations(ctx, x, q, M, w->K, act_rows(M), qx_blocked(M), nullptr, nullptr, &qx, &sx);
     if (rc) return rc;
     return launch_matrix(ctx, w, qx, sx, M, row_scale, out, out_i32);
 }
@@ -428,7 +429,7 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
         const int u = which[g];
         p->quant[u] = QuantProb{x[g], nullptr, reinterpret_cast<int8_t*>(base + qoff[u]),
                                 reinterpret_cast<float*>(base + soff[u]), nullptr, Ku[u], round_up(Ku[u], kChunk),
-                                kQuant, nullptr, 0.0f, nullptr, nullptr, 0, 0};
+                                kQuant, nullptr, 0.0f, nullptr, nullptr, 0, 0, qx_blocked(M)};
     }
     int wg = 0, minC = 1 << 30;
     p->probs.resize(G);
@@ -552,7 +553,8 @@ static int act_fill(rt_ctx* ctx, rt_act* act, int M, int mode, const float* x, c
     q.U = 1;
     q.M = M;
     q.Mpad = act_rows(M);
-    q.p = QuantProb{x, nullptr, act->qx, act->sx, nullptr, act->K, act->Kp, mode, aux, eps, v_out, aux2, 0, 0};
+    q.p = QuantProb{x, nullptr, act->qx, act->sx, nullptr, act->K, act->Kp, mode, aux, eps, v_out, aux2, 0, 0,
+                    qx_blocked(M)};
     RT_HIP(launch_quant(q, ctx->stream));
     act->M = M;
     act->Mpad = q.Mpad;
@@ -584,7 +586,7 @@ int rt_act_export(rt_ctx* ctx, const rt_act* act, int8_t* q, float* s) {
     if (!ctx || !act || !q || !s) return fail(RT_EINVAL, "rt_act_export: NULL argument");
     if (act->M <= 0) return fail(RT_EINVAL, "rt_act_export: activations are empty");
     DeviceGuard g(ctx->device);
-    RT_HIP(launch_unpermute(act->qx, act->M, act->K, act->Kp, q, ctx->stream));
+    RT_HIP(launch_unpermute(act->qx, act->M, act->K, act->Kp, qx_blocked(act->M), q, ctx->stream));
     RT_HIP(hipMemcpyAsync(s, act->sx, (size_t)act->M * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
     return RT_OK;
 }

@@ -1,142 +1,326 @@
 // Prefill / batched ternary GEMM on the int8 matrix cores (gfx950 MFMA):
 // C[M,N] = A[M,K] x W[N,K]^T with A the per-token quantised activations (qx layout)
 // and W the rotor weight tiles, int32 accumulation, fp32 rescale epilogue.
-// Replaces, for M >= 16 tokens, the reference's per-token loop
+// Replaces, for M > 8 tokens, the reference's per-token loop
 // (src/rotor/transformer.py:134-143) and its CPU sgemm (src/rotor/transformer.py:150).
 //
-// Workgroup tile BM x 128 x (K step 64), 4 waves in a 2 x 2 arrangement, each wave
-// (BM/2) x 64 of v_mfma_i32_16x16x64_i8.  Per K step:
-//   * A: BM rows x 64 int8 of qx go global -> registers -> LDS;
-//   * W: the two 64-row blocks of the tile are one coalesced 1 KiB chunk each; 128
-//     threads decode one 16-byte chunk (64 weights) each to int8 and store them to LDS
-//     in the same permuted k order as qx (so operand bytes pair up one to one);
-//   * the next step's global loads are issued before this step's MFMAs.
-// The MFMA consumes, per lane, 16 bytes of one A row and 16 bytes of one W row at the
-// same k positions, so any consistent assignment of k to (lane group, byte) gives the
-// exact sum; the result layout used is D[4*(lane/16) + i][lane % 16], i = 0..3.
+// Workgroup: 4 waves (WAVES_M x WAVES_N), tile BM x BN, K step 64 (one weight chunk) =
+// two k-slices of v_mfma_i32_32x32x32_i8 (this shape runs at full rate from one wave
+// per SIMD, which the large tiles here need: 256 accumulator registers per lane).
+//   * Operands reach LDS by direct global->LDS loads (global_load_lds_dwordx4) into a
+//     ring of STAGES stages, STAGES steps ahead.  A barrier per step publishes the next
+//     stage (each wave first waits for its own loads of it: s_waitcnt vmcnt) and retires
+//     the stage just read, which the next loads then refill.
+//   * A (blocked qx layout) is stored as 1 KiB 16-row x 64-k blocks in operand order
+//     (lane l: row l % 16, bytes 16 (l / 16) .. +15): one load copies a block to LDS with
+//     contiguous 16-byte lanes.  The MFMA lane l wants
+//     row l % 32, bytes 32 h + 16 (l / 32) .. +15 of slice h: one ds_read_b128, every
+//     group of 8 lanes reading 128 contiguous bytes (conflict-free).
+//   * W stays 2-bit in LDS (a 64-row block's chunk is 1 KiB, copied as is).  The 16
+//     weights an MFMA lane needs are one dword of its row's 16-byte unit: ds_read_b32
+//     and four v_perm_b32 expand it to int8 in the qx order.
+//   * Software pipeline per step c: MFMAs of slice 0; barrier; loads of step
+//     c + STAGES; fragment reads of step c + 1; MFMAs of slice 1 (hiding the reads);
+//     weight expansion of step c + 1.
+//   * Tiles are ordered m-major and dealt to the 8 XCDs in contiguous ranges
+//     (workgroup i runs on XCD i % 8), so the workgroups sharing an A row tile share an
+//     L2.
+// Both operands assign k to (lane group, byte) the same way, so the int32 sums are exact
+// whatever that assignment is; the result layout of a 32x32 block is
+// D[8 (k / 4) + 4 (lane / 32) + k % 4][lane % 32], k = 0..15.
+#include <type_traits>
+
 #include "rt_internal.h"
+
+// the epilogue rounds ((float)acc * sx) * sw, then adds the residual, as separate IEEE ops
+#pragma clang fp contract(off)
 
 namespace rt {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr unsigned kLut = 0x0001FF00u;  // v_perm_b32 src1: field 0,1,2,3 -> 00, FF, 01, 00
-constexpr int kBN = 128;
-constexpr int kLdsRow = 80;             // 64 bytes + 16 pad per LDS row (bank spread)
+constexpr int kXcds = 8;
 
-// 16 weight bytes (64 rotor codes) -> 64 int8 weights in qx order: dword j of the
-// source gives output dwords 4j..4j+3 = elements {16j+4b+i : b=0..3}, i = 0..3.
-__device__ __forceinline__ void decode_chunk(const v4u v, v4u (&o)[4]) {
+// one dword of rotor code (16 weights, byte b holds elements 4b..4b+3 at bits 2i) -> 16
+// int8 weights in the qx order of a 16-group: output byte 4i + b = element 4b + i
+__device__ __forceinline__ v4i decode_dword(unsigned u) {
+    v4i o;
+    o[0] = (int)__builtin_amdgcn_perm(0u, kLut, u & 0x03030303u);
+    o[1] = (int)__builtin_amdgcn_perm(0u, kLut, (u >> 2) & 0x03030303u);
+    o[2] = (int)__builtin_amdgcn_perm(0u, kLut, (u >> 4) & 0x03030303u);
+    o[3] = (int)__builtin_amdgcn_perm(0u, kLut, (u >> 6) & 0x03030303u);
+    return o;
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l's bytes land at
+// lds + 16 l (lds wave-uniform)
+__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)lds, 16, 0, 0);
+}
+
+// Wait until at most N of this wave's vector-memory loads are outstanding and all of
+// its LDS reads have returned, then barrier.  The scheduler moves nothing across.
+template <int N>
+__device__ __forceinline__ void wait_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int BM, int BN, int WAVES_M, int STAGES>
+struct GemmTile {
+    static constexpr int WAVES_N = 4 / WAVES_M;
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+    static constexpr int FI = WM / 32, FJ = WN / 32;  // 32 x 32 blocks per wave
+    static constexpr int LA = BM / 64;                // A loads (16-row blocks) per wave per step
+    static constexpr int RB = BN / kRowBlock;         // weight row blocks per tile
+    // W region: one 1 KiB slot per wave (waves past the tile's row blocks fill a spare
+    // slot, so every wave issues the same loads per step)
+    static constexpr int A_BYTES = BM * 64, STAGE_BYTES = A_BYTES + 4 * 1024;
+    static constexpr int SX_OFF = STAGES * STAGE_BYTES;  // BM row scales after the ring
+    static constexpr int LDS_BYTES = SX_OFF + BM * 4;
+    static_assert(WAVES_M * WAVES_N == 4 && FI >= 1 && FJ >= 1 && LA >= 1 && RB >= 1 && RB <= 4, "tile shape");
+    static_assert(STAGES >= 2, "ring depth");
+};
+
+// Writes a wave's FI x FJ blocks.  EPI 0: int32 accumulators; 1: fp32
+// acc * sx[m] * s_w; 2: as 1 plus the residual.  Output (and residual) rows are raw
+// buffers from the tile's first row m0 to row min(m0 + BM, M): rows past M fall outside
+// the range and the hardware drops those stores; a column past N adds bit 31 to the
+// offset (row and column terms stay below 2^31), which puts it outside as well.
+// mrow: this lane's first row relative to m0 (includes 4 (lane / 32)); nb: first column.
+template <int FI, int FJ, int EPI>
+__device__ __forceinline__ void store_tile(const v16i (&acc)[FI][FJ], const GemmArgs& a, int m0, int rows, int mrow,
+                                           int nb, const float* sx_lds, const float (&swv)[FJ]) {
+    const unsigned range = (unsigned)rows * (unsigned)a.ldo * 4u;
+    const __amdgpu_buffer_rsrc_t out =
+        __builtin_amdgcn_make_buffer_rsrc(static_cast<char*>(a.out) + (size_t)m0 * a.ldo * 4, 0, range, kBufDword3);
+    const __amdgpu_buffer_rsrc_t res = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.res ? a.res + (size_t)m0 * a.ldo : nullptr), 0, EPI == 2 ? range : 0u, kBufDword3);
+    int coff[FJ];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const unsigned u = v[j];
-        o[j][0] = __builtin_amdgcn_perm(0u, kLut, u & 0x03030303u);
-        o[j][1] = __builtin_amdgcn_perm(0u, kLut, (u >> 2) & 0x03030303u);
-        o[j][2] = __builtin_amdgcn_perm(0u, kLut, (u >> 4) & 0x03030303u);
-        o[j][3] = __builtin_amdgcn_perm(0u, kLut, (u >> 6) & 0x03030303u);
+    for (int j = 0; j < FJ; ++j) {
+        const int n = nb + j * 32;
+        coff[j] = (int)((unsigned)n * 4u + ((unsigned)(n >= a.N) << 31));
+    }
+    const int row_bytes = a.ldo * 4;
+#pragma unroll
+    for (int i = 0; i < FI; ++i) {
+        float sxv[16];
+        if (EPI) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {  // rows mrow + 32 i + 8 q + 0..3
+                const v4f s4 = *reinterpret_cast<const v4f*>(sx_lds + mrow + i * 32 + q * 8);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sxv[q * 4 + r] = s4[r];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FJ; ++j) {
+            int off[16];
+            float rv[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                off[k] = (mrow + i * 32 + 8 * (k >> 2) + (k & 3)) * row_bytes + coff[j];
+                if (EPI == 2) rv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(res, off[k], 0, 0));
+            }
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                unsigned bits;
+                if (EPI == 0) {
+                    bits = (unsigned)acc[i][j][k];
+                } else {
+                    const float y = ((float)acc[i][j][k] * sxv[k]) * swv[j];
+                    bits = __builtin_bit_cast(unsigned, EPI == 2 ? rv[k] + y : y);
+                }
+                __builtin_amdgcn_raw_buffer_store_b32(bits, out, off[k], 0, 0);
+            }
+        }
     }
 }
 
-template <int BM>
+template <int BM, int BN, int WAVES_M, int STAGES>
 __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
-    constexpr int WM = BM / 2;          // rows per wave
-    constexpr int FI = WM / 16;         // A fragments per wave
-    constexpr int FJ = 4;               // W fragments per wave (64 columns)
-    constexpr int AL = BM * 4 / 256;    // 16-byte A loads per thread per step
-    __shared__ __attribute__((aligned(16))) int8_t As[BM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[kBN * kLdsRow];
+    using T = GemmTile<BM, BN, WAVES_M, STAGES>;
+    constexpr int FI = T::FI, FJ = T::FJ, LA = T::LA;
+    extern __shared__ __attribute__((aligned(16))) v4u lds[];
 
-    const int t = threadIdx.x, lane = t & 63;
+    const int t = threadIdx.x, lane = t & 63, g = lane >> 5, r32 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const int n0 = blockIdx.x * kBN, m0 = blockIdx.y * BM;
-    const int C = a.C, Kp = C * 64, Nb = a.Np / kRowBlock;
+    const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
+    const int C = a.C, Nb = a.Np / kRowBlock;
 
-    // global sources of this thread
-    const v4u* a_src[AL];  // qx rows are 16-byte aligned (Kp is a multiple of 64)
+    // tile of this workgroup: m-major order, contiguous ranges per XCD
+    const int nT = (a.N + BN - 1) / BN, tiles = (int)gridDim.x;
+    const int L = blockIdx.x, xcd = L % kXcds, base = tiles / kXcds, rem = tiles % kXcds;
+    const int tile = xcd * base + min(xcd, rem) + L / kXcds;
+    const int m0 = (tile / nT) * BM, n0 = (tile % nT) * BN;
+    char* const lds_b = reinterpret_cast<char*>(lds);
+    float* const sx_lds = reinterpret_cast<float*>(lds_b + T::SX_OFF);
+
+    // row scales of the tile into LDS (sx holds the padded rows), published by the
+    // barrier before the epilogue; column scales into registers
+    if (!a.out_i32 && t < BM) sx_lds[t] = a.sx[m0 + t];
+    const int mrow = wm * T::WM + 4 * g, nb = n0 + wn * T::WN + r32;
+    float swv[FJ];
 #pragma unroll
-    for (int i = 0; i < AL; ++i) {
-        const int idx = t + i * 256, row = idx >> 2, seg = idx & 3;
-        a_src[i] = reinterpret_cast<const v4u*>(a.qx) + ((size_t)(m0 + row) * Kp >> 4) + seg;
+    for (int j = 0; j < FJ; ++j) swv[j] = a.out_i32 ? 0.f : a.rs ? a.rs[min(nb + j * 32, a.N - 1)] : a.s_w;
+
+    // this lane's global sources; the wave's LDS destinations
+    const int8_t* a_src[LA];
+#pragma unroll
+    for (int k = 0; k < LA; ++k) {
+        const int f = wave + 4 * k;  // 16-row block f
+        a_src[k] = a.qx + ((size_t)((m0 >> 4) + f) * C) * 1024 + lane * 16;  // blocked qx
     }
-    const int w_rb = n0 / kRowBlock + (t >> 6);  // threads 0..127: row block of the tile
-    const bool w_ok = t < 128 && w_rb < Nb;
-    const v4u* w_src = a.w + (size_t)w_rb * C * kRowBlock + (t & 63);
+    // weight row block of this wave's slot: clamped to a valid block (a wave past the
+    // tile's blocks, or past N, loads data nobody reads)
+    const int w_rb = min(n0 / kRowBlock + min(wave, T::RB - 1), Nb - 1);
+    const v4u* w_src = a.w + (size_t)w_rb * C * kRowBlock + lane;
+    constexpr int kLoads = LA + 1;  // loads per wave per step
 
-    v4u ra[AL], rw = {0u, 0u, 0u, 0u};
-    auto gload = [&](int c) {
+    auto issue = [&](int c) {
+        char* st = lds_b + (c % STAGES) * T::STAGE_BYTES;
 #pragma unroll
-        for (int i = 0; i < AL; ++i) ra[i] = a_src[i][c * 4];
-        if (w_ok) rw = __builtin_nontemporal_load(w_src + (size_t)c * kRowBlock);
+        for (int k = 0; k < LA; ++k) load_lds16(a_src[k] + (size_t)c * 1024, st + (wave + 4 * k) * 1024);
+        load_lds16(w_src + (size_t)c * kRowBlock, st + T::A_BYTES + wave * 1024);
     };
 
-    v4i acc[FI][FJ];
+    // per-lane LDS read offsets inside a stage (slice h adds 512 for A, 8 for W)
+    const int a_rd = ((wm * T::WM + r32) >> 4) * 1024 + ((r32 & 15) + 16 * g) * 16;
+    int w_rd[FJ];
 #pragma unroll
-    for (int i = 0; i < FI; ++i)
-#pragma unroll
-        for (int j = 0; j < FJ; ++j) acc[i][j] = v4i{0, 0, 0, 0};
-
-    gload(0);
-    for (int c = 0; c < C; ++c) {
-        __syncthreads();  // previous step's fragments are consumed
-#pragma unroll
-        for (int i = 0; i < AL; ++i) {
-            const int idx = t + i * 256, row = idx >> 2, seg = idx & 3;
-            *reinterpret_cast<v4u*>(As + row * kLdsRow + seg * 16) = ra[i];
-        }
-        if (t < 128) {
-            v4u o[4];
-            decode_chunk(rw, o);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) *reinterpret_cast<v4u*>(Bs + t * kLdsRow + j * 16) = o[j];
-        }
-        __syncthreads();
-        if (c + 1 < C) gload(c + 1);  // in flight during the MFMAs
-
-        const int kseg = (lane >> 4) * 16, r16 = lane & 15;
-        v4i fa[FI], fb[FJ];
-#pragma unroll
-        for (int i = 0; i < FI; ++i)
-            fa[i] = *reinterpret_cast<const v4i*>(As + (wm * WM + i * 16 + r16) * kLdsRow + kseg);
-#pragma unroll
-        for (int j = 0; j < FJ; ++j)
-            fb[j] = *reinterpret_cast<const v4i*>(Bs + (wn * 64 + j * 16 + r16) * kLdsRow + kseg);
-#pragma unroll
-        for (int i = 0; i < FI; ++i)
-#pragma unroll
-            for (int j = 0; j < FJ; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+    for (int j = 0; j < FJ; ++j) {
+        const int n = wn * T::WN + j * 32 + r32;
+        w_rd[j] = T::A_BYTES + (n >> 6) * 1024 + (n & 63) * 16 + g * 4;
     }
 
-    // epilogue: D[4*(lane/16) + r][lane % 16] of every 16x16 fragment
+    // Fragments of two steps (current p, next 1 - p): A per slice and block row, W raw
+    // and expanded.  Index [p][h * F + block].
+    v4i fa[2][2 * FI], fb[2][2 * FJ];
+    unsigned wraw[2][2 * FJ];
+    // read item r of step c into set p: W pairs (both slices of block j) first, then A
+    auto read_item = [&](int p, int c, int r) {
+        const char* st = lds_b + (c % STAGES) * T::STAGE_BYTES;
+        if (r < FJ) {
+            wraw[p][r] = *reinterpret_cast<const unsigned*>(st + w_rd[r]);
+            wraw[p][FJ + r] = *reinterpret_cast<const unsigned*>(st + w_rd[r] + 8);
+        } else {
+            const int h = (r - FJ) / FI, i = (r - FJ) % FI;
+            fa[p][h * FI + i] = *reinterpret_cast<const v4i*>(st + a_rd + i * 2048 + h * 512);
+        }
+    };
+    auto issue_item = [&](int c, int k) {  // load k of step c (A blocks, then W)
+        char* st = lds_b + (c % STAGES) * T::STAGE_BYTES;
+        if (k < LA) load_lds16(a_src[k] + (size_t)c * 1024, st + (wave + 4 * k) * 1024);
+        else load_lds16(w_src + (size_t)c * kRowBlock, st + T::A_BYTES + wave * 1024);
+    };
+
+    v16i acc[FI][FJ];
 #pragma unroll
     for (int i = 0; i < FI; ++i)
 #pragma unroll
-        for (int j = 0; j < FJ; ++j)
+        for (int j = 0; j < FJ; ++j) acc[i][j] = v16i{};
+
+    // prologue: fill the ring, publish step 0, read and expand it
+    for (int c = 0; c < STAGES && c < C; ++c) issue(c);
+    if (C >= STAGES) wait_barrier<(STAGES - 1) * kLoads>();
+    else wait_barrier<0>();
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm * WM + i * 16 + 4 * (lane >> 4) + r;
-                const int n = n0 + wn * 64 + j * 16 + (lane & 15);
-                if (m >= a.M || n >= a.N) continue;
-                const int v = acc[i][j][r];
-                if (a.out_i32) {
-                    static_cast<int*>(a.out)[(size_t)m * a.ldo + n] = v;
-                } else {
-                    const float sw = a.rs ? a.rs[n] : a.s_w;
-                    const size_t o = (size_t)m * a.ldo + n;
-                    const float y = ((float)v * a.sx[m]) * sw;
-                    static_cast<float*>(a.out)[o] = a.res ? a.res[o] + y : y;
-                }
+    for (int r = 0; r < 2 * FI + FJ; ++r) read_item(0, 0, r);
+#pragma unroll
+    for (int u = 0; u < 2 * FJ; ++u) fb[0][u] = decode_dword(wraw[0][u]);
+
+    // Step c (fragments in set p).  MODE 0 (steady): publish step c + 1 (every wave's
+    // reads of step c returned, so step c's stage takes step c + STAGES), read step
+    // c + 1, load step c + STAGES, expand step c + 1's weights.  MODE 1 (tail): the same
+    // without loads.  MODE 2: last step, MFMAs only.
+    // The wave issues in order and an MFMA holds the matrix core 32 cycles, so the
+    // other work is dealt out evenly between the step's MFMAs: the LDS reads (weights
+    // first), the loads, then the weight expansion one output dword at a time (2-3 VALU
+    // ops of 4 cycles).  Fences pin the order; each body is one basic block.
+    constexpr int kMfma = 2 * FI * FJ, kReads = 2 * FI + FJ, kQuarters = 8 * FJ;
+    auto body = [&](auto P, auto MODE, int c) {
+        constexpr int p = decltype(P)::value, mode = decltype(MODE)::value;
+        constexpr int nRd = mode == 2 ? 0 : kReads, nLd = mode == 0 ? kLoads : 0, nDec = mode == 2 ? 0 : kQuarters;
+        constexpr int nItems = nRd + nLd + nDec;
+        if (mode == 0) wait_barrier<(STAGES - 2) * kLoads>();
+        if (mode == 1) wait_barrier<0>();
+        auto item = [&](int t) {
+            if (t < nRd) {
+                read_item(1 - p, c + 1, t);
+            } else if (t < nRd + nLd) {
+                issue_item(c + STAGES, t - nRd);
+            } else {
+                const int d = t - nRd - nLd, u = d >> 2, q = d & 3;  // dword u, output q
+                fb[1 - p][u][q] = (int)__builtin_amdgcn_perm(0u, kLut, (wraw[1 - p][u] >> (2 * q)) & 0x03030303u);
             }
+        };
+#pragma unroll
+        for (int m = 0; m < kMfma; ++m) {
+            const int h = m / (FI * FJ), i = (m / FJ) % FI, j = m % FJ;
+            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[p][h * FI + i], fb[p][h * FJ + j], acc[i][j], 0, 0, 0);
+            // items [m * nItems / kMfma, (m + 1) * nItems / kMfma) follow MFMA m
+#pragma unroll
+            for (int t = m * nItems / kMfma; t < (m + 1) * nItems / kMfma; ++t) {
+                __builtin_amdgcn_sched_barrier(0);
+                item(t);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // steps [c0, c1) in MODE; the register set follows the step's parity
+    auto run = [&](auto MODE, int c0, int c1) {
+        int c = c0;
+        if (c < c1 && (c & 1)) body(std::integral_constant<int, 1>{}, MODE, c++);
+        for (; c + 1 < c1; c += 2) {
+            body(std::integral_constant<int, 0>{}, MODE, c);
+            body(std::integral_constant<int, 1>{}, MODE, c + 1);
+        }
+        if (c < c1) body(std::integral_constant<int, 0>{}, MODE, c);
+    };
+    const int steady_end = max(C - STAGES, 0);
+    run(std::integral_constant<int, 0>{}, 0, steady_end);
+    run(std::integral_constant<int, 1>{}, steady_end, C - 1);
+    run(std::integral_constant<int, 2>{}, C - 1, C);
+
+    // epilogue (this barrier publishes the row scales)
+    wait_barrier<0>();
+    const int rows = min(BM, a.M - m0);
+    if (a.out_i32) store_tile<FI, FJ, 0>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
+    else if (a.res) store_tile<FI, FJ, 2>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
+    else store_tile<FI, FJ, 1>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
+}
+
+template <int BM, int BN, int WAVES_M, int STAGES>
+static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
+    using T = GemmTile<BM, BN, WAVES_M, STAGES>;
+    if (T::LDS_BYTES > 65536) {
+        static const hipError_t attr =
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WAVES_M, STAGES>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
+        if (attr != hipSuccess) return attr;
+    }
+    const long long tiles = (long long)((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WAVES_M, STAGES>), dim3((unsigned)tiles), dim3(256), T::LDS_BYTES, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.M <= 0 || a.N <= 0) return hipSuccess;
+    // byte offsets inside one tile's rows are 32-bit
+    if ((long long)gemm_bm(a.M) * a.ldo * 4 >= (1ll << 31)) return hipErrorInvalidValue;
+    // the row tile divides gemm_bm(M), which sized the activation padding
     const int bm = gemm_bm(a.M);
-    const dim3 grid((unsigned)((a.N + kBN - 1) / kBN), (unsigned)((a.M + bm - 1) / bm));
-    if (bm == 64) hipLaunchKernelGGL(gemm_kernel<64>, grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(gemm_kernel<128>, grid, dim3(256), 0, s, a);
-    return hipGetLastError();
+    if (bm == 64) return launch_tile<64, 64, 2, 4>(a, s);
+    if (bm == 128) return launch_tile<128, 128, 2, 4>(a, s);
+    const long long wide = (long long)((a.N + 255) / 256) * ((a.M + 255) / 256);
+    if (wide >= 192) return launch_tile<256, 256, 2, 4>(a, s);
+    return launch_tile<256, 128, 2, 4>(a, s);
 }
 
 }  // namespace rt

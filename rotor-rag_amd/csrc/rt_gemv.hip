@@ -29,11 +29,13 @@
 // so element positions 0/2 accumulate into accP and 1/3 into accN, acc = accP - accN.
 #include "rt_rowquant.h"
 
+// every fp32 operation rounds on its own, as the reference restatement computes them
+#pragma clang fp contract(off)
+
 namespace rt {
 
 constexpr unsigned kLutLo = 0x0001FF00u;  // src1 of v_perm_b32
 constexpr unsigned kLutHi = 0x00000001u;  // src0 of v_perm_b32
-constexpr int kBufDword3 = 0x00020000;    // buffer resource word 3 for gfx9 raw buffers
 constexpr int kAuxNT = 2;                 // cache policy: non-temporal (streamed once)
 
 // The activations are read-only for the whole launch, so the constant address space
@@ -164,7 +166,7 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
         v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
         RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (a.pro.Kp >> 4));
         sm->fac = reinterpret_cast<float*>(sm + 1);  // kAttnNorm factors follow
-        sx_pro = row_quantize<1>(a.pro, 0, lq, nullptr, nullptr, sm);
+        sx_pro = row_quantize<1>(a.pro, 0, QxRow{lq, 4, 1}, nullptr, nullptr, sm);
         __syncthreads();
         gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accN);
     } else {

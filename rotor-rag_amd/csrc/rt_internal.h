@@ -62,6 +62,7 @@ struct QuantProb {
     float* v_out;        // optional fp32 [M][K]: the values that were quantised
     const float* aux2;   // norm_w [K] (kRelu2MulNorm)
     int attn_S, attn_hd; // kAttnNorm: partial blocks per head, head dimension
+    int blocked;         // qx layout: 0 rows, 1 blocked (see qx_blocked)
 };
 
 // ---- one GEMV problem (a ternary matrix applied to M tokens) -------------------
@@ -110,15 +111,24 @@ struct GemmArgs {
     const float* res;    // optional fp32 [M][ldo] added to y (may alias out)
 };
 
+constexpr int kBufDword3 = 0x00020000;  // buffer resource word 3 for gfx9 raw buffers
 constexpr int kGemvMaxM = 8;  // up to this many tokens: VALU GEMV; beyond: MFMA GEMM
-inline int gemm_bm(int M) { return M <= 64 ? 64 : 128; }
+// qx layout.  Rows (M <= kGemvMaxM, read by the GEMV): row m at m * Kp.  Blocked
+// (M > kGemvMaxM, read by the MFMA GEMM): 16-row x 64-k blocks of 1 KiB, block
+// (m / 16, c) at (m / 16 * C + c) * 1024, where the 16-byte group q (k = 16 q .. 16 q + 15
+// of chunk c) of row m sits at ((m % 16) + 16 q) * 16: the block is laid out as the
+// matrix-core operand fragments, so the GEMM copies it to LDS with contiguous loads.
+inline bool qx_blocked(int M) { return M > kGemvMaxM; }
+
+// rows of the GEMM workgroup tile for M tokens (the activations are zero-padded to it)
+inline int gemm_bm(int M) { return M <= 64 ? 64 : M <= 128 ? 128 : 256; }
 
 // Launchers (return hipSuccess or the launch error).
 hipError_t launch_relayout(const uint8_t* src, int N, int K, v4u* tiles, hipStream_t s);
 hipError_t launch_unrelayout(const v4u* tiles, int N, int K, uint8_t* dst, hipStream_t s);
 hipError_t launch_quant(const QuantArgs& a, hipStream_t s);
 // qx rows [M][Kp] (permuted) -> natural-order int8 [M][K]
-hipError_t launch_unpermute(const int8_t* qx, int M, int K, int Kp, int8_t* q, hipStream_t s);
+hipError_t launch_unpermute(const int8_t* qx, int M, int K, int Kp, bool blocked, int8_t* q, hipStream_t s);
 // mt = tokens per workgroup (1, 2, 4 or 8).
 hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);

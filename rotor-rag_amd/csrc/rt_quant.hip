@@ -6,6 +6,9 @@
 // One 256-thread workgroup per token row; rows in [M, Mpad) are zero-filled.
 #include "rt_rowquant.h"
 
+// every fp32 operation rounds on its own, as the reference restatement computes them
+#pragma clang fp contract(off)
+
 namespace rt {
 
 __device__ __forceinline__ QuantProb select_quant(const QuantArgs& a, int i) { return a.dev ? a.dev[i] : a.p; }
@@ -15,7 +18,9 @@ __global__ void __launch_bounds__(256) quant_kernel(QuantArgs a) {
     const QuantProb P = select_quant(a, blockIdx.y);
     const int m = blockIdx.x;
     const int K = P.K, Kp = P.Kp, groups = Kp >> 4;
-    v4u* qrow = reinterpret_cast<v4u*>(P.qx + (size_t)m * Kp);
+    v4u* const qx = reinterpret_cast<v4u*>(P.qx);
+    const QxRow qrow = P.blocked ? QxRow{qx + (size_t)(m >> 4) * (Kp >> 6) * 64 + (m & 15), 64, 16}
+                                 : QxRow{qx + (size_t)m * (Kp >> 4), 4, 1};
     if (m >= a.M) {  // padding token rows
         const v4u z = {0u, 0u, 0u, 0u};
         for (int g = threadIdx.x; g < groups; g += blockDim.x) qrow[g] = z;
@@ -42,17 +47,20 @@ __global__ void __launch_bounds__(256) quant_kernel(QuantArgs a) {
     if (threadIdx.x == 0 && P.sx) P.sx[m] = s;
 }
 
-__global__ void __launch_bounds__(256) unpermute_kernel(const int8_t* __restrict__ qx, int K, int Kp,
+__global__ void __launch_bounds__(256) unpermute_kernel(const int8_t* __restrict__ qx, int K, int Kp, int blocked,
                                                         int8_t* __restrict__ q) {
     const int m = blockIdx.y;
     const int k = blockIdx.x * blockDim.x + threadIdx.x;
     if (k >= K) return;
     const int g = k >> 4, e = k & 15;  // element e of group g sits at byte 4*(e%4) + e/4
-    q[(size_t)m * K + k] = qx[(size_t)m * Kp + g * 16 + 4 * (e & 3) + (e >> 2)];
+    const size_t group = blocked ? ((size_t)(m >> 4) * (Kp >> 6) + (g >> 2)) * 1024 + ((m & 15) + 16 * (g & 3)) * 16
+                                 : (size_t)m * Kp + g * 16;
+    q[(size_t)m * K + k] = qx[group + 4 * (e & 3) + (e >> 2)];
 }
 
-hipError_t launch_unpermute(const int8_t* qx, int M, int K, int Kp, int8_t* q, hipStream_t s) {
-    hipLaunchKernelGGL(unpermute_kernel, dim3((unsigned)((K + 255) / 256), (unsigned)M), dim3(256), 0, s, qx, K, Kp, q);
+hipError_t launch_unpermute(const int8_t* qx, int M, int K, int Kp, bool blocked, int8_t* q, hipStream_t s) {
+    hipLaunchKernelGGL(unpermute_kernel, dim3((unsigned)((K + 255) / 256), (unsigned)M), dim3(256), 0, s, qx, K, Kp,
+                       (int)blocked, q);
     return hipGetLastError();
 }
 

@@ -175,9 +175,18 @@ __device__ __forceinline__ void rmsnorm_group(const QuantProb& P, float norm, in
     for (int e = 0; e < 16; ++e) v[e] = (v[e] / norm) * w[e];
 }
 
+// Destination of one row's permuted 16-byte groups: group g at
+// base[(g / 4) * chunk + (g % 4) * sub] (v4u units); rows: chunk 4, sub 1; blocked qx:
+// chunk 64, sub 16.
+struct QxRow {
+    v4u* base;
+    int chunk, sub;
+    __device__ __forceinline__ v4u& operator[](int g) const { return base[(g >> 2) * chunk + (g & 3) * sub]; }
+};
+
 // q = clip(rint(v / s), -128, 127) for one group; permuted 16-byte store and, when
 // requested, the natural-order bytes and the fp32 values.
-__device__ __forceinline__ void emit_group(const float (&v)[16], float s, int g, int K, v4u* qrow, int8_t* qn,
+__device__ __forceinline__ void emit_group(const float (&v)[16], float s, int g, int K, const QxRow& qrow, int8_t* qn,
                                            float* vo) {
     int q[16];
 #pragma unroll
@@ -216,7 +225,7 @@ __device__ __forceinline__ double sumsq_group(const float (&v)[16], double s) {
 // per thread stay in registers, longer rows are read again on every pass.  Every
 // thread of the workgroup must call it (it synchronises).
 template <int REG>
-__device__ __forceinline__ float row_quantize(const QuantProb& P, int m, v4u* qrow, int8_t* qn, float* vo,
+__device__ __forceinline__ float row_quantize(const QuantProb& P, int m, const QxRow& qrow, int8_t* qn, float* vo,
                                               RowSmem* sm) {
     const int K = P.K, groups = P.Kp >> 4, T = blockDim.x;
     const float* xr = P.x + (size_t)m * K;

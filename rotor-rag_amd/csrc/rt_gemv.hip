@@ -43,10 +43,16 @@ constexpr int kAuxNT = 2;                 // cache policy: non-temporal (streame
 typedef __attribute__((address_space(4))) const int cint;
 typedef __attribute__((address_space(3))) const int lint;
 
-// Problem of global row block rbg: two dependent scalar loads (table, descriptor).
+// Problem of global row block rbg: two dependent scalar loads (table, descriptor).  Both
+// sources are read through constant-address-space pointers: merged with a generic one,
+// the descriptor would turn into per-lane flat loads and the buffer resource into a
+// readfirstlane loop.
+typedef __attribute__((address_space(4))) const GemvProb cprob;
+typedef __attribute__((address_space(4))) const int cidx;
 __device__ __forceinline__ GemvProb find_prob(const GemvArgs& a, int rbg) {
     if (!a.dev) return a.p;
-    return a.dev[a.rb2p[rbg]];
+    const cprob* q = (cprob*)a.dev + ((cidx*)a.rb2p)[rbg];
+    return GemvProb{q->w, q->qx, q->sx, q->rs, q->out, q->s_w, q->N, q->C, q->ldo, q->wg_begin, q->res};
 }
 
 template <int MT, typename XP>
@@ -155,7 +161,9 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
     const int rb = blockIdx.x - P.wg_begin;
     const int m0 = blockIdx.y * MT;
     const int C = P.C, ldx = C * 16;
-    const int cb = (wave * C) / nw, ce = ((wave + 1) * C) / nw;
+    // wave-uniform, kept in SGPRs (the buffer resource must not be per-lane)
+    const int cb = __builtin_amdgcn_readfirstlane((wave * C) / nw);
+    const int ce = __builtin_amdgcn_readfirstlane(((wave + 1) * C) / nw);
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, ce * 1024, kBufDword3);
     int accP[MT], accN[MT];
@@ -165,7 +173,7 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
     if constexpr (PRO) {
         v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
         RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (a.pro.Kp >> 4));
-        sm->fac = reinterpret_cast<float*>(sm + 1);  // kAttnNorm factors follow
+        sm->fac = (lfloat*)(sm + 1);  // kAttnNorm factors follow
         sx_pro = row_quantize<1>(a.pro, 0, QxRow{lq, 4, 1}, nullptr, nullptr, sm);
         __syncthreads();
         gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accN);

@@ -18,10 +18,12 @@
 
 namespace rt {
 
+typedef __attribute__((address_space(3))) float lfloat;
+
 struct RowSmem {   // reduction scratch in LDS (one slot per wave)
     float f[16];
     double d[16];
-    float* fac;    // kAttnNorm: [heads][S] combine factors (-1 = empty block), then [heads] denominators
+    lfloat* fac;   // kAttnNorm: [heads][S] combine factors (-1 = empty block), then [heads] denominators
 };
 
 template <typename T, typename Op>
@@ -105,7 +107,7 @@ __device__ __forceinline__ float attn_combine_element(const float* __restrict__ 
 // kAttnNorm, per head h: the factor e^(m_s - m) of every partial block (-1 for an
 // empty block) and the denominator sum_s e^(m_s - m) z_s, in the operation order of
 // attn_combine_element.
-__device__ __forceinline__ void attn_factors(const QuantProb& P, float* fac) {
+__device__ __forceinline__ void attn_factors(const QuantProb& P, lfloat* fac) {
     const int hd = P.attn_hd, S = P.attn_S, H = P.K / hd;
     for (int h = threadIdx.x; h < H; h += blockDim.x) {
         const float* wh = P.x + (size_t)h * S * (hd + 2);
@@ -127,7 +129,7 @@ __device__ __forceinline__ void attn_factors(const QuantProb& P, float* fac) {
 }
 
 __device__ __forceinline__ void source_group(const QuantProb& P, const float* xr, const float* ur, int g, bool vec,
-                                             float (&v)[16], const float* fac = nullptr) {
+                                             float (&v)[16], const lfloat* fac = nullptr) {
     if (P.mode == kAttnNorm) {  // 16 consecutive elements of one head (hd % 16 == 0)
         const int hd = P.attn_hd, S = P.attn_S, H = P.K / hd;
         const int k0 = g * 16, h = k0 / hd, d0 = k0 % hd;

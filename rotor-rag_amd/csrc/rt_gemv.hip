@@ -86,28 +86,38 @@ __device__ __forceinline__ void chunk_step(const v4u v, XP* __restrict__ xc, con
 // which the buffer unit range-checks (the SGPR offset is not checked), so the loads
 // that run past the range come back as zeros without touching memory.  That keeps
 // every load unconditional -- two batches of U chunks in flight -- while the math on
-// chunks >= ce is skipped.
+// chunks >= ce is skipped.  The first two batches (A: chunks cb.., B: cb + U..) are
+// issued by gemv_preload, which a caller may run before other work (a prologue) to
+// overlap the weight latency with it.
+template <int U>
+__device__ __forceinline__ v4u gemv_load(__amdgpu_buffer_rsrc_t rsrc, const int lane_off, int c) {
+    return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off + c * 1024, 0, kAuxNT));
+}
+
+template <int U>
+__device__ __forceinline__ void gemv_preload(__amdgpu_buffer_rsrc_t rsrc, const int lane_off, const int cb,
+                                             v4u (&A)[U], v4u (&B)[U]) {
+#pragma unroll
+    for (int i = 0; i < U; ++i) A[i] = gemv_load<U>(rsrc, lane_off, cb + i);
+#pragma unroll
+    for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane_off, cb + U + i);
+}
+
 template <int MT, int U, typename XP>
 __device__ __forceinline__ void gemv_body(__amdgpu_buffer_rsrc_t rsrc, const int lane_off, XP* __restrict__ xq,
                                           const int ldx, const int cb, const int ce, int (&accP)[MT],
-                                          int (&accN)[MT]) {
-    auto ld = [&](int c) {
-        return __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rsrc, lane_off + c * 1024, 0, kAuxNT));
-    };
-    v4u A[U], B[U];
-#pragma unroll
-    for (int i = 0; i < U; ++i) A[i] = ld(cb + i);
+                                          int (&accN)[MT], v4u (&A)[U], v4u (&B)[U]) {
     for (int c = cb; c < ce; c += 2 * U) {
-#pragma unroll
-        for (int i = 0; i < U; ++i) B[i] = ld(c + U + i);
 #pragma unroll
         for (int i = 0; i < U; ++i)
             if (c + i < ce) chunk_step<MT, XP>(A[i], xq + (c + i) * 16, ldx, accP, accN);
 #pragma unroll
-        for (int i = 0; i < U; ++i) A[i] = ld(c + 2 * U + i);
+        for (int i = 0; i < U; ++i) A[i] = gemv_load<U>(rsrc, lane_off, c + 2 * U + i);
 #pragma unroll
         for (int i = 0; i < U; ++i)
             if (c + U + i < ce) chunk_step<MT, XP>(B[i], xq + (c + U + i) * 16, ldx, accP, accN);
+#pragma unroll
+        for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane_off, c + 3 * U + i);
     }
 }
 
@@ -144,7 +154,9 @@ __global__ void __launch_bounds__(1024) gemv_rows_kernel(GemvArgs a) {
     int accP[MT], accN[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
-    gemv_body<MT, U, const __attribute__((address_space(4))) int>(rsrc, lane * 16, xq, ldx, 0, C, accP, accN);
+    v4u A[U], B[U];
+    gemv_preload<U>(rsrc, lane * 16, 0, A, B);
+    gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, 0, C, accP, accN, A, B);
 #pragma unroll
     for (int m = 0; m < MT; ++m) emit(a, P, rb, m0, m, lane, accP[m] - accN[m]);
 }
@@ -170,16 +182,18 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
     float sx_pro = -1.0f;
+    v4u A[U], B[U];
+    gemv_preload<U>(rsrc, lane * 16, cb, A, B);  // weights in flight during the prologue
     if constexpr (PRO) {
         v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
         RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (a.pro.Kp >> 4));
         sm->fac = (lfloat*)(sm + 1);  // kAttnNorm factors follow
         sx_pro = row_quantize<1>(a.pro, 0, QxRow{lq, 4, 1}, nullptr, nullptr, sm);
         __syncthreads();
-        gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accN);
+        gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accN, A, B);
     } else {
         cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
-        gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, cb, ce, accP, accN);
+        gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, cb, ce, accP, accN, A, B);
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) red[(wave * MT + m) * kRowBlock + lane] = accP[m] - accN[m];

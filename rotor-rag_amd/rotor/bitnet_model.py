@@ -196,6 +196,11 @@ class _DeviceModel:
         self.act_d = hip.activations(cap, D)
         self.act_f = hip.activations(cap, F)
         self.state = {}
+        # decode attention: True (default) combines the split-L partials and applies the
+        # sub-norm inside every o_proj workgroup's prologue; False runs a separate combine
+        # kernel and gives o_proj a plain RMSNorm prologue (one more launch per layer,
+        # ~0.04 ms/token slower at 30 layers)
+        self.attn_in_prologue = True
 
     def _state(self, M):
         st = self.state.get(M)
@@ -214,10 +219,13 @@ class _DeviceModel:
                 h, o, g, u = st["h"][0], st["o"][0], st["g"][0], st["u"][0]
                 st["qkv"].append(hip.plan_fused([L["q_proj"], L["k_proj"], L["v_proj"]], _hip.SRC_RMSNORM, h,
                                                 L["input_norm"], eps=eps, ys=[st["q"][0], st["k"][0], st["v"][0]]))
-                if L["attn_sub_norm"] is not None:  # combine the attention partials + sub-norm in the prologue
+                if L["attn_sub_norm"] is not None and self.attn_in_prologue:
                     st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_ATTN_NORM, self.attn_ws,
                                                        L["attn_sub_norm"], eps=eps, ys=[h], residuals=[h],
                                                        attn_head_dim=self.hd, attn_max_len=self.Lmax))
+                elif L["attn_sub_norm"] is not None:
+                    st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_RMSNORM, o, L["attn_sub_norm"],
+                                                       eps=eps, ys=[h], residuals=[h]))
                 else:
                     st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_QUANT, o, ys=[h], residuals=[h]))
                 st["gu"].append(hip.plan_fused([L["gate_proj"], L["up_proj"]], _hip.SRC_RMSNORM, h, L["post_norm"],
@@ -255,7 +263,7 @@ class _DeviceModel:
             chk(lib.rt_rope_kv_append(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
                                       L["vc"].data_ptr(), self.rope.data_ptr(), M, self.H, self.Hkv, self.hd,
                                       self.Lmax, self.pos.data_ptr()), "rt_rope_kv_append")
-            if M == 1 and L["attn_sub_norm"] is not None:  # o_proj's prologue combines the partials
+            if M == 1 and L["attn_sub_norm"] is not None and self.attn_in_prologue:
                 chk(lib.rt_attention_decode_partials(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(),
                                                      self.H, self.Hkv, self.hd, self.Lmax, self.pos.data_ptr(),
                                                      self.attn_ws.data_ptr(), self.attn_ws_bytes),

@@ -220,6 +220,17 @@ int rt_attention_decode(rt_ctx* ctx, const float* q, const float* k_cache, const
 int rt_attention_decode_partials(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, int H,
                                  int Hkv, int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes);
 
+/* The decode step's RoPE + KV append + rt_attention_decode_partials in one launch, for the
+ * single token at *pos: q [H*hd], k and v [Hkv*hd] are the raw projection outputs (not
+ * modified); every workgroup rotates its query head, the new key and value enter the
+ * caches at *pos and take part in the attention from on-chip copies.  The partials are
+ * left in `workspace` (for a RT_SRC_ATTN_NORM plan) and, when out is non-NULL, combined
+ * into out [H*hd].  Equals rt_rope_kv_append followed by rt_attention_decode(_partials)
+ * bit for bit.  Replaces, for one token, src/rotor/transformer.py:250-281. */
+int rt_rope_attention_decode(rt_ctx* ctx, const float* q, const float* k, const float* v, float* k_cache,
+                             float* v_cache, const float* rope, int H, int Hkv, int hd, int Lmax, const int* pos,
+                             void* workspace, size_t workspace_bytes, float* out);
+
 /* Final RMSNorm of x fp32 [D] with norm_w, tied bf16 LM head logits [V]
  * (src/rotor/bitnet_model.py:231-235) and greedy argmax (src/rotor/generation.py:42;
  * first index of the maximum).  `best` (device u64, zero before first use) is left

@@ -714,8 +714,24 @@ int rt_attention_decode_partials(rt_ctx* ctx, const float* q, const float* k_cac
                                "rt_attention_decode_partials");
     if (rc) return rc;
     DeviceGuard g(ctx->device);
-    RT_HIP(launch_attn_partial(q, k_cache, v_cache, H, Hkv, hd, Lmax, pos, 1.0f / sqrtf((float)hd),
+    RT_HIP(launch_attn_partial(q, nullptr, nullptr, const_cast<float*>(k_cache), const_cast<float*>(v_cache), nullptr,
+                               H, Hkv, hd, Lmax, pos, 1.0f / sqrtf((float)hd), static_cast<float*>(workspace),
+                               ctx->stream));
+    return RT_OK;
+}
+
+int rt_rope_attention_decode(rt_ctx* ctx, const float* q, const float* k, const float* v, float* k_cache,
+                             float* v_cache, const float* rope, int H, int Hkv, int hd, int Lmax, const int* pos,
+                             void* workspace, size_t workspace_bytes, float* out) {
+    int rc = attn_decode_check(ctx, q, k_cache, v_cache, pos, workspace, workspace_bytes, H, Hkv, hd, Lmax,
+                               "rt_rope_attention_decode");
+    if (rc) return rc;
+    if (!k || !v || !rope) return fail(RT_EINVAL, "rt_rope_attention_decode: NULL argument");
+    DeviceGuard g(ctx->device);
+    RT_HIP(launch_attn_partial(q, k, v, k_cache, v_cache, rope, H, Hkv, hd, Lmax, pos, 1.0f / sqrtf((float)hd),
                                static_cast<float*>(workspace), ctx->stream));
+    if (out)
+        RT_HIP(launch_attn_combine(static_cast<const float*>(workspace), H, hd, attn_splits(Lmax), out, ctx->stream));
     return RT_OK;
 }
 

@@ -141,8 +141,12 @@ hipError_t launch_attention(const float* q, const float* Kc, const float* Vc, fl
                             int hd, int Lmax, const int* pos, float scale, hipStream_t s);
 // decode attention split over blocks of 64 keys: partials [H][S][hd + 2], S = attn_splits(Lmax)
 inline int attn_splits(int Lmax) { return (Lmax + 63) / 64; }
-hipError_t launch_attn_partial(const float* q, const float* Kc, const float* Vc, int H, int Hkv, int hd, int Lmax,
-                               const int* pos, float scale, float* work, hipStream_t s);
+// rope != nullptr: q/knew/vnew are the raw projection outputs of the token at *pos; the
+// kernel applies RoPE, appends knew (rotated) and vnew to the caches and uses them for that
+// key.  rope == nullptr: q is rotated and the caches already hold the token.
+hipError_t launch_attn_partial(const float* q, const float* knew, const float* vnew, float* Kc, float* Vc,
+                               const float* rope, int H, int Hkv, int hd, int Lmax, const int* pos, float scale,
+                               float* work, hipStream_t s);
 hipError_t launch_attn_combine(const float* work, int H, int hd, int S, float* out, hipStream_t s);
 hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w, float eps, int V, int D,
                           float* logits, unsigned long long* best, int* token, int* pos, int advance,

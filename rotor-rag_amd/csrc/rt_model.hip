@@ -122,19 +122,28 @@ __global__ void __launch_bounds__(256) attention_kernel(const float* __restrict_
 // empty block).  The partials are combined by attn_combine_kernel or, in the decode
 // layer, by the prologue of the o_proj GEMV (rt_rowquant.h, kAttnNorm); both use
 // attn_combine_element, so the two give identical values.
-template <int HD>
-__global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restrict__ q, const float* __restrict__ Kc,
-                                                           const float* __restrict__ Vc, int H, int Hkv, int Lmax,
-                                                           const int* __restrict__ pos_p, float scale,
-                                                           float* __restrict__ work) {
-    constexpr int BL = 64;
+// ROPE: q, knew, vnew are the raw projection outputs of the token at *pos_p.  Every
+// workgroup rotates its head's q (the arithmetic of rope_append_kernel); the workgroup
+// whose block holds position *pos_p takes that key and value from LDS (rotated knew,
+// vnew) instead of the cache, in the same summation order, and the first query head of
+// each KV group writes them into the caches for the later steps.  Without ROPE, q is
+// already rotated and the caches hold the new key.
+template <int HD, bool ROPE>
+__global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restrict__ q, const float* __restrict__ knew,
+                                                           const float* __restrict__ vnew, float* __restrict__ Kc,
+                                                           float* __restrict__ Vc, const float* __restrict__ rope,
+                                                           int H, int Hkv, int Lmax, const int* __restrict__ pos_p,
+                                                           float scale, float* __restrict__ work) {
+    constexpr int BL = 64, half = HD / 2;
     __shared__ float qs[HD];
+    __shared__ float ks[HD];
+    __shared__ float vs[HD];
     __shared__ float part[4][BL];
     __shared__ float pr[BL];
     __shared__ float ored[256];
     const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
-    const int kh = h / (H / Hkv), L = *pos_p + 1;
+    const int kh = h / (H / Hkv), pos = *pos_p, L = pos + 1;
     const int j0 = s * BL, nk = min(BL, L - j0);  // keys of this block (may be <= 0)
     float* wp = work + ((size_t)h * S + s) * (HD + 2);
     if (nk <= 0) {
@@ -144,18 +153,53 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restri
         }
         return;
     }
-    for (int d = t; d < HD; d += 256) qs[d] = q[(size_t)h * HD + d];
+    const bool holds_new = ROPE && pos < j0 + BL;  // this block ends with the new key
+    const int lp = pos - j0;                       // its lane / key index in the block
+    if (ROPE) {
+        const float* cs = rope + (size_t)pos * half * 2;
+        for (int i = t; i < half; i += 256) {
+            const float c = cs[2 * i], sn = cs[2 * i + 1];
+            const float x1 = q[(size_t)h * HD + i], x2 = q[(size_t)h * HD + i + half];
+            qs[i] = x1 * c - x2 * sn;
+            qs[i + half] = x2 * c + x1 * sn;
+            if (holds_new) {
+                const float k1 = knew[(size_t)kh * HD + i], k2 = knew[(size_t)kh * HD + i + half];
+                ks[i] = k1 * c - k2 * sn;
+                ks[i + half] = k2 * c + k1 * sn;
+            }
+        }
+        if (holds_new)
+            for (int d = t; d < HD; d += 256) vs[d] = vnew[(size_t)kh * HD + d];
+    } else {
+        for (int d = t; d < HD; d += 256) qs[d] = q[(size_t)h * HD + d];
+    }
     __syncthreads();
+    if (holds_new && h % (H / Hkv) == 0)  // one writer per KV head
+        for (int d = t; d < HD; d += 256) {
+            Kc[((size_t)kh * HD + d) * Lmax + pos] = ks[d];
+            Vc[((size_t)kh * Lmax + pos) * HD + d] = vs[d];
+        }
     // scores: wave w sums dims [w*HD/4, (w+1)*HD/4) for key j0 + lane
     const float* K = Kc + (size_t)kh * HD * Lmax + j0 + lane;
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
     if (lane < nk) {
+        if (holds_new) {
+            const bool mine = lane == lp;
 #pragma unroll
-        for (int d = wave * (HD / 4); d < (wave + 1) * (HD / 4); d += 4) {
-            a0 += qs[d + 0] * K[(size_t)(d + 0) * Lmax];
-            a1 += qs[d + 1] * K[(size_t)(d + 1) * Lmax];
-            a2 += qs[d + 2] * K[(size_t)(d + 2) * Lmax];
-            a3 += qs[d + 3] * K[(size_t)(d + 3) * Lmax];
+            for (int d = wave * (HD / 4); d < (wave + 1) * (HD / 4); d += 4) {
+                a0 += qs[d + 0] * (mine ? ks[d + 0] : K[(size_t)(d + 0) * Lmax]);
+                a1 += qs[d + 1] * (mine ? ks[d + 1] : K[(size_t)(d + 1) * Lmax]);
+                a2 += qs[d + 2] * (mine ? ks[d + 2] : K[(size_t)(d + 2) * Lmax]);
+                a3 += qs[d + 3] * (mine ? ks[d + 3] : K[(size_t)(d + 3) * Lmax]);
+            }
+        } else {
+#pragma unroll
+            for (int d = wave * (HD / 4); d < (wave + 1) * (HD / 4); d += 4) {
+                a0 += qs[d + 0] * K[(size_t)(d + 0) * Lmax];
+                a1 += qs[d + 1] * K[(size_t)(d + 1) * Lmax];
+                a2 += qs[d + 2] * K[(size_t)(d + 2) * Lmax];
+                a3 += qs[d + 3] * K[(size_t)(d + 3) * Lmax];
+            }
         }
     }
     part[wave][lane] = (a0 + a1) + (a2 + a3);
@@ -179,13 +223,14 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restri
     constexpr int G = 256 / HD;
     const int d = t % HD, g = t / HD;
     const float* V = Vc + ((size_t)kh * Lmax + j0) * HD + d;
+    auto vrow = [&](int j) { return holds_new && j == lp ? vs[d] : V[(size_t)j * HD]; };
     float o0 = 0.f, o1 = 0.f;
     int j = g;
     for (; j + G < nk; j += 2 * G) {
-        o0 += pr[j] * V[(size_t)j * HD];
-        o1 += pr[j + G] * V[(size_t)(j + G) * HD];
+        o0 += pr[j] * vrow(j);
+        o1 += pr[j + G] * vrow(j + G);
     }
-    if (j < nk) o0 += pr[j] * V[(size_t)j * HD];
+    if (j < nk) o0 += pr[j] * vrow(j);
     ored[t] = o0 + o1;
     __syncthreads();
     if (g == 0) {
@@ -299,12 +344,16 @@ hipError_t launch_attention(const float* q, const float* Kc, const float* Vc, fl
     return hipGetLastError();
 }
 
-hipError_t launch_attn_partial(const float* q, const float* Kc, const float* Vc, int H, int Hkv, int hd, int Lmax,
-                               const int* pos, float scale, float* work, hipStream_t s) {
+hipError_t launch_attn_partial(const float* q, const float* knew, const float* vnew, float* Kc, float* Vc,
+                               const float* rope, int H, int Hkv, int hd, int Lmax, const int* pos, float scale,
+                               float* work, hipStream_t s) {
     const dim3 grid((unsigned)H, (unsigned)attn_splits(Lmax));
-    switch (hd) {
-        case 64: hipLaunchKernelGGL(attn_partial_kernel<64>, grid, dim3(256), 0, s, q, Kc, Vc, H, Hkv, Lmax, pos, scale, work); break;
-        case 128: hipLaunchKernelGGL(attn_partial_kernel<128>, grid, dim3(256), 0, s, q, Kc, Vc, H, Hkv, Lmax, pos, scale, work); break;
+    const bool r = rope != nullptr;
+    switch (hd * 2 + (r ? 1 : 0)) {
+        case 128: hipLaunchKernelGGL((attn_partial_kernel<64, false>), grid, dim3(256), 0, s, q, knew, vnew, Kc, Vc, rope, H, Hkv, Lmax, pos, scale, work); break;
+        case 129: hipLaunchKernelGGL((attn_partial_kernel<64, true>), grid, dim3(256), 0, s, q, knew, vnew, Kc, Vc, rope, H, Hkv, Lmax, pos, scale, work); break;
+        case 256: hipLaunchKernelGGL((attn_partial_kernel<128, false>), grid, dim3(256), 0, s, q, knew, vnew, Kc, Vc, rope, H, Hkv, Lmax, pos, scale, work); break;
+        case 257: hipLaunchKernelGGL((attn_partial_kernel<128, true>), grid, dim3(256), 0, s, q, knew, vnew, Kc, Vc, rope, H, Hkv, Lmax, pos, scale, work); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -260,19 +260,17 @@ class _DeviceModel:
             else:
                 hip.act_rmsnorm_quantize(h, L["input_norm"], self.act_d, eps)
                 st["qkv"][li].gemv()
-            chk(lib.rt_rope_kv_append(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
-                                      L["vc"].data_ptr(), self.rope.data_ptr(), M, self.H, self.Hkv, self.hd,
-                                      self.Lmax, self.pos.data_ptr()), "rt_rope_kv_append")
-            if M == 1 and L["attn_sub_norm"] is not None and self.attn_in_prologue:
-                chk(lib.rt_attention_decode_partials(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(),
-                                                     self.H, self.Hkv, self.hd, self.Lmax, self.pos.data_ptr(),
-                                                     self.attn_ws.data_ptr(), self.attn_ws_bytes),
-                    "rt_attention_decode_partials")
-            elif M == 1:
-                chk(lib.rt_attention_decode(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), o.data_ptr(),
-                                            self.H, self.Hkv, self.hd, self.Lmax, self.pos.data_ptr(),
-                                            self.attn_ws.data_ptr(), self.attn_ws_bytes), "rt_attention_decode")
+            if M == 1:  # RoPE + KV append + split attention in one launch; o_proj's prologue may combine
+                combine_here = L["attn_sub_norm"] is None or not self.attn_in_prologue
+                chk(lib.rt_rope_attention_decode(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
+                                                 L["vc"].data_ptr(), self.rope.data_ptr(), self.H, self.Hkv, self.hd,
+                                                 self.Lmax, self.pos.data_ptr(), self.attn_ws.data_ptr(),
+                                                 self.attn_ws_bytes, o.data_ptr() if combine_here else None),
+                    "rt_rope_attention_decode")
             else:
+                chk(lib.rt_rope_kv_append(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
+                                          L["vc"].data_ptr(), self.rope.data_ptr(), M, self.H, self.Hkv, self.hd,
+                                          self.Lmax, self.pos.data_ptr()), "rt_rope_kv_append")
                 chk(lib.rt_attention(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), o.data_ptr(), M,
                                      self.H, self.Hkv, self.hd, self.Lmax, self.pos.data_ptr()), "rt_attention")
             if fused:

@@ -125,6 +125,53 @@ def test_attention_decode_split(hip, pos0, H, Hkv, hd, Lmax):
     assert torch.equal(y, hip.linear_act(w, act, residual=res[None])[0])
 
 
+@pytest.mark.parametrize("pos0,H,Hkv,hd,Lmax", [(0, 20, 5, 128, 640), (63, 20, 5, 128, 640), (64, 8, 2, 64, 200),
+                                                (639, 20, 5, 128, 640), (130, 4, 4, 64, 131)])
+def test_rope_attention_decode_equals_separate_launches(hip, pos0, H, Hkv, hd, Lmax):
+    """One launch of RoPE + KV append + split attention gives the partials, the combined
+    output and the caches of rt_rope_kv_append followed by rt_attention_decode, bit for
+    bit, and leaves the projection outputs untouched."""
+    import torch
+
+    from oracle.rotor_oracle import rope_table
+
+    lib, chk = _lib()
+    rng = np.random.default_rng(7 * pos0 + H + Lmax)
+    f = lambda *shape: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).cuda()
+    kc0, vc0 = f(Hkv, hd, Lmax), f(Hkv, Lmax, hd)
+    q0, k0, v0 = f(1, H * hd) * 2, f(1, Hkv * hd), f(1, Hkv * hd)
+    rope = torch.from_numpy(np.ascontiguousarray(rope_table(Lmax, hd, 500000.0), np.float32)).cuda()
+    pos = torch.tensor([pos0], dtype=torch.int32, device="cuda")
+    nbytes = lib.rt_attention_decode_workspace(H, hd, Lmax)
+    hip._bind_stream()
+    # separate launches (q and k are rotated in place there)
+    q, k, kc, vc = q0.clone(), k0.clone(), kc0.clone(), vc0.clone()
+    ws_ref = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    out_ref = torch.empty((1, H * hd), device="cuda")
+    chk(lib.rt_rope_kv_append(hip.ctx, q.data_ptr(), k.data_ptr(), v0.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                              rope.data_ptr(), 1, H, Hkv, hd, Lmax, pos.data_ptr()))
+    chk(lib.rt_attention_decode(hip.ctx, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), out_ref.data_ptr(), H, Hkv, hd,
+                                Lmax, pos.data_ptr(), ws_ref.data_ptr(), nbytes))
+    # fused, twice (the second call sees the key already in the cache: same result)
+    qf, kf, vf, kcf, vcf = q0.clone(), k0.clone(), v0.clone(), kc0.clone(), vc0.clone()
+    for rep in range(2):
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+        out = torch.empty((1, H * hd), device="cuda")
+        chk(lib.rt_rope_attention_decode(hip.ctx, qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), kcf.data_ptr(),
+                                         vcf.data_ptr(), rope.data_ptr(), H, Hkv, hd, Lmax, pos.data_ptr(),
+                                         ws.data_ptr(), nbytes, out.data_ptr()))
+        assert torch.equal(ws, ws_ref), f"partials differ (call {rep})"
+        assert torch.equal(out, out_ref), f"output differs (call {rep})"
+        assert torch.equal(kcf, kc) and torch.equal(vcf, vc), f"caches differ (call {rep})"
+    assert torch.equal(qf, q0) and torch.equal(kf, k0) and torch.equal(vf, v0)
+    # partials only (out = NULL) leave the same workspace
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    chk(lib.rt_rope_attention_decode(hip.ctx, qf.data_ptr(), kf.data_ptr(), vf.data_ptr(), kcf.data_ptr(),
+                                     vcf.data_ptr(), rope.data_ptr(), H, Hkv, hd, Lmax, pos.data_ptr(), ws.data_ptr(),
+                                     nbytes, None))
+    assert torch.equal(ws, ws_ref)
+
+
 @pytest.mark.parametrize("V,D", [(1000, 512), (5000, 2560), (777, 1024)])
 def test_lm_head_argmax(hip, V, D):
     import torch

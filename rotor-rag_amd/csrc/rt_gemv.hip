@@ -96,11 +96,13 @@ __device__ __forceinline__ v4u gemv_load(__amdgpu_buffer_rsrc_t rsrc, const int 
 
 template <int U>
 __device__ __forceinline__ void gemv_preload(__amdgpu_buffer_rsrc_t rsrc, const int lane_off, const int cb,
-                                             v4u (&A)[U], v4u (&B)[U]) {
+                                             v4u (&A)[U], v4u (&B)[U], bool second = true) {
 #pragma unroll
     for (int i = 0; i < U; ++i) A[i] = gemv_load<U>(rsrc, lane_off, cb + i);
+    if (second) {
 #pragma unroll
-    for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane_off, cb + U + i);
+        for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane_off, cb + U + i);
+    }
 }
 
 template <int MT, int U, typename XP>
@@ -169,26 +171,37 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) int red[];
     const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int m0 = blockIdx.y * MT;
+    // With a prologue whose row fits one group per thread, the row's loads go out first
+    // (they do not depend on the problem); then the problem, the weight resource and the
+    // first weight batches, which stream in during the prologue's arithmetic.
+    RowRegs rr;
+    const bool early = PRO && row_fits1(a.pro, blockDim.x);
+    if (early) row_load1(a.pro, 0, rr);
     const GemvProb P = find_prob(a, blockIdx.x);
     const int rb = blockIdx.x - P.wg_begin;
-    const int m0 = blockIdx.y * MT;
     const int C = P.C, ldx = C * 16;
     // wave-uniform, kept in SGPRs (the buffer resource must not be per-lane)
     const int cb = __builtin_amdgcn_readfirstlane((wave * C) / nw);
     const int ce = __builtin_amdgcn_readfirstlane(((wave + 1) * C) / nw);
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, ce * 1024, kBufDword3);
+    v4u A[U], B[U];
+    // with a prologue only the first batch is in flight during it (register budget)
+    gemv_preload<U>(rsrc, lane * 16, cb, A, B, !PRO);
     int accP[MT], accN[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
     float sx_pro = -1.0f;
-    v4u A[U], B[U];
-    gemv_preload<U>(rsrc, lane * 16, cb, A, B);  // weights in flight during the prologue
     if constexpr (PRO) {
         v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
         RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (a.pro.Kp >> 4));
         sm->fac = (lfloat*)(sm + 1);  // kAttnNorm factors follow
-        sx_pro = row_quantize<1>(a.pro, 0, QxRow{lq, 4, 1}, nullptr, nullptr, sm);
+        const QxRow qrow{lq, 4, 1};
+        sx_pro = early ? row_finish1(a.pro, rr, qrow, nullptr, nullptr, sm)
+                       : row_quantize<1>(a.pro, 0, qrow, nullptr, nullptr, sm);
+#pragma unroll
+        for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane * 16, cb + U + i);
         __syncthreads();
         gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accN, A, B);
     } else {

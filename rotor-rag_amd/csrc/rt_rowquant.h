@@ -26,12 +26,18 @@ struct RowSmem {   // reduction scratch in LDS (one slot per wave)
     lfloat* fac;   // kAttnNorm: [heads][S] combine factors (-1 = empty block), then [heads] denominators
 };
 
+// Workgroup reduction through one slot per wave.  Each slot array serves one reduction
+// per row_quantize call (sums in RowSmem::d, maxima in RowSmem::f), so no barrier is
+// needed before the slots are written.
+// `wave_live` (wave-uniform) false: the wave only contributes v (the identity) and
+// skips the shuffles.
 template <typename T, typename Op>
-__device__ __forceinline__ T block_reduce(T v, T* red, Op op) {
+__device__ __forceinline__ T block_reduce(T v, T* red, Op op, bool wave_live = true) {
+    if (wave_live) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+        for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    }
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-    __syncthreads();  // `red` may still be read by a previous reduction
     if (lane == 0) red[wave] = v;
     __syncthreads();
     T r = red[0];
@@ -222,19 +228,77 @@ __device__ __forceinline__ double sumsq_group(const float (&v)[16], double s) {
     return s;
 }
 
-// Quantise token row m of P (modes kQuant, kRmsNorm, kRelu2Mul, kRelu2MulNorm) into
-// qrow (Kp/16 permuted groups) and return its scale.  Rows of up to REG groups of 16
-// per thread stay in registers, longer rows are read again on every pass.  Every
-// thread of the workgroup must call it (it synchronises).
+// One group of 16 per thread (Kp/16 <= threads), modes other than kAttnNorm: the row's
+// loads (x, up, norm weight) and, separately, the arithmetic, so a caller can issue its
+// own loads in between.  Waves past the row's groups do no arithmetic (they would share
+// the SIMDs with the live ones) and only take part in the barriers.
+struct RowRegs {
+    float v[16], u[16], w[16];
+    bool live;  // wave-uniform: some lane of this wave owns a group
+};
+
+__device__ __forceinline__ bool row_vec(const QuantProb& P, const float* xr, const float* ur) {
+    bool vec = (P.K & 15) == 0 && ((uintptr_t)xr & 15u) == 0 && P.mode != kAttnNorm;
+    if (ur) vec = vec && ((uintptr_t)ur & 15u) == 0;
+    if (has_norm(P)) vec = vec && ((uintptr_t)norm_weight(P) & 15u) == 0;
+    return vec;
+}
+
+__device__ __forceinline__ void row_load1(const QuantProb& P, int m, RowRegs& r) {
+    const int K = P.K, groups = P.Kp >> 4, g = threadIdx.x;
+    const float* xr = P.x + (size_t)m * K;
+    const float* ur = has_relu2(P) ? P.aux + (size_t)m * K : nullptr;
+    const bool vec = row_vec(P, xr, ur);
+    r.live = __builtin_amdgcn_readfirstlane(threadIdx.x & ~63) < groups;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) r.v[e] = r.u[e] = r.w[e] = 0.0f;
+    if (r.live) {
+        load_group(xr, g, K, vec, r.v);  // zeros past K
+        if (ur) load_group(ur, g, K, vec, r.u);
+        if (has_norm(P)) load_group(norm_weight(P), g, K, vec, r.w);
+    }
+}
+
+__device__ __forceinline__ float row_finish1(const QuantProb& P, RowRegs& r, const QxRow& qrow, int8_t* qn, float* vo,
+                                             RowSmem* sm) {
+    auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
+    auto dadd_op = [](double x, double y) { return x + y; };
+    const int K = P.K, groups = P.Kp >> 4, g = threadIdx.x;
+    float (&v)[16] = r.v;
+    if (r.live && has_relu2(P)) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) v[e] = v[e] > 0.0f ? (v[e] * v[e]) * r.u[e] : 0.0f;
+    }
+    if (has_norm(P)) {
+        const double ss = block_reduce(r.live ? sumsq_group(v, 0.0) : 0.0, sm->d, dadd_op, r.live);
+        const float norm = sqrtf((float)(ss / (double)K) + P.eps);
+        if (r.live) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) v[e] = (v[e] / norm) * r.w[e];
+        }
+    }
+    const float amax = block_reduce(r.live ? amax_group(v, 0.0f) : 0.0f, sm->f, fmax_op, r.live);
+    const float s = amax > 0.0f ? amax / 127.0f : 1.0f;
+    if (g < groups) emit_group(v, s, g, K, qrow, qn, vo);
+    return s;
+}
+
+// True when row_load1 / row_finish1 apply to P with T threads.
+__device__ __forceinline__ bool row_fits1(const QuantProb& P, int T) {
+    return P.mode != kAttnNorm && (P.Kp >> 4) <= T;
+}
+
+// Quantise token row m of P (all modes but kPermute) into qrow (Kp/16 permuted groups)
+// and return its scale.  Rows of up to REG groups of 16 per thread stay in registers,
+// longer rows are read again on every pass.  Every thread of the workgroup must call it
+// (it synchronises).
 template <int REG>
 __device__ __forceinline__ float row_quantize(const QuantProb& P, int m, const QxRow& qrow, int8_t* qn, float* vo,
                                               RowSmem* sm) {
     const int K = P.K, groups = P.Kp >> 4, T = blockDim.x;
     const float* xr = P.x + (size_t)m * K;
     const float* ur = has_relu2(P) ? P.aux + (size_t)m * K : nullptr;
-    bool vec = (K & 15) == 0 && ((uintptr_t)xr & 15u) == 0 && P.mode != kAttnNorm;
-    if (ur) vec = vec && ((uintptr_t)ur & 15u) == 0;
-    if (has_norm(P)) vec = vec && ((uintptr_t)norm_weight(P) & 15u) == 0;
+    const bool vec = row_vec(P, xr, ur);
     auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
     auto dadd_op = [](double x, double y) { return x + y; };
 

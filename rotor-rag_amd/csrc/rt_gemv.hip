@@ -27,6 +27,8 @@
 //     t0: sel 0,1,2,3  -> 00, FF, 01, 00  =  w  for f = 00, 01, 10, 11
 //     t1: sel 0,4,8,12 -> 00, 01, FF, 00  = -w  for f = 00, 01, 10, 11
 // so element positions 0/2 accumulate into accP and 1/3 into accN, acc = accP - accN.
+#include <type_traits>
+
 #include "rt_rowquant.h"
 
 // every fp32 operation rounds on its own, as the reference restatement computes them
@@ -165,7 +167,9 @@ __global__ void __launch_bounds__(1024) gemv_rows_kernel(GemvArgs a) {
 
 // LDS of the KSPLIT kernel: [nw][MT][64] int partial sums, then (prologue) the
 // quantised input row (Kp bytes) and the reduction scratch of the prologue.
-template <int MT, bool PRO>
+// PRO: 0 no prologue; 1 prologue quantising a row source (plain, RMSNorm, relu²·up,
+// relu²·up + sub-norm); 2 prologue combining decode-attention partials (kAttnNorm).
+template <int MT, int PRO>
 __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
     constexpr int U = MT == 1 ? 4 : 2;
     extern __shared__ __attribute__((aligned(16))) int red[];
@@ -175,9 +179,16 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
     // With a prologue whose row fits one group per thread, the row's loads go out first
     // (they do not depend on the problem); then the problem, the weight resource and the
     // first weight batches, which stream in during the prologue's arithmetic.
-    RowRegs rr;
-    const bool early = PRO && row_fits1(a.pro, blockDim.x);
-    if (early) row_load1(a.pro, 0, rr);
+    using Regs = typename std::conditional<PRO == 2, AttnRegs, RowRegs>::type;
+    Regs rr;
+    bool early = false;
+    if constexpr (PRO == 1) {
+        early = row_fits1(a.pro, blockDim.x);
+        if (early) row_load1(a.pro, 0, rr);
+    } else if constexpr (PRO == 2) {
+        early = attn_fits1(a.pro, blockDim.x);
+        if (early) attn_load1(a.pro, rr);
+    }
     const GemvProb P = find_prob(a, blockIdx.x);
     const int rb = blockIdx.x - P.wg_begin;
     const int C = P.C, ldx = C * 16;
@@ -188,18 +199,19 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
         __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, ce * 1024, kBufDword3);
     v4u A[U], B[U];
     // with a prologue only the first batch is in flight during it (register budget)
-    gemv_preload<U>(rsrc, lane * 16, cb, A, B, !PRO);
+    gemv_preload<U>(rsrc, lane * 16, cb, A, B, PRO == 0);
     int accP[MT], accN[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
     float sx_pro = -1.0f;
-    if constexpr (PRO) {
+    if constexpr (PRO != 0) {
         v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
         RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (a.pro.Kp >> 4));
         sm->fac = (lfloat*)(sm + 1);  // kAttnNorm factors follow
         const QxRow qrow{lq, 4, 1};
-        sx_pro = early ? row_finish1(a.pro, rr, qrow, nullptr, nullptr, sm)
-                       : row_quantize<1>(a.pro, 0, qrow, nullptr, nullptr, sm);
+        if (!early) sx_pro = row_quantize<1>(a.pro, 0, qrow, nullptr, nullptr, sm);
+        else if constexpr (PRO == 1) sx_pro = row_finish1(a.pro, rr, qrow, nullptr, nullptr, sm);
+        else sx_pro = attn_finish1(a.pro, rr, lq, sm);
 #pragma unroll
         for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane * 16, cb + U + i);
         __syncthreads();
@@ -254,15 +266,16 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
         const dim3 grid((unsigned)a.total_rb, 1);
         size_t lds = (size_t)shape.nw * kRowBlock * sizeof(int) + (size_t)a.pro.Kp + sizeof(RowSmem);
         if (a.pro.mode == kAttnNorm) lds += (size_t)(a.pro.K / a.pro.attn_hd) * (a.pro.attn_S + 1) * sizeof(float);
-        hipLaunchKernelGGL((gemv_ksplit_kernel<1, true>), grid, block, lds, s, a);
+        if (a.pro.mode == kAttnNorm) hipLaunchKernelGGL((gemv_ksplit_kernel<1, 2>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((gemv_ksplit_kernel<1, 1>), grid, block, lds, s, a);
     } else if (shape.ksplit) {
         const dim3 grid((unsigned)a.total_rb, mblocks);
         const size_t lds = (size_t)shape.nw * mt * kRowBlock * sizeof(int);
         switch (mt) {
-            case 1: hipLaunchKernelGGL((gemv_ksplit_kernel<1, false>), grid, block, lds, s, a); break;
-            case 2: hipLaunchKernelGGL((gemv_ksplit_kernel<2, false>), grid, block, lds, s, a); break;
-            case 4: hipLaunchKernelGGL((gemv_ksplit_kernel<4, false>), grid, block, lds, s, a); break;
-            case 8: hipLaunchKernelGGL((gemv_ksplit_kernel<8, false>), grid, block, lds, s, a); break;
+            case 1: hipLaunchKernelGGL((gemv_ksplit_kernel<1, 0>), grid, block, lds, s, a); break;
+            case 2: hipLaunchKernelGGL((gemv_ksplit_kernel<2, 0>), grid, block, lds, s, a); break;
+            case 4: hipLaunchKernelGGL((gemv_ksplit_kernel<4, 0>), grid, block, lds, s, a); break;
+            case 8: hipLaunchKernelGGL((gemv_ksplit_kernel<8, 0>), grid, block, lds, s, a); break;
             default: return hipErrorInvalidValue;
         }
     } else {

@@ -288,6 +288,104 @@ __device__ __forceinline__ bool row_fits1(const QuantProb& P, int T) {
     return P.mode != kAttnNorm && (P.Kp >> 4) <= T;
 }
 
+// kAttnNorm for one token with K % 64 == 0 and at most kAttnSMax partial blocks: lane
+// t owns output dword i = t % 4 of group g = t / 4, i.e. elements 16 g + i + 4 j,
+// j = 0..3 (one dword of the permuted layout).  attn_load1 issues every load the lane
+// needs (its head's block maxima and sums, its 4 values of every block, its 4 norm
+// weights) at once; attn_finish1 combines them in the operation order of
+// attn_combine_element, then RMSNorm and quantisation as row_finish1.
+constexpr int kAttnSMax = 10;  // Lmax <= 640 (longer contexts take the general path)
+struct AttnRegs {
+    float p[kAttnSMax][4], m[kAttnSMax], z[kAttnSMax], w[4];
+    bool live;  // wave-uniform: some lane of this wave owns a dword
+};
+
+__device__ __forceinline__ bool attn_fits1(const QuantProb& P, int T) {
+    return P.mode == kAttnNorm && P.attn_S <= kAttnSMax && (P.K & 63) == 0 && P.K / 4 <= T &&
+           P.attn_hd % 16 == 0;
+}
+
+__device__ __forceinline__ void attn_load1(const QuantProb& P, AttnRegs& r) {
+    const int t = threadIdx.x, K = P.K, hd = P.attn_hd, S = P.attn_S;
+    r.live = __builtin_amdgcn_readfirstlane(threadIdx.x & ~63) < K / 4;
+#pragma unroll
+    for (int s = 0; s < kAttnSMax; ++s) {
+        r.m[s] = -INFINITY;
+        r.z[s] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.p[s][j] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.w[j] = 0.0f;
+    if (t < K / 4) {
+        const int g = t >> 2, i = t & 3, k0 = 16 * g, h = k0 / hd, d = k0 % hd + i;
+        const float* wh = P.x + (size_t)h * S * (hd + 2);
+#pragma unroll
+        for (int s = 0; s < kAttnSMax; ++s) {
+            if (s < S) {
+                const float* ps = wh + (size_t)s * (hd + 2);
+                r.m[s] = ps[hd];
+                r.z[s] = ps[hd + 1];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) r.p[s][j] = ps[d + 4 * j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r.w[j] = P.aux[k0 + i + 4 * j];
+    }
+}
+
+__device__ __forceinline__ float attn_finish1(const QuantProb& P, AttnRegs& r, v4u* lq, RowSmem* sm) {
+    auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
+    auto dadd_op = [](double x, double y) { return x + y; };
+    const int t = threadIdx.x, K = P.K, S = P.attn_S;
+    const bool mine = t < K / 4;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (mine) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < kAttnSMax; ++s)
+            if (s < S) mx = fmaxf(mx, r.m[s]);
+        float num[4] = {0.0f, 0.0f, 0.0f, 0.0f}, den = 0.0f;
+#pragma unroll
+        for (int s = 0; s < kAttnSMax; ++s) {
+            if (s >= S || r.m[s] == -INFINITY) continue;
+            const float f = expf(r.m[s] - mx);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) num[j] += f * r.p[s][j];
+            den += f * r.z[s];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = num[j] / den;
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ss += (double)v[j] * (double)v[j];
+    ss = block_reduce(ss, sm->d, dadd_op, r.live);
+    const float norm = sqrtf((float)(ss / (double)K) + P.eps);
+    float amax = 0.0f;
+    if (mine) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = (v[j] / norm) * r.w[j];
+            amax = fmaxf(amax, fabsf(v[j]));
+        }
+    }
+    amax = block_reduce(amax, sm->f, fmax_op, r.live);
+    const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
+    if (mine) {  // byte b of dword i of a group = element 4 b + i = v[b]
+        unsigned dw = 0u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            float q = rintf(v[b] / sc);
+            q = fminf(fmaxf(q, -128.0f), 127.0f);
+            dw |= ((unsigned)(int)q & 0xffu) << (8 * b);
+        }
+        reinterpret_cast<unsigned*>(lq)[t] = dw;
+    }
+    return sc;
+}
+
 // Quantise token row m of P (all modes but kPermute) into qrow (Kp/16 permuted groups)
 // and return its scale.  Rows of up to REG groups of 16 per thread stay in registers,
 // longer rows are read again on every pass.  Every thread of the workgroup must call it

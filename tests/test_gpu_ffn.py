@@ -141,7 +141,8 @@ def test_ffn_block_graph_replay(hip):
         gpu_layers._gpu_instance = None
 
 
-@pytest.mark.parametrize("mode,K,N", [(0, 2560, 640), (2, 2560, 2560), (3, 6912, 2560), (4, 6912, 2560), (2, 100, 77)])
+@pytest.mark.parametrize("mode,K,N", [(0, 2560, 640), (2, 2560, 2560), (3, 6912, 2560), (4, 6912, 2560), (2, 100, 77),
+                                      (4, 20000, 128)])  # more groups than threads: general prologue path
 def test_fused_plan_equals_act_path(hip, mode, K, N):
     """One-launch decode plans (input quantised in the GEMV prologue) give exactly the
     result of the separate quantiser + linear path, with and without the residual."""

@@ -80,7 +80,8 @@ def test_rope_append_and_attention(hip, M, pos0, H, Hkv, hd):
 
 
 @pytest.mark.parametrize("pos0,H,Hkv,hd,Lmax", [(0, 20, 5, 128, 640), (63, 20, 5, 128, 640), (64, 8, 2, 64, 200),
-                                                (511, 20, 5, 128, 640), (639, 20, 5, 128, 640), (100, 4, 4, 64, 130)])
+                                                (511, 20, 5, 128, 640), (639, 20, 5, 128, 640), (100, 4, 4, 64, 130),
+                                                (700, 8, 2, 64, 1000)])  # 16 blocks: general prologue path
 def test_attention_decode_split(hip, pos0, H, Hkv, hd, Lmax):
     """Flash-decoding form equals the single-workgroup form; the workspace is reusable."""
     import torch

@@ -1,0 +1,90 @@
+"""Code-generation guards for the hot kernels (CPU only: compiles to gfx950 assembly).
+
+Each check pins a property the kernels' speed depends on and that a small source change
+can silently lose:
+  * GEMV kernels read their problem descriptors with scalar loads: no flat (per-lane)
+    loads, and no readfirstlane "waterfall" loops (a loop of v_readfirstlane + 64-bit
+    compares that makes a per-lane buffer resource uniform, once per chunk);
+  * no register spills (scratch) in the GEMV kernels;
+  * the GEMM's main loop is free of scratch traffic and of waterfall loops.
+"""
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+CSRC = Path(__file__).resolve().parents[1] / "rotor-rag_amd" / "csrc"
+HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "--cuda-device-only", "-S",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _asm(src, tmp_path):
+    if not Path(HIPCC).exists():
+        pytest.skip("hipcc not available")
+    out = tmp_path / (Path(src).stem + ".s")
+    r = subprocess.run([HIPCC, *FLAGS, str(CSRC / src), "-o", str(out)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return out.read_text()
+
+
+def _kernels(asm):
+    """kernel symbol -> its instruction text (label to s_endpgm)."""
+    out, name, body = {}, None, []
+    for line in asm.splitlines():
+        m = re.match(r"^(_Z\S+):", line)
+        if m:
+            name, body = m.group(1), []
+            continue
+        if name is not None:
+            body.append(line)
+            if "s_endpgm" in line:
+                out[name] = "\n".join(body)
+                name = None
+    return out
+
+
+def _waterfalls(text):
+    return len(re.findall(r"v_readfirstlane_b32[^\n]*\n\s*v_readfirstlane_b32[^\n]*\n(?:[^\n]*\n){0,2}\s*v_cmp_eq_u64", text))
+
+
+@pytest.fixture(scope="module")
+def gemv(tmp_path_factory):
+    return _kernels(_asm("rt_gemv.hip", tmp_path_factory.mktemp("gemv")))
+
+
+@pytest.fixture(scope="module")
+def gemm(tmp_path_factory):
+    return _kernels(_asm("rt_gemm.hip", tmp_path_factory.mktemp("gemm")))
+
+
+def test_gemv_kernels_scalar_descriptors_no_spills(gemv):
+    names = [n for n in gemv if "gemv_rows_kernel" in n or "gemv_ksplit_kernel" in n]
+    assert len(names) >= 9, names
+    for n in names:
+        t = gemv[n]
+        assert "flat_load" not in t, f"{n}: per-lane flat loads"
+        assert _waterfalls(t) == 0, f"{n}: readfirstlane loop"
+        assert "scratch_" not in t or "gemv_ksplit_kernelILi1ELi2E" in n, f"{n}: register spills"
+
+
+def test_gemv_rows_reads_activations_with_scalar_loads(gemv):
+    (n,) = [n for n in gemv if "gemv_rows_kernelILi1E" in n]
+    assert "s_load_dwordx16" in gemv[n] or "s_load_dwordx8" in gemv[n]
+    assert "global_load" not in gemv[n]
+
+
+def test_gemm_main_loop_clean(gemm):
+    names = [n for n in gemm if "gemm_kernel" in n]
+    assert len(names) >= 4, names
+    for n in names:
+        t = gemm[n]
+        assert _waterfalls(t) == 0, f"{n}: readfirstlane loop"
+        # the main loop is the region between the first s_barrier after the ring fill and
+        # the epilogue's first buffer store; spills may only appear in the epilogue
+        body = t.split("buffer_store_dword")[0]
+        assert "scratch_load" not in body, f"{n}: scratch reloads before the epilogue"
+        assert "v_mfma_i32_32x32x32_i8" in t
+        assert "global_load_lds_dwordx4" in t

@@ -266,42 +266,70 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
                                                       unsigned long long* __restrict__ best) {
     constexpr int D = SLICES * 512;
     __shared__ double redd[4];
+    __shared__ float xs[D];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    // RMSNorm statistics of x over D (every workgroup recomputes them)
+    // RMSNorm of x over D (every workgroup recomputes it, each element once, into LDS)
+    float xv[D / 256], wv[D / 256];
+#pragma unroll
+    for (int i = 0; i < D / 256; ++i) {
+        xv[i] = x[t + 256 * i];
+        wv[i] = norm_w[t + 256 * i];
+    }
     double ss = 0.0;
-    for (int k = t; k < D; k += 256) ss += (double)x[k] * (double)x[k];
+#pragma unroll
+    for (int i = 0; i < D / 256; ++i) ss += (double)xv[i] * (double)xv[i];
     for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
     if (lane == 0) redd[wave] = ss;
     __syncthreads();
     ss = (redd[0] + redd[1]) + (redd[2] + redd[3]);
     const float norm = sqrtf((float)(ss / (double)D) + eps);
+#pragma unroll
+    for (int i = 0; i < D / 256; ++i) xs[t + 256 * i] = (xv[i] / norm) * wv[i];
+    __syncthreads();
     float xn[SLICES][8];
 #pragma unroll
     for (int s = 0; s < SLICES; ++s)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int k = s * 512 + lane * 8 + e;
-            xn[s][e] = (x[k] / norm) * norm_w[k];
-        }
+        for (int e = 0; e < 8; ++e) xn[s][e] = xs[s * 512 + lane * 8 + e];
+    // rows in batches of RB: the batch's RB * SLICES loads go out together, then the math
+    constexpr int RB = 4;
     const int r0 = (blockIdx.x * 4 + wave) * rows_per_wave;
     unsigned long long key = 0ull;
-    for (int r = r0; r < r0 + rows_per_wave && r < V; ++r) {
-        const v4u* row = reinterpret_cast<const v4u*>(E + (size_t)r * D);
-        float acc = 0.0f;
+    for (int rb = r0; rb < r0 + rows_per_wave && rb < V; rb += RB) {
+        v4u w[RB][SLICES];
 #pragma unroll
-        for (int s = 0; s < SLICES; ++s) {
-            const v4u w = __builtin_nontemporal_load(row + s * 64 + lane);
+        for (int i = 0; i < RB; ++i) {
+            const int r = min(rb + i, V - 1);  // rows past V re-read the last row (discarded)
+            const v4u* row = reinterpret_cast<const v4u*>(E + (size_t)r * D);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                acc += __uint_as_float(w[e] << 16) * xn[s][2 * e];
-                acc += __uint_as_float(w[e] & 0xFFFF0000u) * xn[s][2 * e + 1];
-            }
+            for (int s = 0; s < SLICES; ++s) w[i][s] = __builtin_nontemporal_load(row + s * 64 + lane);
         }
-        for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off, 64);
+        float acc[RB];
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            acc[i] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < SLICES; ++s)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc[i] += __uint_as_float(w[i][s][e] << 16) * xn[s][2 * e];
+                    acc[i] += __uint_as_float(w[i][s][e] & 0xFFFF0000u) * xn[s][2 * e + 1];
+                }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+            for (int i = 0; i < RB; ++i) acc[i] += __shfl_xor(acc[i], off, 64);
         if (lane == 0) {
-            logits[r] = acc;
-            const unsigned long long kk = argmax_key(acc, (unsigned)r);
-            key = kk > key ? kk : key;
+#pragma unroll
+            for (int i = 0; i < RB; ++i) {
+                const int r = rb + i;
+                if (r < r0 + rows_per_wave && r < V) {
+                    logits[r] = acc[i];
+                    const unsigned long long kk = argmax_key(acc[i], (unsigned)r);
+                    key = kk > key ? kk : key;
+                }
+            }
         }
     }
     if (lane == 0 && key) atomicMax(best, key);
@@ -367,7 +395,7 @@ hipError_t launch_attn_combine(const float* work, int H, int hd, int S, float* o
 hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w, float eps, int V, int D,
                           float* logits, unsigned long long* best, int* token, int* pos, int advance,
                           int* next_ids, int* out_tokens, int pos_base, int out_cap, hipStream_t s) {
-    const int rpw = 16;
+    const int rpw = 32;
     const unsigned blocks = (unsigned)((V + 4 * rpw - 1) / (4 * rpw));
     switch (D / 512) {
         case 1: hipLaunchKernelGGL(lm_head_kernel<1>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;

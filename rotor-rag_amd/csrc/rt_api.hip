@@ -103,6 +103,7 @@ struct rt_plan {
     std::vector<GemvProb> probs;
     std::vector<QuantProb> quant;
     std::vector<GemmArgs> gemms;     // M > kGemvMaxM: one MFMA GEMM launch per problem
+    GemmArgs* dev_gemms = nullptr;   // 8 < M <= 64: the problems of one grouped launch [G]
     std::vector<const rt_act*> acts; // plans over caller-quantised activations
     bool fused = false;              // M = 1, input quantised in the GEMV prologue
     QuantProb pro{};
@@ -364,10 +365,21 @@ int rt_plan_free(rt_plan* plan) {
     DeviceGuard g(plan->device);
     if (plan->dev_probs) (void)hipFree(plan->dev_probs);
     if (plan->dev_rb2p) (void)hipFree(plan->dev_rb2p);
+    if (plan->dev_gemms) (void)hipFree(plan->dev_gemms);
     if (plan->dev_quant) (void)hipFree(plan->dev_quant);
     if (plan->act) (void)hipFree(plan->act);
     delete plan;
     return RT_OK;
+}
+
+// 8 < M <= 64: one split-K launch serves all problems (row blocks numbered as in probs)
+static hipError_t upload_gemm_group(rt_plan* p) {
+    if (p->gemms.empty() || gemm_bm(p->M) != 64) return hipSuccess;
+    std::vector<GemmArgs> g = p->gemms;
+    for (size_t i = 0; i < g.size(); ++i) g[i].wg_begin = p->probs[i].wg_begin;
+    hipError_t e = hipMalloc(&p->dev_gemms, sizeof(GemmArgs) * g.size());
+    if (e == hipSuccess) e = hipMemcpy(p->dev_gemms, g.data(), sizeof(GemmArgs) * g.size(), hipMemcpyHostToDevice);
+    return e;
 }
 
 int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* const* x, int M, float* const* y,
@@ -457,6 +469,7 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
         e = hipMemcpy(p->dev_probs, p->probs.data(), sizeof(GemvProb) * G, hipMemcpyHostToDevice);
     if (e == hipSuccess)
         e = hipMemcpy(p->dev_quant, p->quant.data(), sizeof(QuantProb) * p->U, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = upload_gemm_group(p);
     if (e != hipSuccess) {
         rt_plan_free(p);
         return hip_fail(e, "rt_plan_create");
@@ -500,6 +513,10 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
     a.M = plan->M;
     a.out_i32 = 0;
     a.total_rb = plan->total_rb;
+    if (plan->dev_gemms) {
+        RT_HIP(launch_gemm_group(plan->dev_gemms, plan->dev_rb2p, plan->total_rb, ctx->stream));
+        return RT_OK;
+    }
     if (!plan->gemms.empty()) {
         for (const GemmArgs& ga : plan->gemms) RT_HIP(launch_gemm(ga, ctx->stream));
         return RT_OK;
@@ -642,6 +659,7 @@ int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_
     if (e == hipSuccess) e = hipMalloc(&p->dev_rb2p, sizeof(int) * wg);
     if (e == hipSuccess) e = hipMemcpy(p->dev_rb2p, rb2p.data(), sizeof(int) * wg, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(p->dev_probs, p->probs.data(), sizeof(GemvProb) * G, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = upload_gemm_group(p);
     if (e != hipSuccess) {
         rt_plan_free(p);
         return hip_fail(e, "rt_plan_create_act");

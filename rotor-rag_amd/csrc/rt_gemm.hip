@@ -296,6 +296,164 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
     else store_tile<FI, FJ, 1>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
 }
 
+// ---- M <= 64: K split over the waves ------------------------------------------------
+// One workgroup per 64-column tile of the output and all (<= 64) rows; wave w of NW
+// covers chunks [w C / NW, (w + 1) C / NW).  Each wave fills a private LDS ring of S
+// stages by direct loads (4 A blocks + 1 weight chunk per step, S - 1 steps ahead) and
+// needs no barrier inside its loop: s_waitcnt on its own loads publishes a stage to
+// itself.  The NW int32 partial tiles are then summed in LDS (exact) and one pass
+// applies the fp32 epilogue.  Fragment reads, weight expansion and the result layout
+// are those of gemm_kernel (a wave tile of 64 x 64 = 2 x 2 blocks of 32 x 32).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// one problem, or a group of them (dev != nullptr: workgroup b serves problem rb2p[b])
+struct GemmGroupArgs {
+    const GemmArgs* dev;
+    const int* rb2p;
+    GemmArgs one;
+};
+
+// Problem of workgroup b, read through constant-address-space pointers so that it stays
+// in scalar registers (see the GEMV's find_prob).
+typedef __attribute__((address_space(4))) const GemmArgs cgemm;
+typedef __attribute__((address_space(4))) const int cidx_g;
+__device__ __forceinline__ GemmArgs find_gemm(const GemmGroupArgs& ga, int b) {
+    if (!ga.dev) return ga.one;
+    const cgemm* q = (cgemm*)ga.dev + ((cidx_g*)ga.rb2p)[b];
+    return GemmArgs{q->w, q->qx, q->sx, q->rs, q->out, q->s_w, q->M, q->N, q->Np, q->C, q->ldo, q->out_i32, q->res,
+                    q->wg_begin};
+}
+
+template <int NW, int S>
+__global__ void __launch_bounds__(NW * 64) gemm_splitk_kernel(GemmGroupArgs ga) {
+    constexpr int STAGE = 4 * 1024 + 1024, LOADS = 5;  // A: 4 blocks of 16 rows; W: 1 chunk
+    extern __shared__ __attribute__((aligned(16))) v4u lds[];
+    char* const lds_b = reinterpret_cast<char*>(lds);
+    const int t = threadIdx.x, lane = t & 63, g = lane >> 5, r32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const GemmArgs a = find_gemm(ga, blockIdx.x);
+    const int C = a.C, n0 = ((int)blockIdx.x - a.wg_begin) * kRowBlock;
+    const int cb = __builtin_amdgcn_readfirstlane((wave * C) / NW);
+    const int ce = __builtin_amdgcn_readfirstlane(((wave + 1) * C) / NW);
+    char* const ring = lds_b + wave * S * STAGE;
+    const int8_t* a_src = a.qx + (size_t)lane * 16;  // block f of chunk c at (f C + c) KiB
+    const v4u* w_src = a.w + (size_t)(n0 / kRowBlock) * C * kRowBlock + lane;
+    auto issue = [&](int c) {
+        char* st = ring + (c % S) * STAGE;
+#pragma unroll
+        for (int f = 0; f < 4; ++f) load_lds16(a_src + ((size_t)f * C + c) * 1024, st + f * 1024);
+        load_lds16(w_src + (size_t)c * kRowBlock, st + 4096);
+    };
+    // per-lane read offsets in a stage (as gemm_kernel with WM = WN = 64)
+    const int a_rd = (r32 >> 4) * 1024 + ((r32 & 15) + 16 * g) * 16;
+    const int w_rd = 4096 + r32 * 16 + g * 4;  // column block j adds 32 rows = 512 bytes
+
+    v16i acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
+    for (int c = cb; c < ce && c < cb + S - 1; ++c) issue(c);
+    for (int c = cb; c < ce; ++c) {
+        if (c + S - 1 < ce) {
+            issue(c + S - 1);  // its stage was read in step c - 1 (values already consumed)
+            wait_vm<(S - 1) * LOADS>();
+        } else {
+            wait_vm<0>();
+        }
+        const char* st = ring + (c % S) * STAGE;
+        v4i fa[2][2], fb[2][2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) fa[h][i] = *reinterpret_cast<const v4i*>(st + a_rd + i * 2048 + h * 512);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) fb[h][j] = decode_dword(*reinterpret_cast<const unsigned*>(st + w_rd + j * 512 + h * 8));
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[h][i], fb[h][j], acc[i][j], 0, 0, 0);
+    }
+
+    // sum the NW partial tiles: wave w stores its 64 x 64 int32 tile over its own ring
+    __syncthreads();  // every wave is done with its ring
+    int* part = reinterpret_cast<int*>(ring);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                part[(i * 32 + 8 * (k >> 2) + 4 * g + (k & 3)) * 64 + j * 32 + r32] = acc[i][j][k];
+    __syncthreads();
+    // thread t: column n0 + t % 64, rows t / 64 + (NW) j, j < EPT; output and residual as
+    // raw buffers over M rows (rows past M fall outside; a column past N adds bit 31)
+    constexpr int EPT = 64 * 64 / (NW * 64);
+    const int n = n0 + lane, mb = t >> 6;
+    int v[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const int e = t + j * NW * 64;
+        int acc_e = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) acc_e += reinterpret_cast<const int*>(lds_b + w * S * STAGE)[e];
+        v[j] = acc_e;
+    }
+    const unsigned range = (unsigned)a.M * (unsigned)a.ldo * 4u;
+    const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(a.out, 0, range, kBufDword3);
+    const int coff = (int)((unsigned)n * 4u + ((unsigned)(n >= a.N) << 31));
+    if (a.out_i32) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            __builtin_amdgcn_raw_buffer_store_b32((unsigned)v[j], out, (mb + NW * j) * a.ldo * 4 + coff, 0, 0);
+        return;
+    }
+    const float sw = a.rs ? a.rs[min(n, a.N - 1)] : a.s_w;
+    float sxv[EPT], rv[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) sxv[j] = a.sx[mb + NW * j];  // sx holds the 64 padded rows
+    const __amdgpu_buffer_rsrc_t res =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.res, 0, a.res ? range : 0u, kBufDword3);
+    if (a.res) {
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            rv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(res, (mb + NW * j) * a.ldo * 4 + coff, 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+        const float y = ((float)v[j] * sxv[j]) * sw;
+        const float o = a.res ? rv[j] + y : y;
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, o), out, (mb + NW * j) * a.ldo * 4 + coff, 0, 0);
+    }
+}
+
+template <int NW, int S>
+static hipError_t launch_splitk(const GemmGroupArgs& ga, int blocks, hipStream_t s) {
+    constexpr int LDS = NW * S * (5 * 1024);
+    static_assert(S * 5 * 1024 >= 64 * 64 * 4, "a wave's ring must hold its partial tile");
+    if (LDS > 65536) {
+        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_splitk_kernel<NW, S>),
+                                                           hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
+        if (attr != hipSuccess) return attr;
+    }
+    hipLaunchKernelGGL((gemm_splitk_kernel<NW, S>), dim3((unsigned)blocks), dim3(NW * 64), LDS, s, ga);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, int total_rb, hipStream_t s) {
+    if (total_rb <= 0) return hipSuccess;
+    return launch_splitk<8, 4>(GemmGroupArgs{dev, rb2p, GemmArgs{}}, total_rb, s);
+}
+
 template <int BM, int BN, int WAVES_M, int STAGES>
 static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
     using T = GemmTile<BM, BN, WAVES_M, STAGES>;
@@ -316,7 +474,11 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     if ((long long)gemm_bm(a.M) * a.ldo * 4 >= (1ll << 31)) return hipErrorInvalidValue;
     // the row tile divides gemm_bm(M), which sized the activation padding
     const int bm = gemm_bm(a.M);
-    if (bm == 64) return launch_tile<64, 64, 2, 4>(a, s);
+    if (bm == 64) {
+        GemmArgs one = a;
+        one.wg_begin = 0;
+        return launch_splitk<8, 4>(GemmGroupArgs{nullptr, nullptr, one}, a.Np / kRowBlock, s);
+    }
     if (bm == 128) return launch_tile<128, 128, 2, 4>(a, s);
     const long long wide = (long long)((a.N + 255) / 256) * ((a.M + 255) / 256);
     if (wide >= 192) return launch_tile<256, 256, 2, 4>(a, s);

@@ -109,6 +109,7 @@ struct GemmArgs {
     float s_w;
     int M, N, Np, C, ldo, out_i32;
     const float* res;    // optional fp32 [M][ldo] added to y (may alias out)
+    int wg_begin;        // grouped launches: first global row block of this problem
 };
 
 constexpr int kBufDword3 = 0x00020000;  // buffer resource word 3 for gfx9 raw buffers
@@ -132,6 +133,9 @@ hipError_t launch_unpermute(const int8_t* qx, int M, int K, int Kp, bool blocked
 // mt = tokens per workgroup (1, 2, 4 or 8).
 hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+// M <= 64 (gemm_bm(M) == 64): G problems in one launch over all their row blocks;
+// dev [G] (wg_begin set), rb2p [total_rb] problem of every global row block.
+hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, int total_rb, hipStream_t s);
 
 // model kernels (rt_model.hip)
 hipError_t launch_embed(const uint16_t* E, const int* ids, int M, int V, int D, float* h, hipStream_t s);

@@ -144,11 +144,12 @@ def test_ternary_matmul_duck_type(hip):
     assert y.shape == (300,)
 
 
-def test_plan_matches_single_calls(hip):
+@pytest.mark.parametrize("M", [1, 16, 37, 64, 130])
+def test_plan_matches_single_calls(hip, M):
+    """A plan launches its problems together (one grid over all row blocks for M <= 64)."""
     import torch
 
-    rng = np.random.default_rng(12)
-    M = 1
+    rng = np.random.default_rng(12 + M)
     x1 = torch.from_numpy(rng.standard_normal((M, 2560), dtype=np.float32)).cuda()
     x2 = torch.from_numpy(rng.standard_normal((M, 6912), dtype=np.float32)).cuda()
     shapes = [(2560, 2560, x1), (640, 2560, x1), (640, 2560, x1), (2560, 6912, x2)]

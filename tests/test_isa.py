@@ -77,14 +77,17 @@ def test_gemv_rows_reads_activations_with_scalar_loads(gemv):
 
 
 def test_gemm_main_loop_clean(gemm):
-    names = [n for n in gemm if "gemm_kernel" in n]
-    assert len(names) >= 4, names
-    for n in names:
+    tiles = [n for n in gemm if "gemm_kernel" in n]
+    splitk = [n for n in gemm if "gemm_splitk_kernel" in n]
+    assert len(tiles) >= 3 and len(splitk) >= 1, list(gemm)
+    for n in tiles + splitk:
         t = gemm[n]
         assert _waterfalls(t) == 0, f"{n}: readfirstlane loop"
-        # the main loop is the region between the first s_barrier after the ring fill and
-        # the epilogue's first buffer store; spills may only appear in the epilogue
-        body = t.split("buffer_store_dword")[0]
-        assert "scratch_load" not in body, f"{n}: scratch reloads before the epilogue"
         assert "v_mfma_i32_32x32x32_i8" in t
         assert "global_load_lds_dwordx4" in t
+    for n in tiles:
+        # spills may only appear in the epilogue (after the first output store)
+        body = gemm[n].split("buffer_store_dword")[0]
+        assert "scratch_load" not in body, f"{n}: scratch reloads before the epilogue"
+    for n in splitk:
+        assert "scratch_" not in gemm[n], f"{n}: register spills"

@@ -111,7 +111,8 @@ int rt_quantize_rows(rt_ctx* ctx, const float* x, int M, int K, int8_t* q, float
 int rt_linear_i32(rt_ctx* ctx, const rt_weights* w, const int8_t* q, int M, int32_t* acc);
 
 /* The ternary linear, W2A8: per-token quantise x fp32 [M][K], accumulate in int32,
- * y[m][n] = ((float)acc[m][n] * s_x[m]) * s_w.  y fp32 [M][N] (device).
+ * y[m][n] = ((float)acc[m][n] * s_x[m]) * s_w.  y fp32 [M][N] (device).  M = 1 is one
+ * launch (the GEMV quantises x in its prologue); otherwise a quantiser launch + one. */
  * Replaces TernaryLinear.forward (src/rotor/transformer.py:111-155; the op at :150)
  * and, per token, GPUTernaryOps.ternary_matmul (src/rotor/gpu_ternary.py:138-202). */
 int rt_linear_f32(rt_ctx* ctx, const rt_weights* w, const float* x, int M, float* y);
@@ -129,10 +130,14 @@ int rt_linear_f32_rowscale(rt_ctx* ctx, const rt_weights* w, const float* x, int
  * creation; the device buffers they name must outlive the plan. */
 int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* const* x, int M,
                    float* const* y, rt_plan** out);
+/* Runs the plan.  For M = 1 this is ONE launch when the GEMV can quantise in its
+ * prologue: every problem's own input (many row blocks), or the one input all problems
+ * share (few row blocks); the plan's quantised-activation buffer is then not written.
+ * Otherwise a quantiser launch, then the GEMV/GEMM launch. */
 int rt_plan_run(rt_ctx* ctx, const rt_plan* plan);
-/* The two launches of rt_plan_run, for callers that schedule them apart (e.g. to time
- * or overlap them): quantise the plan's distinct inputs, then run its GEMV launch on
- * the activations quantised last. */
+/* The two-launch form of rt_plan_run, for callers that schedule them apart (e.g. to
+ * time or overlap them): quantise the plan's distinct inputs, then run its GEMV launch
+ * on the activations quantised last.  Results equal rt_plan_run's bit for bit. */
 int rt_plan_quantize(rt_ctx* ctx, const rt_plan* plan);
 int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan);
 int rt_plan_free(rt_plan* plan);

@@ -16,6 +16,7 @@
 
 #include "../../include/rotor_hip.h"
 #include "rt_internal.h"
+#include "rt_rowquant.h"
 
 using namespace rt;
 
@@ -107,6 +108,11 @@ struct rt_plan {
     std::vector<const rt_act*> acts; // plans over caller-quantised activations
     bool fused = false;              // M = 1, input quantised in the GEMV prologue
     QuantProb pro{};
+    // rt_plan_run of an M = 1 plan over fp32 inputs: 1 the one shared input is quantised in
+    // the KSPLIT prologue (pro), 2 every problem's own input in the ROWS prologue
+    // (run_shape); 0 a quantiser launch, then the GEMV
+    int run_pro = 0;
+    GemvShape run_shape{};
 };
 
 struct rt_act {
@@ -305,6 +311,32 @@ int rt_quantize_rows(rt_ctx* ctx, const float* x, int M, int K, int8_t* q, float
     return stage_activations(ctx, x, nullptr, M, K, M, false, q, s, &qx, &sx);
 }
 
+// M = 1 over fp32 inputs: can the quantisation run in the GEMV's prologue?  Sets
+// a->has_pro / a->pro and *shape; false when the launch needs a separate quantiser pass.
+// KSPLIT (few row blocks): only with one input shared by all problems.  ROWS: each
+// workgroup quantises its own problem's row, so nw (4, 2 or 1 waves) must divide every
+// problem's row-block count.
+static bool prologue_launch(const GemvShape& base, int U, const int* Nb, int G, int Kp_max, const QuantProb& shared,
+                            GemvArgs* a, GemvShape* shape) {
+    const size_t row_lds = (size_t)Kp_max + sizeof(RowSmem);
+    if (base.ksplit) {
+        if (U != 1 || (size_t)base.nw * kRowBlock * sizeof(int) + row_lds > 64 * 1024) return false;
+        a->has_pro = 1;
+        a->pro = shared;
+        *shape = base;
+        return true;
+    }
+    if (row_lds > 64 * 1024) return false;
+    int nw = 4;
+    for (int g = 0; g < G; ++g)
+        while (Nb[g] % nw) nw >>= 1;
+    a->has_pro = 2;
+    a->pro = QuantProb{};
+    a->pro.Kp = Kp_max;
+    *shape = GemvShape{false, nw};
+    return true;
+}
+
 // GEMV (M <= kGemvMaxM) or MFMA GEMM on activations already in the qx layout.
 static int launch_matrix(rt_ctx* ctx, const rt_weights* w, const int8_t* qx, const float* sx, int M,
                          const float* row_scale, void* out, bool out_i32, const float* res = nullptr) {
@@ -335,6 +367,21 @@ static int run_linear(rt_ctx* ctx, const rt_weights* w, const float* x, const in
     if ((!x && !q) || !out) return fail(RT_EINVAL, std::string(who) + ": NULL pointer");
     if (w->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": weights live on another device");
     DeviceGuard g(ctx->device);
+    if (M == 1 && x && !out_i32) {  // one launch: the GEMV quantises x in its prologue
+        GemvArgs a{};
+        a.G = 1;
+        a.M = 1;
+        a.total_rb = w->Np / kRowBlock;
+        a.p = GemvProb{w->tiles, nullptr, nullptr, row_scale, out, w->scale, w->N, w->C, w->N, 0, nullptr, x, w->K};
+        const QuantProb src{x, nullptr, nullptr, nullptr, nullptr, w->K, w->Kp, kQuant, nullptr, 0.0f, nullptr,
+                            nullptr, 0, 0, 0};
+        const int nb = a.total_rb;
+        GemvShape shape;
+        if (prologue_launch(gemv_shape(a.total_rb, 1, w->C), 1, &nb, 1, w->Kp, src, &a, &shape)) {
+            RT_HIP(launch_gemv(a, 1, shape, ctx->stream));
+            return RT_OK;
+        }
+    }
     int8_t* qx;
     float* sx;
     rc = stage_activations(ctx, x, q, M, w->K, act_rows(M), qx_blocked(M), nullptr, nullptr, &qx, &sx);
@@ -454,6 +501,21 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
     }
     p->total_rb = wg;
     p->shape = gemv_shape(wg, (M + p->mt - 1) / p->mt, minC);
+    if (M == 1) {
+        std::vector<int> nb(G);
+        int kp_max = 0;
+        for (int g = 0; g < G; ++g) {
+            p->probs[g].xs = x[g];
+            p->probs[g].K = w[g]->K;
+            nb[g] = w[g]->Np / kRowBlock;
+            kp_max = std::max(kp_max, round_up(w[g]->K, kChunk));
+        }
+        GemvArgs probe{};
+        if (prologue_launch(p->shape, p->U, nb.data(), G, kp_max, p->quant[0], &probe, &p->run_shape)) {
+            p->run_pro = probe.has_pro;
+            p->pro = probe.pro;
+        }
+    }
     if (M > kGemvMaxM)
         for (int g = 0; g < G; ++g)
             p->gemms.push_back(GemmArgs{w[g]->tiles, p->probs[g].qx, p->probs[g].sx, nullptr, y[g], w[g]->scale, M,
@@ -492,6 +554,20 @@ int rt_plan_quantize(rt_ctx* ctx, const rt_plan* plan) {
 }
 
 int rt_plan_run(rt_ctx* ctx, const rt_plan* plan) {
+    if (plan && plan->run_pro && ctx && plan->device == ctx->device) {  // one launch: quantise in the prologue
+        DeviceGuard g(ctx->device);
+        GemvArgs a{};
+        a.dev = plan->dev_probs;
+        a.rb2p = plan->dev_rb2p;
+        a.G = plan->G;
+        a.M = 1;
+        a.out_i32 = 0;
+        a.total_rb = plan->total_rb;
+        a.has_pro = plan->run_pro;
+        a.pro = plan->pro;
+        RT_HIP(launch_gemv(a, 1, plan->run_shape, ctx->stream));
+        return RT_OK;
+    }
     int rc = rt_plan_quantize(ctx, plan);
     return rc ? rc : rt_plan_gemv(ctx, plan);
 }

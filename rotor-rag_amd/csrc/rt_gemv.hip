@@ -54,7 +54,13 @@ typedef __attribute__((address_space(4))) const int cidx;
 __device__ __forceinline__ GemvProb find_prob(const GemvArgs& a, int rbg) {
     if (!a.dev) return a.p;
     const cprob* q = (cprob*)a.dev + ((cidx*)a.rb2p)[rbg];
-    return GemvProb{q->w, q->qx, q->sx, q->rs, q->out, q->s_w, q->N, q->C, q->ldo, q->wg_begin, q->res};
+    return GemvProb{q->w, q->qx, q->sx, q->rs, q->out, q->s_w, q->N, q->C, q->ldo, q->wg_begin, q->res, q->xs, q->K};
+}
+
+// The plain absmax quantisation of problem P's own input row (has_pro == 2).
+__device__ __forceinline__ QuantProb own_source(const GemvProb& P) {
+    return QuantProb{P.xs, nullptr, nullptr, nullptr, nullptr, P.K, P.C * kChunk, kQuant, nullptr, 0.0f, nullptr,
+                     nullptr, 0, 0, 0};
 }
 
 template <int MT, typename XP>
@@ -141,28 +147,51 @@ __device__ __forceinline__ void emit(const GemvArgs& a, const GemvProb& P, int r
     }
 }
 
-template <int MT>
+// PRO 0: activations quantised beforehand (qx); PRO 1 (M = 1): the workgroup first
+// quantises its problem's own fp32 row into LDS.  With PRO the host sizes workgroups so
+// that nw divides every problem's row-block count: all waves of a workgroup are live and
+// serve one problem (the prologue synchronises the workgroup).
+template <int MT, int PRO>
 __global__ void __launch_bounds__(1024) gemv_rows_kernel(GemvArgs a) {
     constexpr int U = MT == 1 ? 4 : 2;
+    extern __shared__ __attribute__((aligned(16))) v4u lds_row[];
     const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform
     const int rbg = blockIdx.x * nw + wave;                               // global row block
-    if (rbg >= a.total_rb) return;
+    if (PRO == 0 && rbg >= a.total_rb) return;
     const GemvProb P = find_prob(a, rbg);
     const int rb = rbg - P.wg_begin;
     const int m0 = blockIdx.y * MT;
     const int C = P.C, ldx = C * 16;
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, C * 1024, kBufDword3);
-    cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
     int accP[MT], accN[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
     v4u A[U], B[U];
-    gemv_preload<U>(rsrc, lane * 16, 0, A, B);
-    gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, 0, C, accP, accN, A, B);
+    if constexpr (PRO != 0) {
+        static_assert(MT == 1, "the prologue quantises one token");
+        const QuantProb Q = own_source(P);
+        RowRegs rr;
+        const bool early = row_fits1(Q, blockDim.x);
+        if (early) row_load1(Q, 0, rr);
+        gemv_preload<U>(rsrc, lane * 16, 0, A, B, false);
+        RowSmem* sm = reinterpret_cast<RowSmem*>(lds_row + (Q.Kp >> 4));
+        const QxRow qrow{lds_row, 4, 1};
+        const float sx = early ? row_finish1(Q, rr, qrow, nullptr, nullptr, sm)
+                               : row_quantize<1>(Q, 0, qrow, nullptr, nullptr, sm);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) emit(a, P, rb, m0, m, lane, accP[m] - accN[m]);
+        for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane * 16, U + i);
+        __syncthreads();
+        gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lds_row, ldx, 0, C, accP, accN, A, B);
+        emit(a, P, rb, 0, 0, lane, accP[0] - accN[0], sx);
+    } else {
+        cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
+        gemv_preload<U>(rsrc, lane * 16, 0, A, B);
+        gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, 0, C, accP, accN, A, B);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) emit(a, P, rb, m0, m, lane, accP[m] - accN[m]);
+    }
 }
 
 // LDS of the KSPLIT kernel: [nw][MT][64] int partial sums, then (prologue) the
@@ -261,7 +290,12 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
     if (a.total_rb <= 0 || a.M <= 0) return hipSuccess;
     const unsigned mblocks = (unsigned)((a.M + mt - 1) / mt);
     const dim3 block((unsigned)(64 * shape.nw));
-    if (a.has_pro) {  // single token, prologue-quantised input: KSPLIT shape only
+    if (a.has_pro == 2) {  // single token, each problem's own row quantised in the prologue: ROWS
+        if (mt != 1 || a.M != 1 || shape.ksplit || a.total_rb % shape.nw) return hipErrorInvalidValue;
+        const dim3 grid((unsigned)(a.total_rb / shape.nw), 1);
+        const size_t lds = (size_t)a.pro.Kp + sizeof(RowSmem);  // pro.Kp: the largest Kp of the problems
+        hipLaunchKernelGGL((gemv_rows_kernel<1, 1>), grid, block, lds, s, a);
+    } else if (a.has_pro) {  // single token, prologue-quantised input: KSPLIT shape only
         if (mt != 1 || a.M != 1 || !shape.ksplit) return hipErrorInvalidValue;
         const dim3 grid((unsigned)a.total_rb, 1);
         size_t lds = (size_t)shape.nw * kRowBlock * sizeof(int) + (size_t)a.pro.Kp + sizeof(RowSmem);
@@ -281,10 +315,10 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
     } else {
         const dim3 grid((unsigned)((a.total_rb + shape.nw - 1) / shape.nw), mblocks);
         switch (mt) {
-            case 1: hipLaunchKernelGGL(gemv_rows_kernel<1>, grid, block, 0, s, a); break;
-            case 2: hipLaunchKernelGGL(gemv_rows_kernel<2>, grid, block, 0, s, a); break;
-            case 4: hipLaunchKernelGGL(gemv_rows_kernel<4>, grid, block, 0, s, a); break;
-            case 8: hipLaunchKernelGGL(gemv_rows_kernel<8>, grid, block, 0, s, a); break;
+            case 1: hipLaunchKernelGGL((gemv_rows_kernel<1, 0>), grid, block, 0, s, a); break;
+            case 2: hipLaunchKernelGGL((gemv_rows_kernel<2, 0>), grid, block, 0, s, a); break;
+            case 4: hipLaunchKernelGGL((gemv_rows_kernel<4, 0>), grid, block, 0, s, a); break;
+            case 8: hipLaunchKernelGGL((gemv_rows_kernel<8, 0>), grid, block, 0, s, a); break;
             default: return hipErrorInvalidValue;
         }
     }

@@ -76,6 +76,8 @@ struct GemvProb {
     int N, C, ldo;
     int wg_begin;        // first global row block of this problem (prefix sum over problems)
     const float* res;    // optional fp32 [M][ldo] added to y (may alias out)
+    const float* xs;     // has_pro == 2: the problem's own fp32 input row [K] (quantised in the prologue)
+    int K;               // has_pro == 2: its length
 };
 
 struct GemvArgs {
@@ -84,8 +86,9 @@ struct GemvArgs {
     int G, M, out_i32;
     int total_rb;         // row blocks over all problems
     GemvProb p;           // the problem of a single-problem launch
-    int has_pro;          // M = 1: every workgroup quantises `pro` (row 0) into LDS first
-    QuantProb pro;        // source row of the prologue (mode, x, aux, aux2, eps, K, Kp)
+    int has_pro;          // M = 1: every workgroup quantises its input row into LDS first:
+                          // 1 the shared row `pro` (KSPLIT), 2 its problem's xs (ROWS, plain absmax)
+    QuantProb pro;        // has_pro == 1: source row of the prologue (mode, x, aux, aux2, eps, K, Kp)
 };
 
 struct GemvShape {

@@ -73,18 +73,20 @@ class LinearPlan:
         self._keep = keep  # tensors / weights the plan's device pointers refer to
 
     def run(self) -> None:
+        """Run the plan: one launch at M = 1 when the GEMV quantises in its prologue,
+        else quantize() then gemv()."""
         b = self._backend
         b._bind_stream()
         _hip.check(_hip.load().rt_plan_run(b.ctx, self.handle), "rt_plan_run")
 
     def quantize(self) -> None:
-        """First launch of run(): per-token quantisation of the distinct inputs."""
+        """Two-launch form of run(), first launch: per-token quantisation of the distinct inputs."""
         b = self._backend
         b._bind_stream()
         _hip.check(_hip.load().rt_plan_quantize(b.ctx, self.handle), "rt_plan_quantize")
 
     def gemv(self) -> None:
-        """Second launch of run(): the ternary GEMV over all problems."""
+        """Two-launch form of run(), second launch: the ternary GEMV over all problems."""
         b = self._backend
         b._bind_stream()
         _hip.check(_hip.load().rt_plan_gemv(b.ctx, self.handle), "rt_plan_gemv")

@@ -167,6 +167,66 @@ def test_plan_matches_single_calls(hip, M):
             assert torch.equal(y, hip.linear_device(w, x))
 
 
+# M = 1 plans whose one launch quantises in the GEMV prologue: (N, K) per problem.
+# >= 1024 row blocks -> ROWS shape, each workgroup quantising its own problem's row with
+# nw = 4 / 2 / 1 waves (the largest dividing every problem's row-block count); K = 6912
+# exceeds one 16-group per thread (the multi-pass quantiser); few row blocks with one
+# shared input -> KSPLIT prologue.
+PROLOGUE_PLANS = {
+    "rows_nw4": [(6912, 2560)] * 10,
+    "rows_nw2_ragged": [(6912, 2500)] * 10 + [(100, 2500), (2560, 2500)],
+    "rows_nw1_long_k": [(6912, 6912)] * 10 + [(50, 6912), (130, 6912)],
+    "ksplit_shared": [(2560, 2560), (640, 2560), (640, 2560)],
+}
+
+
+@pytest.mark.parametrize("name", list(PROLOGUE_PLANS))
+def test_plan_run_prologue_equals_two_launches(hip, name):
+    import torch
+
+    shapes = PROLOGUE_PLANS[name]
+    rng = np.random.default_rng(len(name))
+    shared = name.startswith("ksplit")
+    x0 = torch.from_numpy(rng.standard_normal((1, shapes[0][1]), dtype=np.float32)).cuda()
+    ws, xs, ys, Ws = [], [], [], []
+    for N, K in shapes:
+        W, scale = O.make_ternary(rng, N, K)
+        Ws.append((W, scale))
+        ws.append(hip.upload(O.pack_rotor(W), K, scale))
+        xs.append(x0 if shared else torch.from_numpy(rng.standard_normal((1, K), dtype=np.float32)).cuda())
+        ys.append(torch.full((1, N), float("nan"), dtype=torch.float32, device="cuda"))
+    plan = hip.plan(ws, xs, ys)
+    plan.run()
+    torch.cuda.synchronize()
+    fused = [y.clone() for y in ys]
+    for y in ys:
+        y.fill_(float("nan"))
+    plan.quantize()
+    plan.gemv()
+    torch.cuda.synchronize()
+    for a, b in zip(fused, ys):
+        assert torch.equal(a, b)
+    for g in (0, len(shapes) - 2, len(shapes) - 1):  # against the oracle
+        W, scale = Ws[g]
+        x = xs[g].cpu().numpy()
+        y_ref, q, s, acc = O.ternary_linear(x, W, scale)
+        assert np.array_equal(fused[g].cpu().numpy(), (acc.astype(np.float32) * s[:, None]) * np.float32(scale))
+
+
+@pytest.mark.parametrize("N,K", [(65600, 300), (65664, 2560)])
+def test_linear_f32_single_rows_prologue(hip, N, K):
+    """One linear with >= 1024 row blocks at M = 1: the ROWS kernel quantises x itself
+    (1025 row blocks -> one wave per workgroup, 1026 -> two)."""
+    import torch
+
+    x, W, scale = _case(N + K, 1, N, K)
+    w = hip.upload(O.pack_rotor(W), K, scale)
+    y = hip.linear_device(w, torch.from_numpy(x)).cpu().numpy()
+    y_ref, q, s, acc = O.ternary_linear(x, W, scale)
+    np.testing.assert_allclose(y, y_ref, atol=ATOL, rtol=RTOL)
+    assert np.array_equal(y, (acc.astype(np.float32) * s[:, None]) * np.float32(scale))
+
+
 def test_ternary_linear_layer_gpu(hip):
     from rotor import gpu_layers
     from rotor.transformer import TernaryLinear

@@ -71,7 +71,7 @@ def test_gemv_kernels_scalar_descriptors_no_spills(gemv):
 
 
 def test_gemv_rows_reads_activations_with_scalar_loads(gemv):
-    (n,) = [n for n in gemv if "gemv_rows_kernelILi1E" in n]
+    (n,) = [n for n in gemv if "gemv_rows_kernelILi1ELi0E" in n]
     assert "s_load_dwordx16" in gemv[n] or "s_load_dwordx8" in gemv[n]
     assert "global_load" not in gemv[n]
 

@@ -112,7 +112,7 @@ int rt_linear_i32(rt_ctx* ctx, const rt_weights* w, const int8_t* q, int M, int3
 
 /* The ternary linear, W2A8: per-token quantise x fp32 [M][K], accumulate in int32,
  * y[m][n] = ((float)acc[m][n] * s_x[m]) * s_w.  y fp32 [M][N] (device).  M = 1 is one
- * launch (the GEMV quantises x in its prologue); otherwise a quantiser launch + one. */
+ * launch (the GEMV quantises x in its prologue); otherwise a quantiser launch + one.
  * Replaces TernaryLinear.forward (src/rotor/transformer.py:111-155; the op at :150)
  * and, per token, GPUTernaryOps.ternary_matmul (src/rotor/gpu_ternary.py:138-202). */
 int rt_linear_f32(rt_ctx* ctx, const rt_weights* w, const float* x, int M, float* y);

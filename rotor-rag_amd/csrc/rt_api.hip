@@ -540,6 +540,13 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
     return RT_OK;
 }
 
+// Plans of up to kInlineProbs problems pass their descriptors as kernel arguments.
+static void inline_probs(const rt_plan* plan, GemvArgs* a) {
+    if (plan->G > kInlineProbs) return;
+    a->ninl = plan->G;
+    for (int g = 0; g < plan->G; ++g) a->inl[g] = plan->probs[g];
+}
+
 int rt_plan_quantize(rt_ctx* ctx, const rt_plan* plan) {
     if (!ctx || !plan) return fail(RT_EINVAL, "rt_plan_quantize: NULL argument");
     if (plan->device != ctx->device) return fail(RT_EINVAL, "rt_plan_quantize: plan belongs to another device");
@@ -559,6 +566,7 @@ int rt_plan_run(rt_ctx* ctx, const rt_plan* plan) {
         GemvArgs a{};
         a.dev = plan->dev_probs;
         a.rb2p = plan->dev_rb2p;
+        inline_probs(plan, &a);
         a.G = plan->G;
         a.M = 1;
         a.out_i32 = 0;
@@ -585,6 +593,7 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
     }
     a.dev = plan->dev_probs;
     a.rb2p = plan->dev_rb2p;
+    inline_probs(plan, &a);
     a.G = plan->G;
     a.M = plan->M;
     a.out_i32 = 0;

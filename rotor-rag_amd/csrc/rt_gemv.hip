@@ -45,13 +45,21 @@ constexpr int kAuxNT = 2;                 // cache policy: non-temporal (streame
 typedef __attribute__((address_space(4))) const int cint;
 typedef __attribute__((address_space(3))) const int lint;
 
-// Problem of global row block rbg: two dependent scalar loads (table, descriptor).  Both
-// sources are read through constant-address-space pointers: merged with a generic one,
-// the descriptor would turn into per-lane flat loads and the buffer resource into a
-// readfirstlane loop.
+// Problem of global row block rbg.  Small plans: the descriptors are kernel arguments and
+// the problem is the last one whose wg_begin <= rbg (scalar compares and selects).  Larger
+// plans: two dependent scalar loads (table, descriptor), both read through
+// constant-address-space pointers: merged with a generic one, the descriptor would turn
+// into per-lane flat loads and the buffer resource into a readfirstlane loop.
 typedef __attribute__((address_space(4))) const GemvProb cprob;
 typedef __attribute__((address_space(4))) const int cidx;
 __device__ __forceinline__ GemvProb find_prob(const GemvArgs& a, int rbg) {
+    if (a.ninl > 0) {  // every descriptor is loaded (independent loads), then selected
+        GemvProb P = a.inl[0];
+#pragma unroll
+        for (int j = 1; j < kInlineProbs; ++j)
+            if (j < a.ninl && rbg >= a.inl[j].wg_begin) P = a.inl[j];
+        return P;
+    }
     if (!a.dev) return a.p;
     const cprob* q = (cprob*)a.dev + ((cidx*)a.rb2p)[rbg];
     return GemvProb{q->w, q->qx, q->sx, q->rs, q->out, q->s_w, q->N, q->C, q->ldo, q->wg_begin, q->res, q->xs, q->K};

@@ -80,6 +80,11 @@ struct GemvProb {
     int K;               // has_pro == 2: its length
 };
 
+// Plans of up to this many problems carry their descriptors in the kernel arguments
+// (GemvArgs::inl): the workgroup finds its problem by comparing its row block with the
+// problems' wg_begin, with no dependent loads from a descriptor table.
+constexpr int kInlineProbs = 4;
+
 struct GemvArgs {
     const GemvProb* dev;  // device descriptor array [G] (plans) or nullptr -> p
     const int* rb2p;      // [total_rb] problem index of every global row block (plans)
@@ -89,6 +94,8 @@ struct GemvArgs {
     int has_pro;          // M = 1: every workgroup quantises its input row into LDS first:
                           // 1 the shared row `pro` (KSPLIT), 2 its problem's xs (ROWS, plain absmax)
     QuantProb pro;        // has_pro == 1: source row of the prologue (mode, x, aux, aux2, eps, K, Kp)
+    int ninl;             // > 0: the G = ninl problems are inl[] (dev and rb2p unused)
+    GemvProb inl[kInlineProbs];
 };
 
 struct GemvShape {

@@ -36,6 +36,14 @@ def test_header_declares_expected_api():
         assert n in names
 
 
+@pytest.mark.parametrize("lang,compiler", [("c", "gcc"), ("c++", "g++")])
+def test_header_compiles_standalone(lang, compiler, tmp_path):
+    """The C ABI header is valid C and C++ on its own (what a cgo / JNI / ctypes user includes)."""
+    r = subprocess.run([compiler, "-fsyntax-only", "-Wall", "-Werror", "-x", lang, str(HEADER)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
 def test_library_exports_every_declared_symbol():
     assert LIB.exists(), "build librotor_hip.so first (__graft_entry__.build())"
     out = subprocess.run(["nm", "-D", "--defined-only", str(LIB)], capture_output=True, text=True, check=True).stdout

@@ -288,6 +288,75 @@ __device__ __forceinline__ bool row_fits1(const QuantProb& P, int T) {
     return P.mode != kAttnNorm && (P.Kp >> 4) <= T;
 }
 
+// One output dword per thread, modes other than kAttnNorm, K % 64 == 0 and K / 4 <=
+// threads: thread t owns dword i = t % 4 of group g = t / 4, i.e. elements
+// 16 g + i + 4 j, j = 0..3 (byte j of that dword in the permuted layout).  Four elements
+// per thread instead of sixteen spread the row's arithmetic over four times as many waves.
+struct RowRegs4 {
+    float v[4], u[4], w[4];
+    bool live;  // wave-uniform: some lane of this wave owns a dword
+};
+
+__device__ __forceinline__ bool row_fits4(const QuantProb& P, int T) {
+    return P.mode != kAttnNorm && (P.K & 63) == 0 && P.K / 4 <= T;
+}
+
+__device__ __forceinline__ void row_load4(const QuantProb& P, RowRegs4& r) {
+    const int t = threadIdx.x, K = P.K;
+    r.live = __builtin_amdgcn_readfirstlane(threadIdx.x & ~63) < K / 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r.v[j] = r.u[j] = r.w[j] = 0.0f;
+    if (t < K / 4) {
+        const int k0 = 16 * (t >> 2) + (t & 3);
+        const float* nw = norm_weight(P);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            r.v[j] = P.x[k0 + 4 * j];
+            if (has_relu2(P)) r.u[j] = P.aux[k0 + 4 * j];
+            if (has_norm(P)) r.w[j] = nw[k0 + 4 * j];
+        }
+    }
+}
+
+__device__ __forceinline__ float row_finish4(const QuantProb& P, RowRegs4& r, v4u* lq, RowSmem* sm) {
+    auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
+    auto dadd_op = [](double x, double y) { return x + y; };
+    const int t = threadIdx.x, K = P.K;
+    const bool mine = t < K / 4;
+    float (&v)[4] = r.v;
+    if (mine && has_relu2(P)) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = v[j] > 0.0f ? (v[j] * v[j]) * r.u[j] : 0.0f;
+    }
+    if (has_norm(P)) {
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ss += (double)v[j] * (double)v[j];
+        ss = block_reduce(ss, sm->d, dadd_op, r.live);
+        const float norm = sqrtf((float)(ss / (double)K) + P.eps);
+        if (mine) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] = (v[j] / norm) * r.w[j];
+        }
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = block_reduce(amax, sm->f, fmax_op, r.live);
+    const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
+    if (mine) {  // byte b of the dword = element 16 g + i + 4 b = v[b]
+        unsigned dw = 0u;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            float q = rintf(v[b] / sc);
+            q = fminf(fmaxf(q, -128.0f), 127.0f);
+            dw |= ((unsigned)(int)q & 0xffu) << (8 * b);
+        }
+        reinterpret_cast<unsigned*>(lq)[t] = dw;
+    }
+    return sc;
+}
+
 // kAttnNorm for one token with K % 64 == 0 and at most kAttnSMax partial blocks: lane
 // t owns output dword i = t % 4 of group g = t / 4, i.e. elements 16 g + i + 4 j,
 // j = 0..3 (one dword of the permuted layout).  attn_load1 issues every load the lane

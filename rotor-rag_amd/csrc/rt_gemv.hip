@@ -27,6 +27,7 @@
 //     t0: sel 0,1,2,3  -> 00, FF, 01, 00  =  w  for f = 00, 01, 10, 11
 //     t1: sel 0,4,8,12 -> 00, 01, FF, 00  = -w  for f = 00, 01, 10, 11
 // so element positions 0/2 accumulate into accP and 1/3 into accN, acc = accP - accN.
+#include <algorithm>
 #include <type_traits>
 
 #include "rt_rowquant.h"
@@ -202,14 +203,19 @@ __global__ void __launch_bounds__(1024) gemv_rows_kernel(GemvArgs a) {
     }
 }
 
+// The attention prologue holds 4 (kAttnSMax + 1) + 2 kAttnSMax values per thread in
+// registers; its kernel runs at most 10 waves per workgroup, which leaves 168 VGPRs per
+// lane (at 16 waves the budget is 128 and the partials would spill to scratch).
+constexpr int kAttnMaxThreads = 640;
+
 // LDS of the KSPLIT kernel: [nw][MT][64] int partial sums, then (prologue) the
 // quantised input row (Kp bytes) and the reduction scratch of the prologue.
 // PRO: 0 no prologue; 1 prologue quantising a row source (plain, RMSNorm, relu²·up,
 // relu²·up + sub-norm), 16 elements per thread; 3 the same with 4 elements per thread
-// (K % 64 == 0, K / 4 <= threads); 2 prologue combining decode-attention partials
-// (kAttnNorm).
+// (K % 64 == 0, K / 4 <= threads, 16-byte aligned sources); 2 prologue combining
+// decode-attention partials (kAttnNorm).
 template <int MT, int PRO>
-__global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
+__global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024) gemv_ksplit_kernel(GemvArgs a) {
     constexpr int U = MT == 1 ? 4 : 2;
     extern __shared__ __attribute__((aligned(16))) int red[];
     const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
@@ -241,8 +247,10 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, ce * 1024, kBufDword3);
     v4u A[U], B[U];
-    // with a prologue only the first batch is in flight during it (register budget)
-    gemv_preload<U>(rsrc, lane * 16, cb, A, B, PRO == 0);
+    // With a prologue only the first batch is in flight during it (register budget); the
+    // attention prologue holds its partials in registers first and issues it after their
+    // combine.
+    if (PRO != 2 || !early) gemv_preload<U>(rsrc, lane * 16, cb, A, B, PRO == 0);
     int accP[MT], accN[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
@@ -255,7 +263,13 @@ __global__ void __launch_bounds__(1024) gemv_ksplit_kernel(GemvArgs a) {
         if (!early) sx_pro = row_quantize<1>(a.pro, 0, qrow, nullptr, nullptr, sm);
         else if constexpr (PRO == 1) sx_pro = row_finish1(a.pro, rr, qrow, nullptr, nullptr, sm);
         else if constexpr (PRO == 3) sx_pro = row_finish4(a.pro, rr, lq, sm);
-        else sx_pro = attn_finish1(a.pro, rr, lq, sm);
+        else {
+            float v[4];
+            attn_combine1(a.pro, rr, v);
+            const float w[4] = {rr.w[0], rr.w[1], rr.w[2], rr.w[3]};
+            gemv_preload<U>(rsrc, lane * 16, cb, A, B, false);
+            sx_pro = attn_norm1(a.pro, v, w, rr.live, lq, sm);
+        }
 #pragma unroll
         for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane * 16, cb + U + i);
         __syncthreads();
@@ -301,6 +315,8 @@ GemvShape gemv_shape(int total_rb, int m_blocks, int min_C) {
     return s;
 }
 
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
 hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s) {
     if (a.total_rb <= 0 || a.M <= 0) return hipSuccess;
     const unsigned mblocks = (unsigned)((a.M + mt - 1) / mt);
@@ -313,10 +329,13 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
     } else if (a.has_pro) {  // single token, prologue-quantised input: KSPLIT shape only
         if (mt != 1 || a.M != 1 || !shape.ksplit) return hipErrorInvalidValue;
         const dim3 grid((unsigned)a.total_rb, 1);
-        size_t lds = (size_t)shape.nw * kRowBlock * sizeof(int) + (size_t)a.pro.Kp + sizeof(RowSmem);
-        if (a.pro.mode == kAttnNorm) lds += (size_t)(a.pro.K / a.pro.attn_hd) * (a.pro.attn_S + 1) * sizeof(float);
-        if (a.pro.mode == kAttnNorm) hipLaunchKernelGGL((gemv_ksplit_kernel<1, 2>), grid, block, lds, s, a);
-        else if (a.pro.K % 64 == 0 && a.pro.K / 4 <= (int)block.x)
+        const int nw = a.pro.mode == kAttnNorm ? std::min(shape.nw, kAttnMaxThreads / 64) : shape.nw;
+        size_t lds = (size_t)nw * kRowBlock * sizeof(int) + (size_t)a.pro.Kp + sizeof(RowSmem);
+        if (a.pro.mode == kAttnNorm) {
+            lds += (size_t)(a.pro.K / a.pro.attn_hd) * (a.pro.attn_S + 1) * sizeof(float);
+            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 2>), grid, dim3((unsigned)(64 * nw)), lds, s, a);
+        } else if (a.pro.K % 64 == 0 && a.pro.K / 4 <= (int)block.x && aligned16(a.pro.x) && aligned16(a.pro.aux) &&
+                 aligned16(a.pro.aux2))
             hipLaunchKernelGGL((gemv_ksplit_kernel<1, 3>), grid, block, lds, s, a);
         else hipLaunchKernelGGL((gemv_ksplit_kernel<1, 1>), grid, block, lds, s, a);
     } else if (shape.ksplit) {

@@ -288,17 +288,39 @@ __device__ __forceinline__ bool row_fits1(const QuantProb& P, int T) {
     return P.mode != kAttnNorm && (P.Kp >> 4) <= T;
 }
 
-// One output dword per thread, modes other than kAttnNorm, K % 64 == 0 and K / 4 <=
-// threads: thread t owns dword i = t % 4 of group g = t / 4, i.e. elements
-// 16 g + i + 4 j, j = 0..3 (byte j of that dword in the permuted layout).  Four elements
-// per thread instead of sixteen spread the row's arithmetic over four times as many waves.
+// Four consecutive elements per thread (K % 64 == 0, K / 4 <= threads): thread t owns
+// elements k = 4 t .. 4 t + 3, read with one 16-byte load per operand.  In the permuted
+// layout element k = 16 g + e of group g sits at byte 4 (e % 4) + e / 4, so the thread's
+// four int8 values go to bytes 4 b + t % 4 (b = 0..3) of group t / 4: scatter_q4 writes
+// them to the LDS row one byte each.  Four elements per thread instead of sixteen spread
+// the row's arithmetic over four times as many waves.
+typedef float v4f_a8 __attribute__((ext_vector_type(4), aligned(8)));
+typedef float v2f_a8 __attribute__((ext_vector_type(2), aligned(8)));
+
+__device__ __forceinline__ void scatter_q4(const float (&v)[4], float sc, v4u* lq) {
+    const int t = threadIdx.x;
+    unsigned char* lb = reinterpret_cast<unsigned char*>(lq) + 16 * (t >> 2) + (t & 3);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        float q = rintf(v[b] / sc);
+        q = fminf(fmaxf(q, -128.0f), 127.0f);
+        lb[4 * b] = (unsigned char)(int)q;
+    }
+}
+
 struct RowRegs4 {
     float v[4], u[4], w[4];
-    bool live;  // wave-uniform: some lane of this wave owns a dword
+    bool live;  // wave-uniform: some lane of this wave owns elements
 };
 
 __device__ __forceinline__ bool row_fits4(const QuantProb& P, int T) {
     return P.mode != kAttnNorm && (P.K & 63) == 0 && P.K / 4 <= T;
+}
+
+__device__ __forceinline__ void load4(const float* p, float (&v)[4]) {
+    const v4f_a8 t = *reinterpret_cast<const v4f_a8*>(p);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = t[j];
 }
 
 __device__ __forceinline__ void row_load4(const QuantProb& P, RowRegs4& r) {
@@ -307,14 +329,9 @@ __device__ __forceinline__ void row_load4(const QuantProb& P, RowRegs4& r) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) r.v[j] = r.u[j] = r.w[j] = 0.0f;
     if (t < K / 4) {
-        const int k0 = 16 * (t >> 2) + (t & 3);
-        const float* nw = norm_weight(P);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            r.v[j] = P.x[k0 + 4 * j];
-            if (has_relu2(P)) r.u[j] = P.aux[k0 + 4 * j];
-            if (has_norm(P)) r.w[j] = nw[k0 + 4 * j];
-        }
+        load4(P.x + 4 * t, r.v);
+        if (has_relu2(P)) load4(P.aux + 4 * t, r.u);
+        if (has_norm(P)) load4(norm_weight(P) + 4 * t, r.w);
     }
 }
 
@@ -344,29 +361,20 @@ __device__ __forceinline__ float row_finish4(const QuantProb& P, RowRegs4& r, v4
     for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(v[j]));
     amax = block_reduce(amax, sm->f, fmax_op, r.live);
     const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
-    if (mine) {  // byte b of the dword = element 16 g + i + 4 b = v[b]
-        unsigned dw = 0u;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            float q = rintf(v[b] / sc);
-            q = fminf(fmaxf(q, -128.0f), 127.0f);
-            dw |= ((unsigned)(int)q & 0xffu) << (8 * b);
-        }
-        reinterpret_cast<unsigned*>(lq)[t] = dw;
-    }
+    if (mine) scatter_q4(v, sc, lq);
     return sc;
 }
 
-// kAttnNorm for one token with K % 64 == 0 and at most kAttnSMax partial blocks: lane
-// t owns output dword i = t % 4 of group g = t / 4, i.e. elements 16 g + i + 4 j,
-// j = 0..3 (one dword of the permuted layout).  attn_load1 issues every load the lane
-// needs (its head's block maxima and sums, its 4 values of every block, its 4 norm
-// weights) at once; attn_finish1 combines them in the operation order of
-// attn_combine_element, then RMSNorm and quantisation as row_finish1.
+// kAttnNorm for one token with K % 64 == 0 and at most kAttnSMax partial blocks, four
+// consecutive elements k = 4 t .. 4 t + 3 per thread (one head h = k / hd, dims
+// d = k % hd ..): attn_load1 issues every load the thread needs at once -- per block one
+// 16-byte load of its four values and one 8-byte load of the block's (max, sum) -- and its
+// four norm weights; attn_finish1 combines them in the operation order of
+// attn_combine_element, then RMSNorm and quantisation as row_finish4.
 constexpr int kAttnSMax = 10;  // Lmax <= 640 (longer contexts take the general path)
 struct AttnRegs {
     float p[kAttnSMax][4], m[kAttnSMax], z[kAttnSMax], w[4];
-    bool live;  // wave-uniform: some lane of this wave owns a dword
+    bool live;  // wave-uniform: some lane of this wave owns elements
 };
 
 __device__ __forceinline__ bool attn_fits1(const QuantProb& P, int T) {
@@ -375,41 +383,37 @@ __device__ __forceinline__ bool attn_fits1(const QuantProb& P, int T) {
 }
 
 __device__ __forceinline__ void attn_load1(const QuantProb& P, AttnRegs& r) {
-    const int t = threadIdx.x, K = P.K, hd = P.attn_hd, S = P.attn_S;
+    const int K = P.K, hd = P.attn_hd, S = P.attn_S;
     r.live = __builtin_amdgcn_readfirstlane(threadIdx.x & ~63) < K / 4;
+    // Straight-line loads, no branch: threads past K / 4 re-read the last thread's
+    // elements and blocks past S re-read block S - 1; the combine ignores both.
+    // Raw buffer loads: one resource for the partials, the lane's offset in a VGPR and the
+    // block stride in the scalar offset, so the 2 S loads need no per-load address registers.
+    const int t = min((int)threadIdx.x, K / 4 - 1);
+    const int k0 = 4 * t, h = k0 / hd, d = k0 % hd, row = (hd + 2) * 4;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)P.x, 0, (unsigned)((K / hd) * S * row), kBufDword3);
+    const int off = h * S * row;
 #pragma unroll
     for (int s = 0; s < kAttnSMax; ++s) {
-        r.m[s] = -INFINITY;
-        r.z[s] = 0.0f;
+        const int so = min(s, S - 1) * row;
+        const v4f_a8 pv = __builtin_bit_cast(v4f_a8, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 4 * d, so, 0));
+        const v2f_a8 mz = __builtin_bit_cast(v2f_a8, __builtin_amdgcn_raw_buffer_load_b64(rs, off + 4 * hd, so, 0));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) r.p[s][j] = 0.0f;
+        for (int j = 0; j < 4; ++j) r.p[s][j] = pv[j];
+        r.m[s] = mz[0];
+        r.z[s] = mz[1];
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) r.w[j] = 0.0f;
-    if (t < K / 4) {
-        const int g = t >> 2, i = t & 3, k0 = 16 * g, h = k0 / hd, d = k0 % hd + i;
-        const float* wh = P.x + (size_t)h * S * (hd + 2);
-#pragma unroll
-        for (int s = 0; s < kAttnSMax; ++s) {
-            if (s < S) {
-                const float* ps = wh + (size_t)s * (hd + 2);
-                r.m[s] = ps[hd];
-                r.z[s] = ps[hd + 1];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) r.p[s][j] = ps[d + 4 * j];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) r.w[j] = P.aux[k0 + i + 4 * j];
-    }
+    load4(P.aux + k0, r.w);
 }
 
-__device__ __forceinline__ float attn_finish1(const QuantProb& P, AttnRegs& r, v4u* lq, RowSmem* sm) {
-    auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
-    auto dadd_op = [](double x, double y) { return x + y; };
+// The combine (attn_combine1, ends the AttnRegs' lifetime) and the RMSNorm +
+// quantisation (attn_norm1) are separate so a caller can issue loads in between.
+__device__ __forceinline__ void attn_combine1(const QuantProb& P, const AttnRegs& r, float (&v)[4]) {
     const int t = threadIdx.x, K = P.K, S = P.attn_S;
     const bool mine = t < K / 4;
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = 0.0f;
     if (mine) {
         float mx = -INFINITY;
 #pragma unroll
@@ -427,31 +431,30 @@ __device__ __forceinline__ float attn_finish1(const QuantProb& P, AttnRegs& r, v
 #pragma unroll
         for (int j = 0; j < 4; ++j) v[j] = num[j] / den;
     }
+}
+
+__device__ __forceinline__ float attn_norm1(const QuantProb& P, float (&v)[4], const float (&w)[4], bool live,
+                                            v4u* lq, RowSmem* sm) {
+    auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
+    auto dadd_op = [](double x, double y) { return x + y; };
+    const int t = threadIdx.x, K = P.K;
+    const bool mine = t < K / 4;
     double ss = 0.0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) ss += (double)v[j] * (double)v[j];
-    ss = block_reduce(ss, sm->d, dadd_op, r.live);
+    ss = block_reduce(ss, sm->d, dadd_op, live);
     const float norm = sqrtf((float)(ss / (double)K) + P.eps);
     float amax = 0.0f;
     if (mine) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            v[j] = (v[j] / norm) * r.w[j];
+            v[j] = (v[j] / norm) * w[j];
             amax = fmaxf(amax, fabsf(v[j]));
         }
     }
-    amax = block_reduce(amax, sm->f, fmax_op, r.live);
+    amax = block_reduce(amax, sm->f, fmax_op, live);
     const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
-    if (mine) {  // byte b of dword i of a group = element 4 b + i = v[b]
-        unsigned dw = 0u;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            float q = rintf(v[b] / sc);
-            q = fminf(fmaxf(q, -128.0f), 127.0f);
-            dw |= ((unsigned)(int)q & 0xffu) << (8 * b);
-        }
-        reinterpret_cast<unsigned*>(lq)[t] = dw;
-    }
+    if (mine) scatter_q4(v, sc, lq);
     return sc;
 }
 

@@ -5,7 +5,8 @@ can silently lose:
   * GEMV kernels read their problem descriptors with scalar loads: no flat (per-lane)
     loads, and no readfirstlane "waterfall" loops (a loop of v_readfirstlane + 64-bit
     compares that makes a per-lane buffer resource uniform, once per chunk);
-  * no register spills (scratch) in the GEMV kernels;
+  * no register spills (scratch) in the GEMV kernels (a spill of a value just loaded
+    makes the wave wait for that load, serialising the prologue's loads);
   * the GEMM's main loop is free of scratch traffic and of waterfall loops.
 """
 import re
@@ -67,7 +68,7 @@ def test_gemv_kernels_scalar_descriptors_no_spills(gemv):
         t = gemv[n]
         assert "flat_load" not in t, f"{n}: per-lane flat loads"
         assert _waterfalls(t) == 0, f"{n}: readfirstlane loop"
-        assert "scratch_" not in t or "gemv_ksplit_kernelILi1ELi2E" in n, f"{n}: register spills"
+        assert "scratch_" not in t, f"{n}: register spills"
 
 
 def test_gemv_rows_reads_activations_with_scalar_loads(gemv):

@@ -134,7 +134,7 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restri
                                                            float* __restrict__ Vc, const float* __restrict__ rope,
                                                            int H, int Hkv, int Lmax, const int* __restrict__ pos_p,
                                                            float scale, float* __restrict__ work) {
-    constexpr int BL = 64, half = HD / 2;
+    constexpr int BL = 64, half = HD / 2, G = 256 / HD, KD = HD / 4, VN = BL / G;
     __shared__ float qs[HD];
     __shared__ float ks[HD];
     __shared__ float vs[HD];
@@ -143,8 +143,23 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restri
     __shared__ float ored[256];
     const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
-    const int kh = h / (H / Hkv), pos = *pos_p, L = pos + 1;
-    const int j0 = s * BL, nk = min(BL, L - j0);  // keys of this block (may be <= 0)
+    const int kh = h / (H / Hkv), j0 = s * BL;
+    // The block's keys and values do not depend on the position: their loads go out first
+    // (wave w: dims [w HD/4, (w+1) HD/4) of key j0 + lane; thread (d, g): value dim d of
+    // keys g, g + G, ..), together with the position's.  Keys past Lmax re-read the last
+    // cached key; keys past the position are masked below.
+    const int d = t % HD, g = t / HD;
+    float kreg[KD], vreg[VN];
+    {
+        const float* K = Kc + (size_t)kh * HD * Lmax + min(j0 + lane, Lmax - 1);
+#pragma unroll
+        for (int i = 0; i < KD; ++i) kreg[i] = K[(size_t)(wave * KD + i) * Lmax];
+        const float* V = Vc + (size_t)kh * Lmax * HD + d;
+#pragma unroll
+        for (int i = 0; i < VN; ++i) vreg[i] = V[(size_t)min(j0 + g + i * G, Lmax - 1) * HD];
+    }
+    const int pos = *pos_p, L = pos + 1;
+    const int nk = min(BL, L - j0);  // keys of this block (may be <= 0)
     float* wp = work + ((size_t)h * S + s) * (HD + 2);
     if (nk <= 0) {
         if (t == 0) {
@@ -169,37 +184,27 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restri
             }
         }
         if (holds_new)
-            for (int d = t; d < HD; d += 256) vs[d] = vnew[(size_t)kh * HD + d];
+            for (int e = t; e < HD; e += 256) vs[e] = vnew[(size_t)kh * HD + e];
     } else {
-        for (int d = t; d < HD; d += 256) qs[d] = q[(size_t)h * HD + d];
+        for (int e = t; e < HD; e += 256) qs[e] = q[(size_t)h * HD + e];
     }
     __syncthreads();
     if (holds_new && h % (H / Hkv) == 0)  // one writer per KV head
-        for (int d = t; d < HD; d += 256) {
-            Kc[((size_t)kh * HD + d) * Lmax + pos] = ks[d];
-            Vc[((size_t)kh * Lmax + pos) * HD + d] = vs[d];
+        for (int e = t; e < HD; e += 256) {
+            Kc[((size_t)kh * HD + e) * Lmax + pos] = ks[e];
+            Vc[((size_t)kh * Lmax + pos) * HD + e] = vs[e];
         }
-    // scores: wave w sums dims [w*HD/4, (w+1)*HD/4) for key j0 + lane
-    const float* K = Kc + (size_t)kh * HD * Lmax + j0 + lane;
+    // scores: wave w sums its dims for key j0 + lane (the new key from LDS)
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
     if (lane < nk) {
-        if (holds_new) {
-            const bool mine = lane == lp;
+        const bool mine = holds_new && lane == lp;
 #pragma unroll
-            for (int d = wave * (HD / 4); d < (wave + 1) * (HD / 4); d += 4) {
-                a0 += qs[d + 0] * (mine ? ks[d + 0] : K[(size_t)(d + 0) * Lmax]);
-                a1 += qs[d + 1] * (mine ? ks[d + 1] : K[(size_t)(d + 1) * Lmax]);
-                a2 += qs[d + 2] * (mine ? ks[d + 2] : K[(size_t)(d + 2) * Lmax]);
-                a3 += qs[d + 3] * (mine ? ks[d + 3] : K[(size_t)(d + 3) * Lmax]);
-            }
-        } else {
-#pragma unroll
-            for (int d = wave * (HD / 4); d < (wave + 1) * (HD / 4); d += 4) {
-                a0 += qs[d + 0] * K[(size_t)(d + 0) * Lmax];
-                a1 += qs[d + 1] * K[(size_t)(d + 1) * Lmax];
-                a2 += qs[d + 2] * K[(size_t)(d + 2) * Lmax];
-                a3 += qs[d + 3] * K[(size_t)(d + 3) * Lmax];
-            }
+        for (int i = 0; i < KD; i += 4) {
+            const int dd = wave * KD + i;
+            a0 += qs[dd + 0] * (mine ? ks[dd + 0] : kreg[i + 0]);
+            a1 += qs[dd + 1] * (mine ? ks[dd + 1] : kreg[i + 1]);
+            a2 += qs[dd + 2] * (mine ? ks[dd + 2] : kreg[i + 2]);
+            a3 += qs[dd + 3] * (mine ? ks[dd + 3] : kreg[i + 3]);
         }
     }
     part[wave][lane] = (a0 + a1) + (a2 + a3);
@@ -219,18 +224,15 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restri
         }
     }
     __syncthreads();
-    // unnormalised output: thread (d, g) sums keys g, g + G, ... of the block
-    constexpr int G = 256 / HD;
-    const int d = t % HD, g = t / HD;
-    const float* V = Vc + ((size_t)kh * Lmax + j0) * HD + d;
-    auto vrow = [&](int j) { return holds_new && j == lp ? vs[d] : V[(size_t)j * HD]; };
+    // unnormalised output: thread (d, g) sums keys g, g + G, ... of the block, two
+    // alternating partial sums
+    auto vrow = [&](int i) { return holds_new && g + i * G == lp ? vs[d] : vreg[i]; };
     float o0 = 0.f, o1 = 0.f;
-    int j = g;
-    for (; j + G < nk; j += 2 * G) {
-        o0 += pr[j] * vrow(j);
-        o1 += pr[j + G] * vrow(j + G);
+#pragma unroll
+    for (int i = 0; i < VN; i += 2) {
+        if (g + i * G < nk) o0 += pr[g + i * G] * vrow(i);
+        if (g + (i + 1) * G < nk) o1 += pr[g + (i + 1) * G] * vrow(i + 1);
     }
-    if (j < nk) o0 += pr[j] * vrow(j);
     ored[t] = o0 + o1;
     __syncthreads();
     if (g == 0) {

@@ -41,13 +41,19 @@ def test_embed_exact(hip):
     assert np.array_equal(h.cpu().numpy(), O.bf16_to_f32(E)[ids])
 
 
-@pytest.mark.parametrize("M,pos0,H,Hkv,hd", [(1, 0, 20, 5, 128), (1, 37, 20, 5, 128), (7, 3, 8, 2, 64), (16, 0, 4, 4, 64)])
-def test_rope_append_and_attention(hip, M, pos0, H, Hkv, hd):
+# (M, pos0, H, Hkv, hd, Lmax): the tiled prefill kernel (64 (query, head) rows per
+# workgroup, 64-key blocks: several query and key blocks, ragged last blocks, G = H / Hkv
+# of 1, 2, 4) and the general kernel (G = 3 does not divide 64)
+ATTN_CASES = [(1, 0, 20, 5, 128, 64), (1, 37, 20, 5, 128, 64), (7, 3, 8, 2, 64, 64), (16, 0, 4, 4, 64, 64),
+              (100, 50, 20, 5, 128, 256), (70, 0, 8, 4, 64, 128), (130, 5, 4, 4, 64, 192), (33, 20, 6, 2, 64, 64)]
+
+
+@pytest.mark.parametrize("M,pos0,H,Hkv,hd,Lmax", ATTN_CASES)
+def test_rope_append_and_attention(hip, M, pos0, H, Hkv, hd, Lmax):
     import torch
 
     lib, chk = _lib()
     rng = np.random.default_rng(M * 100 + pos0)
-    Lmax = 64
     table = O.rope_table(Lmax, hd, 500000.0)
     # cache already holding pos0 tokens
     Kprev = rng.standard_normal((Hkv, pos0, hd)).astype(np.float32)

@@ -211,9 +211,9 @@ constexpr int kAttnMaxThreads = 640;
 // LDS of the KSPLIT kernel: [nw][MT][64] int partial sums, then (prologue) the
 // quantised input row (Kp bytes) and the reduction scratch of the prologue.
 // PRO: 0 no prologue; 1 prologue quantising a row source (plain, RMSNorm, relu²·up,
-// relu²·up + sub-norm), 16 elements per thread; 3 the same with 4 elements per thread
-// (K % 64 == 0, K / 4 <= threads, 16-byte aligned sources); 2 prologue combining
-// decode-attention partials (kAttnNorm).
+// relu²·up + sub-norm), 16 elements per thread; 3 / 4 the same with 4 / 8 consecutive
+// elements per thread (K % 64 == 0, K / 4 or K / 8 <= threads, 16-byte aligned sources);
+// 2 prologue combining decode-attention partials (kAttnNorm).
 template <int MT, int PRO>
 __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024) gemv_ksplit_kernel(GemvArgs a) {
     constexpr int U = MT == 1 ? 4 : 2;
@@ -224,16 +224,17 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024) gemv_ksplit
     // With a prologue whose row fits one group per thread, the row's loads go out first
     // (they do not depend on the problem); then the problem, the weight resource and the
     // first weight batches, which stream in during the prologue's arithmetic.
-    using Regs = typename std::conditional<PRO == 2, AttnRegs,
-                                           typename std::conditional<PRO == 3, RowRegs4, RowRegs>::type>::type;
+    constexpr int E = PRO == 4 ? 8 : 4;  // elements per thread of PRO 3 / 4
+    using Regs = typename std::conditional<
+        PRO == 2, AttnRegs, typename std::conditional<PRO >= 3, RowRegsE<E>, RowRegs>::type>::type;
     Regs rr;
     bool early = false;
     if constexpr (PRO == 1) {
         early = row_fits1(a.pro, blockDim.x);
         if (early) row_load1(a.pro, 0, rr);
-    } else if constexpr (PRO == 3) {
-        early = true;  // the host launches PRO 3 only where row_fits4 holds
-        row_load4(a.pro, rr);
+    } else if constexpr (PRO >= 3) {
+        early = true;  // the host launches PRO 3 / 4 only where K % 64 == 0 and K / E <= threads
+        row_loadE<E>(a.pro, rr);
     } else if constexpr (PRO == 2) {
         early = attn_fits1(a.pro, blockDim.x);
         if (early) attn_load1(a.pro, rr);
@@ -262,7 +263,7 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024) gemv_ksplit
         const QxRow qrow{lq, 4, 1};
         if (!early) sx_pro = row_quantize<1>(a.pro, 0, qrow, nullptr, nullptr, sm);
         else if constexpr (PRO == 1) sx_pro = row_finish1(a.pro, rr, qrow, nullptr, nullptr, sm);
-        else if constexpr (PRO == 3) sx_pro = row_finish4(a.pro, rr, lq, sm);
+        else if constexpr (PRO >= 3) sx_pro = row_finishE<E>(a.pro, rr, lq, sm);
         else {
             float v[4];
             attn_combine1(a.pro, rr, v);
@@ -334,10 +335,15 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
         if (a.pro.mode == kAttnNorm) {
             lds += (size_t)(a.pro.K / a.pro.attn_hd) * (a.pro.attn_S + 1) * sizeof(float);
             hipLaunchKernelGGL((gemv_ksplit_kernel<1, 2>), grid, dim3((unsigned)(64 * nw)), lds, s, a);
-        } else if (a.pro.K % 64 == 0 && a.pro.K / 4 <= (int)block.x && aligned16(a.pro.x) && aligned16(a.pro.aux) &&
-                 aligned16(a.pro.aux2))
+        } else if (a.pro.K % 64 == 0 && aligned16(a.pro.x) && aligned16(a.pro.aux) && aligned16(a.pro.aux2) &&
+                   a.pro.K / 4 <= (int)block.x) {
             hipLaunchKernelGGL((gemv_ksplit_kernel<1, 3>), grid, block, lds, s, a);
-        else hipLaunchKernelGGL((gemv_ksplit_kernel<1, 1>), grid, block, lds, s, a);
+        } else if (a.pro.K % 64 == 0 && aligned16(a.pro.x) && aligned16(a.pro.aux) && aligned16(a.pro.aux2) &&
+                   a.pro.K / 8 <= (int)block.x) {
+            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 4>), grid, block, lds, s, a);
+        } else {
+            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 1>), grid, block, lds, s, a);
+        }
     } else if (shape.ksplit) {
         const dim3 grid((unsigned)a.total_rb, mblocks);
         const size_t lds = (size_t)shape.nw * mt * kRowBlock * sizeof(int);

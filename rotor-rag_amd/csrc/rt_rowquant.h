@@ -288,80 +288,84 @@ __device__ __forceinline__ bool row_fits1(const QuantProb& P, int T) {
     return P.mode != kAttnNorm && (P.Kp >> 4) <= T;
 }
 
-// Four consecutive elements per thread (K % 64 == 0, K / 4 <= threads): thread t owns
-// elements k = 4 t .. 4 t + 3, read with one 16-byte load per operand.  In the permuted
-// layout element k = 16 g + e of group g sits at byte 4 (e % 4) + e / 4, so the thread's
-// four int8 values go to bytes 4 b + t % 4 (b = 0..3) of group t / 4: scatter_q4 writes
-// them to the LDS row one byte each.  Four elements per thread instead of sixteen spread
-// the row's arithmetic over four times as many waves.
+// E (4 or 8) consecutive elements per thread (K % 64 == 0, K / E <= threads): thread t
+// owns elements k = E t .. E t + E - 1, read with E / 4 16-byte loads per operand.  In the
+// permuted layout element k = 16 g + e of group g sits at byte 4 (e % 4) + e / 4, and
+// scatter_q writes the thread's int8 values to the LDS row one byte each.  Few elements
+// per thread spread the row's arithmetic over many waves.
 typedef float v4f_a8 __attribute__((ext_vector_type(4), aligned(8)));
 typedef float v2f_a8 __attribute__((ext_vector_type(2), aligned(8)));
 
-__device__ __forceinline__ void scatter_q4(const float (&v)[4], float sc, v4u* lq) {
-    const int t = threadIdx.x;
-    unsigned char* lb = reinterpret_cast<unsigned char*>(lq) + 16 * (t >> 2) + (t & 3);
+template <int E>
+__device__ __forceinline__ void scatter_q(const float (&v)[E], float sc, v4u* lq) {
+    unsigned char* lb = reinterpret_cast<unsigned char*>(lq);
+    const int k0 = E * (int)threadIdx.x;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        float q = rintf(v[b] / sc);
+    for (int j = 0; j < E; ++j) {
+        const int k = k0 + j, e = k & 15;
+        float q = rintf(v[j] / sc);
         q = fminf(fmaxf(q, -128.0f), 127.0f);
-        lb[4 * b] = (unsigned char)(int)q;
+        lb[(k & ~15) + 4 * (e & 3) + (e >> 2)] = (unsigned char)(int)q;
     }
 }
 
-struct RowRegs4 {
-    float v[4], u[4], w[4];
+template <int E>
+struct RowRegsE {
+    float v[E], u[E], w[E];
     bool live;  // wave-uniform: some lane of this wave owns elements
 };
 
-__device__ __forceinline__ bool row_fits4(const QuantProb& P, int T) {
-    return P.mode != kAttnNorm && (P.K & 63) == 0 && P.K / 4 <= T;
-}
-
-__device__ __forceinline__ void load4(const float* p, float (&v)[4]) {
-    const v4f_a8 t = *reinterpret_cast<const v4f_a8*>(p);
+template <int E>
+__device__ __forceinline__ void loadE(const float* p, float (&v)[E]) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v[j] = t[j];
-}
-
-__device__ __forceinline__ void row_load4(const QuantProb& P, RowRegs4& r) {
-    const int t = threadIdx.x, K = P.K;
-    r.live = __builtin_amdgcn_readfirstlane(threadIdx.x & ~63) < K / 4;
+    for (int i = 0; i < E / 4; ++i) {
+        const v4f_a8 t = *reinterpret_cast<const v4f_a8*>(p + 4 * i);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r.v[j] = r.u[j] = r.w[j] = 0.0f;
-    if (t < K / 4) {
-        load4(P.x + 4 * t, r.v);
-        if (has_relu2(P)) load4(P.aux + 4 * t, r.u);
-        if (has_norm(P)) load4(norm_weight(P) + 4 * t, r.w);
+        for (int j = 0; j < 4; ++j) v[4 * i + j] = t[j];
     }
 }
 
-__device__ __forceinline__ float row_finish4(const QuantProb& P, RowRegs4& r, v4u* lq, RowSmem* sm) {
+template <int E>
+__device__ __forceinline__ void row_loadE(const QuantProb& P, RowRegsE<E>& r) {
+    const int t = threadIdx.x, K = P.K;
+    r.live = __builtin_amdgcn_readfirstlane(threadIdx.x & ~63) < K / E;
+#pragma unroll
+    for (int j = 0; j < E; ++j) r.v[j] = r.u[j] = r.w[j] = 0.0f;
+    if (t < K / E) {
+        loadE<E>(P.x + E * t, r.v);
+        if (has_relu2(P)) loadE<E>(P.aux + E * t, r.u);
+        if (has_norm(P)) loadE<E>(norm_weight(P) + E * t, r.w);
+    }
+}
+
+template <int E>
+__device__ __forceinline__ float row_finishE(const QuantProb& P, RowRegsE<E>& r, v4u* lq, RowSmem* sm) {
     auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
     auto dadd_op = [](double x, double y) { return x + y; };
     const int t = threadIdx.x, K = P.K;
-    const bool mine = t < K / 4;
-    float (&v)[4] = r.v;
+    const bool mine = t < K / E;
+    float (&v)[E] = r.v;
     if (mine && has_relu2(P)) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = v[j] > 0.0f ? (v[j] * v[j]) * r.u[j] : 0.0f;
+        for (int j = 0; j < E; ++j) v[j] = v[j] > 0.0f ? (v[j] * v[j]) * r.u[j] : 0.0f;
     }
     if (has_norm(P)) {
         double ss = 0.0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ss += (double)v[j] * (double)v[j];
+        for (int j = 0; j < E; ++j) ss += (double)v[j] * (double)v[j];
         ss = block_reduce(ss, sm->d, dadd_op, r.live);
         const float norm = sqrtf((float)(ss / (double)K) + P.eps);
         if (mine) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] = (v[j] / norm) * r.w[j];
+            for (int j = 0; j < E; ++j) v[j] = (v[j] / norm) * r.w[j];
         }
     }
     float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    for (int j = 0; j < E; ++j) amax = fmaxf(amax, fabsf(v[j]));
     amax = block_reduce(amax, sm->f, fmax_op, r.live);
     const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
-    if (mine) scatter_q4(v, sc, lq);
+    if (mine) scatter_q<E>(v, sc, lq);
     return sc;
 }
 
@@ -404,7 +408,7 @@ __device__ __forceinline__ void attn_load1(const QuantProb& P, AttnRegs& r) {
         r.m[s] = mz[0];
         r.z[s] = mz[1];
     }
-    load4(P.aux + k0, r.w);
+    loadE<4>(P.aux + k0, r.w);
 }
 
 // The combine (attn_combine1, ends the AttnRegs' lifetime) and the RMSNorm +
@@ -454,7 +458,7 @@ __device__ __forceinline__ float attn_norm1(const QuantProb& P, float (&v)[4], c
     }
     amax = block_reduce(amax, sm->f, fmax_op, live);
     const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
-    if (mine) scatter_q4(v, sc, lq);
+    if (mine) scatter_q<4>(v, sc, lq);
     return sc;
 }
 

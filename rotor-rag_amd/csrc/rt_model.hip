@@ -11,6 +11,8 @@
 //
 // Floating-point contraction is off in this file so that a*b+c rounds twice, as the
 // NumPy model of the tests computes it.
+#include <algorithm>
+
 #include "rt_rowquant.h"
 
 #pragma clang fp contract(off)
@@ -267,9 +269,25 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
                                                       int rows_per_wave, float* __restrict__ logits,
                                                       unsigned long long* __restrict__ best) {
     constexpr int D = SLICES * 512;
+    constexpr int RB = 4;  // rows per batch: a batch's RB * SLICES loads go out together
     __shared__ double redd[4];
     __shared__ float xs[D];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int r0 = (blockIdx.x * 4 + wave) * rows_per_wave;
+    const int r1 = min(r0 + rows_per_wave, V);  // this wave's rows [r0, r1)
+    // Two batches alternate (A, B): the next batch's loads are in flight during the current
+    // one's arithmetic, and the first batch is issued before the RMSNorm below.
+    v4u wa[RB][SLICES], wb[RB][SLICES];
+    auto load_batch = [&](v4u (&w)[RB][SLICES], int rb) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i) {
+            const int r = min(rb + i, V - 1);  // rows past V re-read the last row (discarded)
+            const v4u* row = reinterpret_cast<const v4u*>(E + (size_t)r * D);
+#pragma unroll
+            for (int sl = 0; sl < SLICES; ++sl) w[i][sl] = __builtin_nontemporal_load(row + sl * 64 + lane);
+        }
+    };
+    if (r0 < r1) load_batch(wa, r0);
     // RMSNorm of x over D (every workgroup recomputes it, each element once, into LDS)
     float xv[D / 256], wv[D / 256];
 #pragma unroll
@@ -290,32 +308,21 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
     __syncthreads();
     float xn[SLICES][8];
 #pragma unroll
-    for (int s = 0; s < SLICES; ++s)
+    for (int sl = 0; sl < SLICES; ++sl)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xn[s][e] = xs[s * 512 + lane * 8 + e];
-    // rows in batches of RB: the batch's RB * SLICES loads go out together, then the math
-    constexpr int RB = 4;
-    const int r0 = (blockIdx.x * 4 + wave) * rows_per_wave;
+        for (int e = 0; e < 8; ++e) xn[sl][e] = xs[sl * 512 + lane * 8 + e];
     unsigned long long key = 0ull;
-    for (int rb = r0; rb < r0 + rows_per_wave && rb < V; rb += RB) {
-        v4u w[RB][SLICES];
-#pragma unroll
-        for (int i = 0; i < RB; ++i) {
-            const int r = min(rb + i, V - 1);  // rows past V re-read the last row (discarded)
-            const v4u* row = reinterpret_cast<const v4u*>(E + (size_t)r * D);
-#pragma unroll
-            for (int s = 0; s < SLICES; ++s) w[i][s] = __builtin_nontemporal_load(row + s * 64 + lane);
-        }
+    auto batch_math = [&](const v4u (&w)[RB][SLICES], int rb) {
         float acc[RB];
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
             acc[i] = 0.0f;
 #pragma unroll
-            for (int s = 0; s < SLICES; ++s)
+            for (int sl = 0; sl < SLICES; ++sl)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    acc[i] += __uint_as_float(w[i][s][e] << 16) * xn[s][2 * e];
-                    acc[i] += __uint_as_float(w[i][s][e] & 0xFFFF0000u) * xn[s][2 * e + 1];
+                    acc[i] += __uint_as_float(w[i][sl][e] << 16) * xn[sl][2 * e];
+                    acc[i] += __uint_as_float(w[i][sl][e] & 0xFFFF0000u) * xn[sl][2 * e + 1];
                 }
         }
 #pragma unroll
@@ -326,13 +333,20 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
 #pragma unroll
             for (int i = 0; i < RB; ++i) {
                 const int r = rb + i;
-                if (r < r0 + rows_per_wave && r < V) {
+                if (r < r1) {
                     logits[r] = acc[i];
                     const unsigned long long kk = argmax_key(acc[i], (unsigned)r);
                     key = kk > key ? kk : key;
                 }
             }
         }
+    };
+    for (int rb = r0; rb < r1; rb += 2 * RB) {
+        if (rb + RB < r1) load_batch(wb, rb + RB);
+        batch_math(wa, rb);
+        if (rb + RB >= r1) break;
+        if (rb + 2 * RB < r1) load_batch(wa, rb + 2 * RB);
+        batch_math(wb, rb + RB);
     }
     if (lane == 0 && key) atomicMax(best, key);
 }
@@ -394,20 +408,43 @@ hipError_t launch_attn_combine(const float* work, int H, int hd, int S, float* o
     return hipGetLastError();
 }
 
+// One round of workgroups: as many as the device holds at once (occupancy x CUs, taken
+// once per device), each wave a run of consecutive rows (a multiple of the two batches).
+template <int SLICES>
+static hipError_t run_lm_head(const uint16_t* E, const float* x, const float* norm_w, float eps, int V, float* logits,
+                              unsigned long long* best, hipStream_t s) {
+    static int slots[64] = {0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (slots[dev] == 0) {
+        int per_cu = 0, cus = 0;
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&lm_head_kernel<SLICES>),
+                                                         256, 0);
+        if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        slots[dev] = std::max(1, per_cu * cus);
+    }
+    int rpw = (V + 4 * slots[dev] - 1) / (4 * slots[dev]);
+    rpw = (rpw + 7) / 8 * 8;
+    const unsigned blocks = (unsigned)((V + 4 * rpw - 1) / (4 * rpw));
+    hipLaunchKernelGGL(lm_head_kernel<SLICES>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best);
+    return hipGetLastError();
+}
+
 hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w, float eps, int V, int D,
                           float* logits, unsigned long long* best, int* token, int* pos, int advance,
                           int* next_ids, int* out_tokens, int pos_base, int out_cap, hipStream_t s) {
-    const int rpw = 32;
-    const unsigned blocks = (unsigned)((V + 4 * rpw - 1) / (4 * rpw));
+    hipError_t e = hipSuccess;
     switch (D / 512) {
-        case 1: hipLaunchKernelGGL(lm_head_kernel<1>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;
-        case 2: hipLaunchKernelGGL(lm_head_kernel<2>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;
-        case 4: hipLaunchKernelGGL(lm_head_kernel<4>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;
-        case 5: hipLaunchKernelGGL(lm_head_kernel<5>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;
-        case 8: hipLaunchKernelGGL(lm_head_kernel<8>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best); break;
+        case 1: e = run_lm_head<1>(E, x, norm_w, eps, V, logits, best, s); break;
+        case 2: e = run_lm_head<2>(E, x, norm_w, eps, V, logits, best, s); break;
+        case 4: e = run_lm_head<4>(E, x, norm_w, eps, V, logits, best, s); break;
+        case 5: e = run_lm_head<5>(E, x, norm_w, eps, V, logits, best, s); break;
+        case 8: e = run_lm_head<8>(E, x, norm_w, eps, V, logits, best, s); break;
         default: return hipErrorInvalidValue;
     }
-    hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(1), 0, s, best, token, pos, advance, next_ids,
                        out_tokens, pos_base, out_cap);

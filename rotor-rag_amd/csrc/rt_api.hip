@@ -104,7 +104,9 @@ struct rt_plan {
     std::vector<GemvProb> probs;
     std::vector<QuantProb> quant;
     std::vector<GemmArgs> gemms;     // M > kGemvMaxM: one MFMA GEMM launch per problem
-    GemmArgs* dev_gemms = nullptr;   // 8 < M <= 64: the problems of one grouped launch [G]
+    GemmArgs* dev_gemms = nullptr;   // M > 8: the problems of one grouped launch [G]
+    int* dev_tile2p = nullptr;       // M > 64: problem of every tile of that launch
+    int gemm_cfg = 0, gemm_tiles = 0;  // M > 64: tile shape, tiles over all problems
     std::vector<const rt_act*> acts; // plans over caller-quantised activations
     bool fused = false;              // M = 1, input quantised in the GEMV prologue
     QuantProb pro{};
@@ -413,6 +415,7 @@ int rt_plan_free(rt_plan* plan) {
     if (plan->dev_probs) (void)hipFree(plan->dev_probs);
     if (plan->dev_rb2p) (void)hipFree(plan->dev_rb2p);
     if (plan->dev_gemms) (void)hipFree(plan->dev_gemms);
+    if (plan->dev_tile2p) (void)hipFree(plan->dev_tile2p);
     if (plan->dev_quant) (void)hipFree(plan->dev_quant);
     if (plan->act) (void)hipFree(plan->act);
     delete plan;
@@ -420,12 +423,36 @@ int rt_plan_free(rt_plan* plan) {
 }
 
 // 8 < M <= 64: one split-K launch serves all problems (row blocks numbered as in probs)
+// M > 8: one launch serves all problems.  M <= 64: the split-K kernel, one unit per row
+// block (numbered as in probs).  M > 64: the tile kernel, the tiles of problem g after
+// those of problems 0..g-1, with a tile -> problem table.
 static hipError_t upload_gemm_group(rt_plan* p) {
-    if (p->gemms.empty() || gemm_bm(p->M) != 64) return hipSuccess;
+    if (p->gemms.empty()) return hipSuccess;
     std::vector<GemmArgs> g = p->gemms;
-    for (size_t i = 0; i < g.size(); ++i) g[i].wg_begin = p->probs[i].wg_begin;
+    std::vector<int> tile2p;
+    if (gemm_bm(p->M) == 64) {
+        for (size_t i = 0; i < g.size(); ++i) g[i].wg_begin = p->probs[i].wg_begin;
+    } else {
+        std::vector<int> Ns(g.size());
+        for (size_t i = 0; i < g.size(); ++i) Ns[i] = g[i].N;
+        p->gemm_cfg = gemm_tile_cfg(p->M, Ns.data(), (int)g.size());
+        long long total = 0;
+        for (size_t i = 0; i < g.size(); ++i) {
+            g[i].wg_begin = (int)total;
+            const long long n = gemm_tile_count(p->gemm_cfg, p->M, g[i].N);
+            tile2p.insert(tile2p.end(), (size_t)n, (int)i);
+            total += n;
+        }
+        if (total <= 0 || total > (1 << 30)) return hipErrorInvalidValue;
+        p->gemm_tiles = (int)total;
+    }
     hipError_t e = hipMalloc(&p->dev_gemms, sizeof(GemmArgs) * g.size());
     if (e == hipSuccess) e = hipMemcpy(p->dev_gemms, g.data(), sizeof(GemmArgs) * g.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess && !tile2p.empty()) {
+        e = hipMalloc(&p->dev_tile2p, sizeof(int) * tile2p.size());
+        if (e == hipSuccess)
+            e = hipMemcpy(p->dev_tile2p, tile2p.data(), sizeof(int) * tile2p.size(), hipMemcpyHostToDevice);
+    }
     return e;
 }
 
@@ -598,12 +625,12 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
     a.M = plan->M;
     a.out_i32 = 0;
     a.total_rb = plan->total_rb;
-    if (plan->dev_gemms) {
-        RT_HIP(launch_gemm_group(plan->dev_gemms, plan->dev_rb2p, plan->total_rb, ctx->stream));
+    if (plan->dev_tile2p) {
+        RT_HIP(launch_gemm_tiles(plan->dev_gemms, plan->dev_tile2p, plan->gemm_tiles, plan->gemm_cfg, ctx->stream));
         return RT_OK;
     }
-    if (!plan->gemms.empty()) {
-        for (const GemmArgs& ga : plan->gemms) RT_HIP(launch_gemm(ga, ctx->stream));
+    if (plan->dev_gemms) {
+        RT_HIP(launch_gemm_group(plan->dev_gemms, plan->dev_rb2p, plan->total_rb, ctx->stream));
         return RT_OK;
     }
     RT_HIP(launch_gemv(a, plan->mt, plan->shape, ctx->stream));

@@ -143,8 +143,28 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[FI][FJ], const Gemm
     }
 }
 
+// One problem, or a group of them (dev != nullptr): unit b (a row block of the split-K
+// kernel, a tile of the tile kernel) serves problem rb2p[b], whose units start at its
+// wg_begin.
+struct GemmGroupArgs {
+    const GemmArgs* dev;
+    const int* rb2p;
+    GemmArgs one;
+};
+
+// Problem of unit b, read through constant-address-space pointers so that it stays
+// in scalar registers (see the GEMV's find_prob).
+typedef __attribute__((address_space(4))) const GemmArgs cgemm;
+typedef __attribute__((address_space(4))) const int cidx_g;
+__device__ __forceinline__ GemmArgs find_gemm(const GemmGroupArgs& ga, int b) {
+    if (!ga.dev) return ga.one;
+    const cgemm* q = (cgemm*)ga.dev + ((cidx_g*)ga.rb2p)[b];
+    return GemmArgs{q->w, q->qx, q->sx, q->rs, q->out, q->s_w, q->M, q->N, q->Np, q->C, q->ldo, q->out_i32, q->res,
+                    q->wg_begin};
+}
+
 template <int BM, int BN, int WAVES_M, int STAGES>
-__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
+__global__ void __launch_bounds__(256) gemm_kernel(GemmGroupArgs ga) {
     using T = GemmTile<BM, BN, WAVES_M, STAGES>;
     constexpr int FI = T::FI, FJ = T::FJ, LA = T::LA;
     extern __shared__ __attribute__((aligned(16))) v4u lds[];
@@ -152,13 +172,16 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs a) {
     const int t = threadIdx.x, lane = t & 63, g = lane >> 5, r32 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int wm = wave / T::WAVES_N, wn = wave % T::WAVES_N;
-    const int C = a.C, Nb = a.Np / kRowBlock;
 
-    // tile of this workgroup: m-major order, contiguous ranges per XCD
-    const int nT = (a.N + BN - 1) / BN, tiles = (int)gridDim.x;
+    // tile of this workgroup: the tiles of all problems in one order (each problem's
+    // m-major), dealt to the XCDs in contiguous ranges; then its problem and local tile
+    const int tiles = (int)gridDim.x;
     const int L = blockIdx.x, xcd = L % kXcds, base = tiles / kXcds, rem = tiles % kXcds;
     const int tile = xcd * base + min(xcd, rem) + L / kXcds;
-    const int m0 = (tile / nT) * BM, n0 = (tile % nT) * BN;
+    const GemmArgs a = find_gemm(ga, tile);
+    const int C = a.C, Nb = a.Np / kRowBlock;
+    const int nT = (a.N + BN - 1) / BN, lt = tile - a.wg_begin;
+    const int m0 = (lt / nT) * BM, n0 = (lt % nT) * BN;
     char* const lds_b = reinterpret_cast<char*>(lds);
     float* const sx_lds = reinterpret_cast<float*>(lds_b + T::SX_OFF);
 
@@ -311,24 +334,6 @@ __device__ __forceinline__ void wait_vm() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// one problem, or a group of them (dev != nullptr: workgroup b serves problem rb2p[b])
-struct GemmGroupArgs {
-    const GemmArgs* dev;
-    const int* rb2p;
-    GemmArgs one;
-};
-
-// Problem of workgroup b, read through constant-address-space pointers so that it stays
-// in scalar registers (see the GEMV's find_prob).
-typedef __attribute__((address_space(4))) const GemmArgs cgemm;
-typedef __attribute__((address_space(4))) const int cidx_g;
-__device__ __forceinline__ GemmArgs find_gemm(const GemmGroupArgs& ga, int b) {
-    if (!ga.dev) return ga.one;
-    const cgemm* q = (cgemm*)ga.dev + ((cidx_g*)ga.rb2p)[b];
-    return GemmArgs{q->w, q->qx, q->sx, q->rs, q->out, q->s_w, q->M, q->N, q->Np, q->C, q->ldo, q->out_i32, q->res,
-                    q->wg_begin};
-}
-
 template <int NW, int S>
 __global__ void __launch_bounds__(NW * 64) gemm_splitk_kernel(GemmGroupArgs ga) {
     constexpr int STAGE = 4 * 1024 + 1024, LOADS = 5;  // A: 4 blocks of 16 rows; W: 1 chunk
@@ -455,7 +460,7 @@ hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, int total_rb,
 }
 
 template <int BM, int BN, int WAVES_M, int STAGES>
-static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
+static hipError_t launch_tile(const GemmGroupArgs& ga, int tiles, hipStream_t s) {
     using T = GemmTile<BM, BN, WAVES_M, STAGES>;
     if (T::LDS_BYTES > 65536) {
         static const hipError_t attr =
@@ -463,9 +468,40 @@ static hipError_t launch_tile(const GemmArgs& a, hipStream_t s) {
                                 hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
         if (attr != hipSuccess) return attr;
     }
-    const long long tiles = (long long)((a.N + BN - 1) / BN) * ((a.M + BM - 1) / BM);
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WAVES_M, STAGES>), dim3((unsigned)tiles), dim3(256), T::LDS_BYTES, s, a);
+    if (tiles <= 0) return hipSuccess;
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WAVES_M, STAGES>), dim3((unsigned)tiles), dim3(256), T::LDS_BYTES, s, ga);
     return hipGetLastError();
+}
+
+static hipError_t launch_tile_cfg(int cfg, const GemmGroupArgs& ga, int tiles, hipStream_t s) {
+    switch (cfg) {
+        case kTile128x128: return launch_tile<128, 128, 2, 4>(ga, tiles, s);
+        case kTile256x128: return launch_tile<256, 128, 2, 4>(ga, tiles, s);
+        case kTile256x256: return launch_tile<256, 256, 2, 4>(ga, tiles, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+int gemm_tile_cfg(int M, const int* N, int G) {
+    if (gemm_bm(M) == 128) return kTile128x128;
+    const long long mt = (M + 255) / 256;
+    long long t256 = 0, t128 = 0;
+    for (int g = 0; g < G; ++g) {
+        t256 += mt * ((N[g] + 255) / 256);
+        t128 += mt * ((N[g] + 127) / 128);
+    }
+    if (t256 >= kGemmFillTiles) return kTile256x256;
+    if (t128 >= kGemmHalfTiles) return kTile256x128;
+    return kTile128x128;
+}
+
+long long gemm_tile_count(int cfg, int M, int N) {
+    const int bm = gemm_tile_bm(cfg), bn = gemm_tile_bn(cfg);
+    return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+}
+
+hipError_t launch_gemm_tiles(const GemmArgs* dev, const int* tile2p, int total_tiles, int cfg, hipStream_t s) {
+    return launch_tile_cfg(cfg, GemmGroupArgs{dev, tile2p, GemmArgs{}}, total_tiles, s);
 }
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
@@ -479,10 +515,10 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
         one.wg_begin = 0;
         return launch_splitk<8, 4>(GemmGroupArgs{nullptr, nullptr, one}, a.Np / kRowBlock, s);
     }
-    if (bm == 128) return launch_tile<128, 128, 2, 4>(a, s);
-    const long long wide = (long long)((a.N + 255) / 256) * ((a.M + 255) / 256);
-    if (wide >= 192) return launch_tile<256, 256, 2, 4>(a, s);
-    return launch_tile<256, 128, 2, 4>(a, s);
+    const int cfg = gemm_tile_cfg(a.M, &a.N, 1);
+    GemmArgs one = a;
+    one.wg_begin = 0;
+    return launch_tile_cfg(cfg, GemmGroupArgs{nullptr, nullptr, one}, (int)gemm_tile_count(cfg, a.M, a.N), s);
 }
 
 }  // namespace rt

@@ -143,6 +143,20 @@ hipError_t launch_unpermute(const int8_t* qx, int M, int K, int Kp, bool blocked
 // mt = tokens per workgroup (1, 2, 4 or 8).
 hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s);
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
+// Tile shapes of the MFMA GEMM for M > 64 (rows x columns per workgroup).  A launch over
+// one or several problems (same M) takes 256 x 256 when that yields kGemmFillTiles tiles,
+// else 256 x 128 when that yields kGemmHalfTiles (measured: 2048 x 2560 x 6912 runs 50 us
+// as 160 tiles of 256 x 128, 57 us as 320 of 128 x 128), else 128 x 128: a few large
+// tiles leave most CUs idle.
+enum GemmTileCfg { kTile128x128 = 0, kTile256x128 = 1, kTile256x256 = 2 };
+constexpr int kGemmFillTiles = 192, kGemmHalfTiles = 128;
+inline int gemm_tile_bm(int cfg) { return cfg == kTile128x128 ? 128 : 256; }
+inline int gemm_tile_bn(int cfg) { return cfg == kTile256x256 ? 256 : 128; }
+int gemm_tile_cfg(int M, const int* N, int G);
+long long gemm_tile_count(int cfg, int M, int N);
+// G problems with M > 64 in one tile launch: dev [G] (wg_begin = first tile of the
+// problem), tile2p [total_tiles] problem of every tile, cfg from gemm_tile_cfg.
+hipError_t launch_gemm_tiles(const GemmArgs* dev, const int* tile2p, int total_tiles, int cfg, hipStream_t s);
 // M <= 64 (gemm_bm(M) == 64): G problems in one launch over all their row blocks;
 // dev [G] (wg_begin set), rb2p [total_rb] problem of every global row block.
 hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, int total_rb, hipStream_t s);

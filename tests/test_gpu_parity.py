@@ -144,9 +144,11 @@ def test_ternary_matmul_duck_type(hip):
     assert y.shape == (300,)
 
 
-@pytest.mark.parametrize("M", [1, 16, 37, 64, 130])
+@pytest.mark.parametrize("M", [1, 16, 37, 64, 130, 300, 600])
 def test_plan_matches_single_calls(hip, M):
-    """A plan launches its problems together (one grid over all row blocks for M <= 64)."""
+    """A plan launches its problems together: one grid over all row blocks for M <= 64, one
+    grid over all tiles above (M = 300: 128 x 128 tiles, M = 600: 256 x 128, while the
+    single calls pick their own shapes)."""
     import torch
 
     rng = np.random.default_rng(12 + M)

@@ -117,6 +117,154 @@ __global__ void __launch_bounds__(256) attention_kernel(const float* __restrict_
     }
 }
 
+// Prefill attention on the fp32 matrix cores (v_mfma_f32_32x32x2_f32, twice the VALU FMA
+// rate).  Workgroup (kv head kh, query block) owns 32 rows r = i G + g (query i of the
+// block, q-head g of the G = H / Hkv heads sharing kh); lane l of every wave works on row
+// l % 32.  Its 4 waves take the visible keys in blocks of 32, wave w blocks w, w + 4, ..,
+// each block staged in the wave's own LDS slice (K dimension-major as in the cache, V
+// key-major), with an online softmax per wave:
+//   S^T = K Q^T   (A = K[key][d] from LDS, B = Q^T from registers; the 128 dims are
+//                  taken in 64 steps pairing d = s and d = 64 + s over the lane halves)
+//   P^T = e^(S^T scale - m) per row, rows are lanes, so max and sum need one
+//                  lane-half exchange
+//   O^T += V^T P^T (A = V^T from LDS, B = P^T straight from the S^T registers: the
+//                  MFMA output layout puts keys 8 (r / 4) + 4 (l / 32) + r % 4 of the
+//                  lane's row in register r, and step r pairs exactly those keys)
+// The 4 waves' (m, l, O) are merged through LDS at the end.  fp32 products, fp32 sums in
+// the matrix cores' order.
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+template <int HD>
+__global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __restrict__ q,
+                                                                const float* __restrict__ Kc,
+                                                                const float* __restrict__ Vc, float* __restrict__ out,
+                                                                int M, int H, int Hkv, int Lmax,
+                                                                const int* __restrict__ pos_p, float scale) {
+    static_assert(HD == 128, "two 64-dim halves per lane");
+    constexpr int BK = 32, SLICE = HD * BK * 2;  // floats per wave: K [HD][BK], V [BK][HD]
+    extern __shared__ __attribute__((aligned(16))) float lds_pf[];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, row = lane & 31, hl = lane >> 5;
+    const int G = H / Hkv, BQ = 32 / G;
+    const int kh = blockIdx.x, i0 = blockIdx.y * BQ;
+    const int pos0 = *pos_p;
+    const int m = i0 + row / G, hq = kh * G + row % G;
+    const int lastpos = m < M ? pos0 + m : -1;     // keys <= lastpos visible to this row
+    const int kend = pos0 + min(i0 + BQ, M);       // keys [0, kend) visible to some row
+    const int nblk = (kend + BK - 1) / BK;
+    float* Ks = lds_pf + wave * SLICE;
+    float* Vs = Ks + HD * BK;
+    // this lane's half of its row of Q: dims 64 hl .. 64 hl + 63
+    float qr[64];
+    {
+        const float* qp = q + (size_t)min(m, M - 1) * H * HD + (size_t)hq * HD + 64 * hl;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float4 v4 = *reinterpret_cast<const float4*>(qp + 4 * i);
+            qr[4 * i] = v4.x;
+            qr[4 * i + 1] = v4.y;
+            qr[4 * i + 2] = v4.z;
+            qr[4 * i + 3] = v4.w;
+        }
+    }
+    v16f o[HD / 32];
+#pragma unroll
+    for (int nb = 0; nb < HD / 32; ++nb) o[nb] = v16f{};
+    float mrow = -INFINITY, lrow = 0.0f;
+    const float* K = Kc + (size_t)kh * HD * Lmax;
+    const float* V = Vc + (size_t)kh * Lmax * HD;
+    for (int b = wave; b < nblk; b += 4) {
+        const int key0 = b * BK;
+        // stage the block (keys past Lmax read as zeros; keys past kend are masked below)
+#pragma unroll
+        for (int it = 0; it < HD * BK / 4 / 64; ++it) {
+            const int idx = it * 64 + lane, d = idx / (BK / 4), jq = 4 * (idx % (BK / 4));
+            float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (key0 + jq + 3 < Lmax) v4 = *reinterpret_cast<const float4*>(K + (size_t)d * Lmax + key0 + jq);
+            *reinterpret_cast<float4*>(Ks + d * BK + jq) = v4;
+        }
+#pragma unroll
+        for (int it = 0; it < HD * BK / 4 / 64; ++it) {
+            const int idx = it * 64 + lane, j = idx / (HD / 4), dq = 4 * (idx % (HD / 4));
+            float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (key0 + j < Lmax) v4 = *reinterpret_cast<const float4*>(V + (size_t)(key0 + j) * HD + dq);
+            *reinterpret_cast<float4*>(Vs + j * HD + dq) = v4;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave reads back its own slice
+        // S^T[key][row]
+        v16f sacc = v16f{};
+#pragma unroll
+        for (int st = 0; st < 64; ++st)
+            sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(64 * hl + st) * BK + row], qr[st], sacc, 0, 0, 0);
+        float pr[16];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = key0 + 8 * (r >> 2) + 4 * hl + (r & 3);
+            pr[r] = key <= lastpos ? sacc[r] * scale : -INFINITY;
+            mx = fmaxf(mx, pr[r]);
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(mrow, mx);
+        const float alpha = mnew == -INFINITY ? 1.0f : expf(mrow - mnew);
+        float ls = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            pr[r] = pr[r] == -INFINITY ? 0.0f : expf(pr[r] - mnew);
+            ls += pr[r];
+        }
+        ls += __shfl_xor(ls, 32, 64);
+        lrow = lrow * alpha + ls;
+        mrow = mnew;
+        // O^T[dim][row] = alpha O^T + V^T P^T
+#pragma unroll
+        for (int nb = 0; nb < HD / 32; ++nb) {
+            v16f acc = o[nb] * alpha;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[(8 * (r >> 2) + 4 * hl + (r & 3)) * HD + 32 * nb + row],
+                                                           pr[r], acc, 0, 0, 0);
+            o[nb] = acc;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is refilled
+    }
+    // merge the waves: slice w becomes [32 rows][HD] of O^T, then (m, l) per row
+    __syncthreads();
+    float* Om = lds_pf + wave * SLICE;
+    float* ml = lds_pf + 4 * SLICE;  // [4 waves][32 rows][2]
+#pragma unroll
+    for (int nb = 0; nb < HD / 32; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) Om[row * HD + 32 * nb + 8 * (r >> 2) + 4 * hl + (r & 3)] = o[nb][r];
+    if (hl == 0) {
+        ml[(wave * 32 + row) * 2] = mrow;
+        ml[(wave * 32 + row) * 2 + 1] = lrow;
+    }
+    __syncthreads();
+    const int orow = t >> 3, d0 = (t & 7) * (HD / 8);
+    const int om = i0 + orow / G, oh = kh * G + orow % G;
+    if (om >= M) return;
+    float mw[4], fw[4], mmax = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        mw[w] = ml[(w * 32 + orow) * 2];
+        mmax = fmaxf(mmax, mw[w]);
+    }
+    float den = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        fw[w] = mw[w] == -INFINITY ? 0.0f : expf(mw[w] - mmax);
+        den += fw[w] * ml[(w * 32 + orow) * 2 + 1];
+    }
+    float* dst = out + (size_t)om * H * HD + (size_t)oh * HD + d0;
+#pragma unroll
+    for (int e = 0; e < HD / 8; ++e) {
+        float num = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) num += fw[w] * lds_pf[w * SLICE + orow * HD + d0 + e];
+        dst[e] = num / den;
+    }
+}
+
 // Decode attention, split over the keys: workgroup (h, s) handles keys
 // [64 s, 64 s + 64) of query head h for the single query at *pos_p and writes a partial
 // result to work[h][s][0..HD+2): the unnormalised output sum_j e^(s_j - m) V_j (HD
@@ -382,6 +530,18 @@ hipError_t launch_rope_append(float* q, float* k, const float* v, float* Kc, flo
 
 hipError_t launch_attention(const float* q, const float* Kc, const float* Vc, float* out, int M, int H, int Hkv,
                             int hd, int Lmax, const int* pos, float scale, hipStream_t s) {
+    const int G = H / Hkv;
+    if (hd == 128 && G <= 32 && 32 % G == 0 && Lmax % 4 == 0) {  // matrix-core kernel
+        constexpr size_t lds = (size_t)(4 * 128 * 32 * 2 + 4 * 32 * 2) * sizeof(float);
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(&attn_prefill_mfma_kernel<128>), hipFuncAttributeMaxDynamicSharedMemorySize,
+            (int)lds);
+        if (attr != hipSuccess) return attr;
+        const int BQ = 32 / G;
+        hipLaunchKernelGGL((attn_prefill_mfma_kernel<128>), dim3((unsigned)Hkv, (unsigned)((M + BQ - 1) / BQ)),
+                           dim3(256), lds, s, q, Kc, Vc, out, M, H, Hkv, Lmax, pos, scale);
+        return hipGetLastError();
+    }
     const size_t lds = (size_t)(hd + Lmax + 256) * sizeof(float);
     hipLaunchKernelGGL(attention_kernel, dim3((unsigned)H, (unsigned)M), dim3(256), lds, s, q, Kc, Vc, out, H, Hkv,
                        hd, Lmax, pos, scale);

@@ -41,11 +41,12 @@ def test_embed_exact(hip):
     assert np.array_equal(h.cpu().numpy(), O.bf16_to_f32(E)[ids])
 
 
-# (M, pos0, H, Hkv, hd, Lmax): the tiled prefill kernel (64 (query, head) rows per
-# workgroup, 64-key blocks: several query and key blocks, ragged last blocks, G = H / Hkv
-# of 1, 2, 4) and the general kernel (G = 3 does not divide 64)
+# (M, pos0, H, Hkv, hd, Lmax): hd = 128 runs the matrix-core kernel (32 (query, head) rows
+# per workgroup, 32-key blocks over 4 waves: several query and key blocks, ragged last
+# blocks, G = H / Hkv of 1, 4, 8, Lmax not a multiple of 32); the rest the general kernel
 ATTN_CASES = [(1, 0, 20, 5, 128, 64), (1, 37, 20, 5, 128, 64), (7, 3, 8, 2, 64, 64), (16, 0, 4, 4, 64, 64),
-              (100, 50, 20, 5, 128, 256), (70, 0, 8, 4, 64, 128), (130, 5, 4, 4, 64, 192), (33, 20, 6, 2, 64, 64)]
+              (100, 50, 20, 5, 128, 256), (70, 0, 8, 4, 64, 128), (130, 5, 4, 4, 64, 192), (33, 20, 6, 2, 64, 64),
+              (40, 10, 8, 8, 128, 128), (50, 0, 16, 2, 128, 68), (200, 300, 20, 5, 128, 520)]
 
 
 @pytest.mark.parametrize("M,pos0,H,Hkv,hd,Lmax", ATTN_CASES)

@@ -115,6 +115,7 @@ struct rt_plan {
     // (run_shape); 0 a quantiser launch, then the GEMV
     int run_pro = 0;
     GemvShape run_shape{};
+    int quant_maxK = 0;  // > 0: every quant problem takes the vectorised row kernel (largest K)
 };
 
 struct rt_act {
@@ -298,7 +299,7 @@ static int stage_activations(rt_ctx* ctx, const float* x, const int8_t* q_in, in
     a.Mpad = Mpad;
     a.p = QuantProb{x, q_in, *qx, *sx, q_nat, K, Kp, q_in ? kPermute : kQuant, nullptr, 0.0f, nullptr, nullptr, 0, 0,
                     blocked};
-    RT_HIP(launch_quant(a, ctx->stream));
+    RT_HIP(launch_quant(a, ctx->stream, quant_rows_ok(a.p) ? K : 0));
     if (s_out) RT_HIP(hipMemcpyAsync(s_out, *sx, (size_t)M * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
     return RT_OK;
 }
@@ -517,6 +518,14 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
                                 reinterpret_cast<float*>(base + soff[u]), nullptr, Ku[u], round_up(Ku[u], kChunk),
                                 kQuant, nullptr, 0.0f, nullptr, nullptr, 0, 0, qx_blocked(M)};
     }
+    p->quant_maxK = 0;
+    for (const QuantProb& qp : p->quant) {
+        if (!quant_rows_ok(qp)) {
+            p->quant_maxK = 0;
+            break;
+        }
+        p->quant_maxK = std::max(p->quant_maxK, qp.K);
+    }
     int wg = 0, minC = 1 << 30;
     p->probs.resize(G);
     for (int g = 0; g < G; ++g) {
@@ -583,7 +592,7 @@ int rt_plan_quantize(rt_ctx* ctx, const rt_plan* plan) {
     q.U = plan->U;
     q.M = plan->M;
     q.Mpad = plan->Mpad;
-    RT_HIP(launch_quant(q, ctx->stream));
+    RT_HIP(launch_quant(q, ctx->stream, plan->quant_maxK));
     return RT_OK;
 }
 
@@ -684,7 +693,7 @@ static int act_fill(rt_ctx* ctx, rt_act* act, int M, int mode, const float* x, c
     q.Mpad = act_rows(M);
     q.p = QuantProb{x, nullptr, act->qx, act->sx, nullptr, act->K, act->Kp, mode, aux, eps, v_out, aux2, 0, 0,
                     qx_blocked(M)};
-    RT_HIP(launch_quant(q, ctx->stream));
+    RT_HIP(launch_quant(q, ctx->stream, quant_rows_ok(q.p) ? act->K : 0));
     act->M = M;
     act->Mpad = q.Mpad;
     return RT_OK;

@@ -137,7 +137,10 @@ inline int gemm_bm(int M) { return M <= 64 ? 64 : M <= 128 ? 128 : 256; }
 // Launchers (return hipSuccess or the launch error).
 hipError_t launch_relayout(const uint8_t* src, int N, int K, v4u* tiles, hipStream_t s);
 hipError_t launch_unrelayout(const v4u* tiles, int N, int K, uint8_t* dst, hipStream_t s);
-hipError_t launch_quant(const QuantArgs& a, hipStream_t s);
+// maxK > 0: every problem passes quant_rows_ok and maxK is their largest K (the
+// vectorised row kernel); 0: the general kernel.
+hipError_t launch_quant(const QuantArgs& a, hipStream_t s, int maxK = 0);
+bool quant_rows_ok(const QuantProb& P);
 // qx rows [M][Kp] (permuted) -> natural-order int8 [M][K]
 hipError_t launch_unpermute(const int8_t* qx, int M, int K, int Kp, bool blocked, int8_t* q, hipStream_t s);
 // mt = tokens per workgroup (1, 2, 4 or 8).

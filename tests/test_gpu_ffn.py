@@ -49,6 +49,27 @@ def test_act_rmsnorm_quantize_bit_exact(hip, M, K):
     assert np.abs(_np(h) - O.rms_norm(x, w, 1e-6)).max() <= 4 * np.spacing(np.abs(ho).max())
 
 
+@pytest.mark.parametrize("M,K", [(1, 2560), (9, 2560), (300, 6912), (2, 4160), (3, 8192), (2, 8256)])
+def test_act_quantize_without_value_outputs(hip, M, K):
+    """Without the fp32 value outputs the quantiser takes its vectorised row kernel (K % 64
+    == 0, K <= 8192, 4 or 8 elements per thread); q and s stay bit-exact."""
+    import torch
+
+    rng = np.random.default_rng(11 * K + M)
+    x = rng.standard_normal((M, K), dtype=np.float32) * rng.uniform(0.1, 10, (M, 1)).astype(np.float32)
+    u = rng.standard_normal((M, K), dtype=np.float32)
+    w = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    act = hip.activations(M, K)
+    hip.act_rmsnorm_quantize(torch.from_numpy(x), torch.from_numpy(w), act, 1e-6)
+    q, s = act.export()
+    qo, so = O.quant_rows(O.rms_norm_f64acc(x, w, 1e-6))
+    assert np.array_equal(_np(s), so) and np.array_equal(_np(q), qo)
+    hip.act_relu2_mul_quantize(torch.from_numpy(x), torch.from_numpy(u), act)
+    q, s = act.export()
+    qo, so = O.quant_rows(O.relu2_gate(x, u))
+    assert np.array_equal(_np(s), so) and np.array_equal(_np(q), qo)
+
+
 @pytest.mark.parametrize("M,K", [(1, 6912), (4, 6912), (64, 6912), (2, 33)])
 def test_act_relu2_mul_quantize_bit_exact(hip, M, K):
     import torch

@@ -145,7 +145,9 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
     extern __shared__ __attribute__((aligned(16))) float lds_pf[];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, row = lane & 31, hl = lane >> 5;
     const int G = H / Hkv, BQ = 32 / G;
-    const int kh = blockIdx.x, i0 = blockIdx.y * BQ;
+    // the last query blocks see the most keys: they go out first, so that the short ones
+    // fill in behind them when the grid takes more than one round of workgroups
+    const int kh = blockIdx.x, i0 = ((int)gridDim.y - 1 - (int)blockIdx.y) * BQ;
     const int pos0 = *pos_p;
     const int m = i0 + row / G, hq = kh * G + row % G;
     const int lastpos = m < M ? pos0 + m : -1;     // keys <= lastpos visible to this row
@@ -172,29 +174,55 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
     float mrow = -INFINITY, lrow = 0.0f;
     const float* K = Kc + (size_t)kh * HD * Lmax;
     const float* V = Vc + (size_t)kh * Lmax * HD;
-    for (int b = wave; b < nblk; b += 4) {
-        const int key0 = b * BK;
-        // stage the block (keys past Lmax read as zeros; keys past kend are masked below)
+    // Staging through registers, one buffer in use at a time: this block's V loads are in
+    // flight during its S^T MFMAs, the next block's K loads during its PV MFMAs.  Keys
+    // past Lmax read as zeros; keys past kend are masked below.
+    float4 stg[HD * BK / 4 / 64];
+    auto load_k = [&](int key0) {
 #pragma unroll
         for (int it = 0; it < HD * BK / 4 / 64; ++it) {
             const int idx = it * 64 + lane, d = idx / (BK / 4), jq = 4 * (idx % (BK / 4));
-            float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (key0 + jq + 3 < Lmax) v4 = *reinterpret_cast<const float4*>(K + (size_t)d * Lmax + key0 + jq);
-            *reinterpret_cast<float4*>(Ks + d * BK + jq) = v4;
+            stg[it] = key0 + jq + 3 < Lmax ? *reinterpret_cast<const float4*>(K + (size_t)d * Lmax + key0 + jq)
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+    };
+    auto store_k = [&]() {
+#pragma unroll
+        for (int it = 0; it < HD * BK / 4 / 64; ++it) {
+            const int idx = it * 64 + lane, d = idx / (BK / 4), jq = 4 * (idx % (BK / 4));
+            *reinterpret_cast<float4*>(Ks + d * BK + jq) = stg[it];
+        }
+    };
+    auto load_v = [&](int key0) {
 #pragma unroll
         for (int it = 0; it < HD * BK / 4 / 64; ++it) {
             const int idx = it * 64 + lane, j = idx / (HD / 4), dq = 4 * (idx % (HD / 4));
-            float4 v4 = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (key0 + j < Lmax) v4 = *reinterpret_cast<const float4*>(V + (size_t)(key0 + j) * HD + dq);
-            *reinterpret_cast<float4*>(Vs + j * HD + dq) = v4;
+            stg[it] = key0 + j < Lmax ? *reinterpret_cast<const float4*>(V + (size_t)(key0 + j) * HD + dq)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+    };
+    auto store_v = [&]() {
+#pragma unroll
+        for (int it = 0; it < HD * BK / 4 / 64; ++it) {
+            const int idx = it * 64 + lane, j = idx / (HD / 4), dq = 4 * (idx % (HD / 4));
+            *reinterpret_cast<float4*>(Vs + j * HD + dq) = stg[it];
+        }
+    };
+    if (wave < nblk) load_k(wave * BK);
+    for (int b = wave; b < nblk; b += 4) {
+        const int key0 = b * BK;
+        store_k();
+        load_v(key0);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave reads back its own slice
-        // S^T[key][row]
+        // S^T[key][row]; the 64 A operands are read from LDS ahead of the MFMA chain (read
+        // one by one in front of each MFMA, every pair of MFMAs would wait for the LDS)
+        float ka[64];
+#pragma unroll
+        for (int st = 0; st < 64; ++st) ka[st] = Ks[(64 * hl + st) * BK + row];
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the chain
         v16f sacc = v16f{};
 #pragma unroll
-        for (int st = 0; st < 64; ++st)
-            sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[(64 * hl + st) * BK + row], qr[st], sacc, 0, 0, 0);
+        for (int st = 0; st < 64; ++st) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[st], qr[st], sacc, 0, 0, 0);
         float pr[16];
         float mx = -INFINITY;
 #pragma unroll
@@ -215,14 +243,21 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
         ls += __shfl_xor(ls, 32, 64);
         lrow = lrow * alpha + ls;
         mrow = mnew;
-        // O^T[dim][row] = alpha O^T + V^T P^T
+        store_v();
+        if (b + 4 < nblk) load_k((b + 4) * BK);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // O^T[dim][row] = alpha O^T + V^T P^T (A operands read ahead, as above)
+        float va[HD / 32][16];
+#pragma unroll
+        for (int nb = 0; nb < HD / 32; ++nb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) va[nb][r] = Vs[(8 * (r >> 2) + 4 * hl + (r & 3)) * HD + 32 * nb + row];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int nb = 0; nb < HD / 32; ++nb) {
             v16f acc = o[nb] * alpha;
 #pragma unroll
-            for (int r = 0; r < 16; ++r)
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(Vs[(8 * (r >> 2) + 4 * hl + (r & 3)) * HD + 32 * nb + row],
-                                                           pr[r], acc, 0, 0, 0);
+            for (int r = 0; r < 16; ++r) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(va[nb][r], pr[r], acc, 0, 0, 0);
             o[nb] = acc;
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is refilled

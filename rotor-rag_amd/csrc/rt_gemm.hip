@@ -478,6 +478,7 @@ static hipError_t launch_tile_cfg(int cfg, const GemmGroupArgs& ga, int tiles, h
         case kTile128x128: return launch_tile<128, 128, 2, 4>(ga, tiles, s);
         case kTile256x128: return launch_tile<256, 128, 2, 4>(ga, tiles, s);
         case kTile256x256: return launch_tile<256, 256, 2, 4>(ga, tiles, s);
+        case kTile64x128: return launch_tile<64, 128, 1, 4>(ga, tiles, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -492,7 +493,7 @@ int gemm_tile_cfg(int M, const int* N, int G) {
     }
     if (t256 >= kGemmFillTiles) return kTile256x256;
     if (t128 >= kGemmHalfTiles) return kTile256x128;
-    return kTile128x128;
+    return 2 * t128 >= kGemmHalfTiles ? kTile128x128 : kTile64x128;
 }
 
 long long gemm_tile_count(int cfg, int M, int N) {

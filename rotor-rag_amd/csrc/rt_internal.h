@@ -149,11 +149,12 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 // Tile shapes of the MFMA GEMM for M > 64 (rows x columns per workgroup).  A launch over
 // one or several problems (same M) takes 256 x 256 when that yields kGemmFillTiles tiles,
 // else 256 x 128 when that yields kGemmHalfTiles (measured: 2048 x 2560 x 6912 runs 50 us
-// as 160 tiles of 256 x 128, 57 us as 320 of 128 x 128), else 128 x 128: a few large
-// tiles leave most CUs idle.
-enum GemmTileCfg { kTile128x128 = 0, kTile256x128 = 1, kTile256x256 = 2 };
+// as 160 tiles of 256 x 128, 57 us as 320 of 128 x 128), else 128 x 128 when that does,
+// else 64 x 128 (measured on the 512-token prefill's projections: 4.95 ms against 5.30 ms
+// with 128 x 128): a few large tiles leave most CUs idle.
+enum GemmTileCfg { kTile128x128 = 0, kTile256x128 = 1, kTile256x256 = 2, kTile64x128 = 3 };
 constexpr int kGemmFillTiles = 192, kGemmHalfTiles = 128;
-inline int gemm_tile_bm(int cfg) { return cfg == kTile128x128 ? 128 : 256; }
+inline int gemm_tile_bm(int cfg) { return cfg == kTile64x128 ? 64 : cfg == kTile128x128 ? 128 : 256; }
 inline int gemm_tile_bn(int cfg) { return cfg == kTile256x256 ? 256 : 128; }
 int gemm_tile_cfg(int M, const int* N, int G);
 long long gemm_tile_count(int cfg, int M, int N);

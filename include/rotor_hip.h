@@ -85,7 +85,7 @@ int rt_ctx_set_stream(rt_ctx* ctx, void* hip_stream);
 int rt_sync(rt_ctx* ctx);
 
 /* Upload a ternary matrix given as rotor bytes [N][ceil(K/4)] in HOST memory and
- * re-lay it on the device in the GEMV/GEMM tile layout.  scale = the per-tensor
+ * re-lay it on the device in the GEMV/GEMM tile layout (N <= 2^26, K <= 2^22).  scale = the per-tensor
  * weight scale (src/rotor/bitnet_model.py:182-185).  Replaces
  * GPUTernaryOps.pack_ternary_weights (src/rotor/gpu_ternary.py:112-136) and the
  * per-call weight upload of ternary_matmul (:160-164): weights stay resident. */
@@ -94,7 +94,8 @@ int rt_weights_upload(rt_ctx* ctx, const uint8_t* rotor_host, int N, int K, floa
 /* Same, from rotor bytes already in DEVICE memory (row-major [N][ceil(K/4)]). */
 int rt_weights_upload_device(rt_ctx* ctx, const uint8_t* rotor_dev, int N, int K, float scale, rt_weights** out);
 
-/* Copy the matrix back as host rotor bytes [N][ceil(K/4)] (exact inverse of upload). */
+/* Copy the matrix back as host rotor bytes [N][ceil(K/4)]: the inverse of upload, except
+ * that the reserved code 11 (which decodes to 0) comes back as the canonical 00. */
 int rt_weights_download(rt_ctx* ctx, const rt_weights* w, uint8_t* rotor_host);
 
 int rt_weights_info(const rt_weights* w, int* N, int* K, float* scale);

@@ -188,8 +188,10 @@ int rt_sync(rt_ctx* ctx) {
 static int weights_alloc(rt_ctx* ctx, int N, int K, float scale, rt_weights** out) {
     if (!ctx || !out) return fail(RT_EINVAL, "rt_weights_upload: ctx/out is NULL");
     if (N <= 0 || K <= 0) return fail(RT_EINVAL, "rt_weights_upload: N and K must be positive");
-    if ((long long)K > (1LL << 24) || (long long)N > (1LL << 26))
-        return fail(RT_EINVAL, "rt_weights_upload: N or K too large");
+    // K <= 2^22 keeps the GEMV's int32 partial sums (4 g x over half the row, device code
+    // g in 0..2, |x| <= 128) in range
+    if ((long long)K > (1LL << 22) || (long long)N > (1LL << 26))
+        return fail(RT_EINVAL, "rt_weights_upload: N or K too large (N <= 2^26, K <= 2^22)");
     rt_weights* w = new rt_weights();
     w->device = ctx->device;
     w->N = N;

@@ -16,7 +16,8 @@
 //     contiguous 16-byte lanes.  The MFMA lane l wants
 //     row l % 32, bytes 32 h + 16 (l / 32) .. +15 of slice h: one ds_read_b128, every
 //     group of 8 lanes reading 128 contiguous bytes (conflict-free).
-//   * W stays 2-bit in LDS (a 64-row block's chunk is 1 KiB, copied as is).  The 16
+//   * W stays 2-bit in LDS (a 64-row block's chunk is 1 KiB, copied as is; device code
+//     g = w + 1, rt_internal.h).  The 16
 //     weights an MFMA lane needs are one dword of its row's 16-byte unit: ds_read_b32
 //     and four v_perm_b32 expand it to int8 in the qx order.
 //   * Software pipeline per step c: MFMAs of slice 0; barrier; loads of step
@@ -42,10 +43,10 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr unsigned kLut = 0x0001FF00u;  // v_perm_b32 src1: field 0,1,2,3 -> 00, FF, 01, 00
+constexpr unsigned kLut = 0x000100FFu;  // v_perm_b32 src1: device code 0,1,2,(3) -> FF, 00, 01, 00
 constexpr int kXcds = 8;
 
-// one dword of rotor code (16 weights, byte b holds elements 4b..4b+3 at bits 2i) -> 16
+// one dword of device code (16 weights, byte b holds elements 4b..4b+3 at bits 2i) -> 16
 // int8 weights in the qx order of a 16-group: output byte 4i + b = element 4b + i
 __device__ __forceinline__ v4i decode_dword(unsigned u) {
     v4i o;

@@ -16,17 +16,16 @@
 //   * KSPLIT (few row blocks, e.g. one 6912x2560 GEMV): a workgroup is one row block
 //     and its nw waves split the K chunks, combined through LDS.
 //
-// Decoding the rotor code (value = bit0 - bit1, field f = 2*bit0 + bit1) costs
-// 9 VALU ops per 16 weights: for a weight dword u
-//     t0 = u & 0x03030303          -> fields of element 0 of each byte (values 0..3)
-//     t1 = u & 0x0C0C0C0C          -> fields of element 1 (values 0,4,8,12)
-//     h  = u >> 4, t2 = h & 0x03030303, t3 = h & 0x0C0C0C0C
-// and one v_perm_b32 per t turns the four selector bytes into four int8 weights.
-// v_perm_b32 byte select: 0..3 pick src1 bytes, 4..7 src0 bytes, 8 replicates bit 7
-// of src1 byte 1, 12 gives 0x00.  With src1 = 0x0001FF00 and src0 = 0x00000001:
-//     t0: sel 0,1,2,3  -> 00, FF, 01, 00  =  w  for f = 00, 01, 10, 11
-//     t1: sel 0,4,8,12 -> 00, 01, FF, 00  = -w  for f = 00, 01, 10, 11
-// so element positions 0/2 accumulate into accP and 1/3 into accN, acc = accP - accN.
+// Decoding costs 5 VALU ops per 16 weights.  The tiles hold the device code g = w + 1
+// (rt_internal.h), and a 2-bit field masked in place is a non-negative int8 multiple
+// of g.  For a weight dword u (four bytes of four fields each) and h = u >> 4:
+//     u & 0x03030303, h & 0x03030303   -> g of elements 0 and 2 of each byte
+//     u & 0x0C0C0C0C, h & 0x0C0C0C0C   -> 4 g of elements 1 and 3
+// so v_dot4_i32_i8 against the matching activation dwords accumulates sum g x into
+// accP and 4 sum g x into accQ, and, with g = w + 1,
+//     sum w x = accP + accQ / 4 - sum x.
+// sum x over the same k range (padding activations are 0) is the same for every lane:
+// each wave computes it once from the activation row (slice_sums).
 #include <algorithm>
 #include <type_traits>
 
@@ -37,8 +36,6 @@
 
 namespace rt {
 
-constexpr unsigned kLutLo = 0x0001FF00u;  // src1 of v_perm_b32
-constexpr unsigned kLutHi = 0x00000001u;  // src0 of v_perm_b32
 constexpr int kAuxNT = 2;                 // cache policy: non-temporal (streamed once)
 
 // The activations are read-only for the whole launch, so the constant address space
@@ -74,16 +71,16 @@ __device__ __forceinline__ QuantProb own_source(const GemvProb& P) {
 
 template <int MT, typename XP>
 __device__ __forceinline__ void chunk_step(const v4u v, XP* __restrict__ xc, const int ldx,
-                                           int (&accP)[MT], int (&accN)[MT]) {
+                                           int (&accP)[MT], int (&accQ)[MT]) {
     int d[16];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const unsigned u = v[j];
         const unsigned h = u >> 4;
-        d[4 * j + 0] = (int)__builtin_amdgcn_perm(kLutHi, kLutLo, u & 0x03030303u);
-        d[4 * j + 1] = (int)__builtin_amdgcn_perm(kLutHi, kLutLo, u & 0x0C0C0C0Cu);
-        d[4 * j + 2] = (int)__builtin_amdgcn_perm(kLutHi, kLutLo, h & 0x03030303u);
-        d[4 * j + 3] = (int)__builtin_amdgcn_perm(kLutHi, kLutLo, h & 0x0C0C0C0Cu);
+        d[4 * j + 0] = (int)(u & 0x03030303u);
+        d[4 * j + 1] = (int)(u & 0x0C0C0C0Cu);
+        d[4 * j + 2] = (int)(h & 0x03030303u);
+        d[4 * j + 3] = (int)(h & 0x0C0C0C0Cu);
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -91,12 +88,62 @@ __device__ __forceinline__ void chunk_step(const v4u v, XP* __restrict__ xc, con
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             accP[m] = __builtin_amdgcn_sdot4(d[4 * j + 0], xm[4 * j + 0], accP[m], false);
-            accN[m] = __builtin_amdgcn_sdot4(d[4 * j + 1], xm[4 * j + 1], accN[m], false);
+            accQ[m] = __builtin_amdgcn_sdot4(d[4 * j + 1], xm[4 * j + 1], accQ[m], false);
             accP[m] = __builtin_amdgcn_sdot4(d[4 * j + 2], xm[4 * j + 2], accP[m], false);
-            accN[m] = __builtin_amdgcn_sdot4(d[4 * j + 3], xm[4 * j + 3], accN[m], false);
+            accQ[m] = __builtin_amdgcn_sdot4(d[4 * j + 3], xm[4 * j + 3], accQ[m], false);
         }
     }
 }
+
+// Sum of v over the 64 lanes of the wave, returned to every lane: row_shr 1/2/4/8 leave
+// each 16-lane row's total in its lane 15, row_bcast 15 and 31 carry those into lane 63.
+__device__ __forceinline__ int wave_sum(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// sum x over activation dwords [d0, d1) (multiples of 4) of each of the MT rows at xq
+// (row stride ldx dwords): lane l takes the 16-byte units d0 / 4 + l + 64 i, all loads
+// issued before the first v_dot4 (against 0x01010101), then the wave adds the lanes up.
+template <int MT, typename XP>
+__device__ __forceinline__ void slice_sums(XP* __restrict__ xq, const int ldx, const int d0, const int d1,
+                                           int (&sx)[MT]) {
+    constexpr int R = 4;  // units per lane per round: one round covers K <= 16384
+    const int lane = threadIdx.x & 63, u0 = d0 >> 2, u1 = d1 >> 2;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        XP* __restrict__ xm = xq + m * ldx;
+        int t = 0;
+        for (int u = u0 + lane; u < u1 + lane; u += 64 * R) {
+            v4u x[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int ur = u + 64 * r;
+                if (ur < u1) {
+                    x[r][0] = xm[4 * ur + 0];
+                    x[r][1] = xm[4 * ur + 1];
+                    x[r][2] = xm[4 * ur + 2];
+                    x[r][3] = xm[4 * ur + 3];
+                } else {
+                    x[r] = v4u{0u, 0u, 0u, 0u};
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) t = __builtin_amdgcn_sdot4((int)x[r][j], 0x01010101, t, false);
+        }
+        sx[m] = wave_sum(t);
+    }
+}
+
+// sum w x of one row from the two accumulators and the slice's sum x
+__device__ __forceinline__ int row_dot(int accP, int accQ, int sx) { return accP + (accQ >> 2) - sx; }
 
 // Accumulate chunks [cb, ce) of one row block.  `rsrc` starts at the row block and
 // ends at chunk ce (num_records = ce KiB).  The chunk offset goes into the VGPR offset,
@@ -125,16 +172,16 @@ __device__ __forceinline__ void gemv_preload(__amdgpu_buffer_rsrc_t rsrc, const 
 template <int MT, int U, typename XP>
 __device__ __forceinline__ void gemv_body(__amdgpu_buffer_rsrc_t rsrc, const int lane_off, XP* __restrict__ xq,
                                           const int ldx, const int cb, const int ce, int (&accP)[MT],
-                                          int (&accN)[MT], v4u (&A)[U], v4u (&B)[U]) {
+                                          int (&accQ)[MT], v4u (&A)[U], v4u (&B)[U]) {
     for (int c = cb; c < ce; c += 2 * U) {
 #pragma unroll
         for (int i = 0; i < U; ++i)
-            if (c + i < ce) chunk_step<MT, XP>(A[i], xq + (c + i) * 16, ldx, accP, accN);
+            if (c + i < ce) chunk_step<MT, XP>(A[i], xq + (c + i) * 16, ldx, accP, accQ);
 #pragma unroll
         for (int i = 0; i < U; ++i) A[i] = gemv_load<U>(rsrc, lane_off, c + 2 * U + i);
 #pragma unroll
         for (int i = 0; i < U; ++i)
-            if (c + U + i < ce) chunk_step<MT, XP>(B[i], xq + (c + U + i) * 16, ldx, accP, accN);
+            if (c + U + i < ce) chunk_step<MT, XP>(B[i], xq + (c + U + i) * 16, ldx, accP, accQ);
 #pragma unroll
         for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane_off, c + 3 * U + i);
     }
@@ -174,9 +221,9 @@ __global__ void __launch_bounds__(1024) gemv_rows_kernel(GemvArgs a) {
     const int C = P.C, ldx = C * 16;
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, C * 1024, kBufDword3);
-    int accP[MT], accN[MT];
+    int accP[MT], accQ[MT], sx[MT];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
+    for (int m = 0; m < MT; ++m) accP[m] = accQ[m] = 0;
     v4u A[U], B[U];
     if constexpr (PRO != 0) {
         static_assert(MT == 1, "the prologue quantises one token");
@@ -187,19 +234,23 @@ __global__ void __launch_bounds__(1024) gemv_rows_kernel(GemvArgs a) {
         gemv_preload<U>(rsrc, lane * 16, 0, A, B, false);
         RowSmem* sm = reinterpret_cast<RowSmem*>(lds_row + (Q.Kp >> 4));
         const QxRow qrow{lds_row, 4, 1};
-        const float sx = early ? row_finish1(Q, rr, qrow, nullptr, nullptr, sm)
-                               : row_quantize<1>(Q, 0, qrow, nullptr, nullptr, sm);
+        const float s_pro = early ? row_finish1(Q, rr, qrow, nullptr, nullptr, sm)
+                                  : row_quantize<1>(Q, 0, qrow, nullptr, nullptr, sm);
 #pragma unroll
         for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane * 16, U + i);
         __syncthreads();
-        gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lds_row, ldx, 0, C, accP, accN, A, B);
-        emit(a, P, rb, 0, 0, lane, accP[0] - accN[0], sx);
+        slice_sums<MT, lint>((lint*)lds_row, ldx, 0, ldx, sx);
+        gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lds_row, ldx, 0, C, accP, accQ, A, B);
+        emit(a, P, rb, 0, 0, lane, row_dot(accP[0], accQ[0], sx[0]), s_pro);
     } else {
         cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
+        // the activation loads for sum x go out before the weights, so waiting for them
+        // does not wait for the weight batches
+        slice_sums<MT, cint>(xq, ldx, 0, ldx, sx);
         gemv_preload<U>(rsrc, lane * 16, 0, A, B);
-        gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, 0, C, accP, accN, A, B);
+        gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, 0, C, accP, accQ, A, B);
 #pragma unroll
-        for (int m = 0; m < MT; ++m) emit(a, P, rb, m0, m, lane, accP[m] - accN[m]);
+        for (int m = 0; m < MT; ++m) emit(a, P, rb, m0, m, lane, row_dot(accP[m], accQ[m], sx[m]));
     }
 }
 
@@ -248,13 +299,17 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024) gemv_ksplit
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, ce * 1024, kBufDword3);
     v4u A[U], B[U];
+    int accP[MT], accQ[MT], sx[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) accP[m] = accQ[m] = 0;
+    // sum x of the wave's slice: without a prologue its activation loads go out before
+    // the weights (waiting for them then does not wait for the weight batches)
+    cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
+    if constexpr (PRO == 0) slice_sums<MT, cint>(xq, ldx, cb * 16, ce * 16, sx);
     // With a prologue only the first batch is in flight during it (register budget); the
     // attention prologue holds its partials in registers first and issues it after their
     // combine.
     if (PRO != 2 || !early) gemv_preload<U>(rsrc, lane * 16, cb, A, B, PRO == 0);
-    int accP[MT], accN[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) accP[m] = accN[m] = 0;
     float sx_pro = -1.0f;
     if constexpr (PRO != 0) {
         v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
@@ -274,13 +329,13 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024) gemv_ksplit
 #pragma unroll
         for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane * 16, cb + U + i);
         __syncthreads();
-        gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accN, A, B);
+        slice_sums<MT, lint>((lint*)lq, ldx, cb * 16, ce * 16, sx);
+        gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accQ, A, B);
     } else {
-        cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
-        gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, cb, ce, accP, accN, A, B);
+        gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, cb, ce, accP, accQ, A, B);
     }
 #pragma unroll
-    for (int m = 0; m < MT; ++m) red[(wave * MT + m) * kRowBlock + lane] = accP[m] - accN[m];
+    for (int m = 0; m < MT; ++m) red[(wave * MT + m) * kRowBlock + lane] = row_dot(accP[m], accQ[m], sx[m]);
     __syncthreads();
     for (int idx = threadIdx.x; idx < MT * kRowBlock; idx += blockDim.x) {
         const int m = idx / kRowBlock, r = idx % kRowBlock;

@@ -5,10 +5,15 @@
 //
 //  * Weight tiles.  Kp = K rounded up to 64, C = Kp/64 "chunks" of 64 weights
 //    (16 bytes) per row, Np = N rounded up to 64, Nb = Np/64 row blocks.  The
-//    16-byte unit (rb, c, r) holds rotor bytes [16c, 16c+16) of row 64*rb + r and
+//    16-byte unit (rb, c, r) holds bytes [16c, 16c+16) of row 64*rb + r and
 //    lives at unit index (rb*C + c)*64 + r.  A wave that owns row block rb and reads
 //    chunk c therefore issues one fully coalesced 1 KiB load (lane r <- row r), and
-//    the whole row block is one contiguous C KiB stream.  Padding codes are 00 (= 0).
+//    the whole row block is one contiguous C KiB stream.
+//    The element positions of the rotor bytes are kept (element j of a byte in bits
+//    2j+1..2j), the 2-bit code is not: the device stores g = w + 1 (00 = -1, 01 = 0,
+//    10 = +1), so that a field masked in place, read as an int8, is g or 4 g and one
+//    v_dot4 gives sum g x = sum w x + sum x; the GEMV subtracts sum x (see
+//    device_code).  Padding weights (k >= K, rows >= N) are 01 (= 0).
 //
 //  * Quantised activations "qx".  Per token, Kp int8 values; inside every group of
 //    16 consecutive k the bytes are stored in the order
@@ -37,6 +42,20 @@ constexpr int kChunk = 64;      // weights per 16-byte chunk
 constexpr size_t kTileSlack = 16384;
 
 inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
+
+// Rotor code (per 2-bit field: high bit = bit0, low bit = bit1, w = bit0 - bit1;
+// src/rotor/core.py:99-108) <-> device code g = w + 1, 16 fields per dword at once.
+// Rotor 00 -> 01, 10 -> 10, 01 -> 00 and the reserved 11 (w = 0) -> 01; back, 01 -> 00,
+// so a reserved 11 returns as the canonical 00.
+__host__ __device__ inline unsigned device_code(unsigned r) {
+    const unsigned b0 = (r >> 1) & 0x55555555u, b1 = r & 0x55555555u;
+    const unsigned hi = b0 & ~b1, lo = ~(b0 ^ b1) & 0x55555555u;
+    return (hi << 1) | lo;
+}
+__host__ __device__ inline unsigned rotor_code(unsigned g) {
+    const unsigned hi = (g >> 1) & 0x55555555u, lo = g & 0x55555555u;
+    return (hi << 1) | (~hi & ~lo & 0x55555555u);
+}
 
 // ---- one quantisation problem (-> qx, sx) -----------------------------------------
 // The value quantised for element k of a row depends on `mode`:

@@ -1,15 +1,16 @@
 // Weight relayout: rotor bytes [N][ceil(K/4)] <-> gfx950 weight tiles.
 //
-// The rotor byte code itself is kept unchanged on the device (element j of a byte
-// in bits (2j+1, 2j) = (bit0, bit1); src/rotor/core.py:99-108), only the placement
-// of 16-byte chunks changes (see rt_internal.h).  This replaces the reference's
-// per-weight Python packing loop (src/rotor/gpu_ternary.py:112-136) and its C
-// conversion loop (native/c/rotor_core.c:202-260): one thread per 16-byte unit.
+// Element j of a byte stays in bits (2j+1, 2j) (src/rotor/core.py:99-108); the 16-byte
+// chunks move to the tile placement and each 2-bit rotor code (bit0, bit1) becomes the
+// device code g = w + 1 (rt_internal.h: device_code / rotor_code).  This replaces the
+// reference's per-weight Python packing loop (src/rotor/gpu_ternary.py:112-136) and its
+// C conversion loop (native/c/rotor_core.c:202-260): one thread per 16-byte unit.
 #include "rt_internal.h"
 
 namespace rt {
 
-// Bytes of row n, byte columns [b0, b0+16), with codes of k >= K cleared to 00.
+// Bytes of row n, byte columns [b0, b0+16), in device code; codes of k >= K and rows
+// n >= N are weight 0.
 __device__ __forceinline__ v4u gather_row_bytes(const uint8_t* __restrict__ src, int N, int K, int n, int b0) {
     const int kb = (K + 3) >> 2;
     unsigned wd[4] = {0u, 0u, 0u, 0u};
@@ -27,7 +28,7 @@ __device__ __forceinline__ v4u gather_row_bytes(const uint8_t* __restrict__ src,
             wd[i >> 2] |= byte << (8 * (i & 3));
         }
     }
-    v4u v = {wd[0], wd[1], wd[2], wd[3]};
+    v4u v = {device_code(wd[0]), device_code(wd[1]), device_code(wd[2]), device_code(wd[3])};
     return v;
 }
 
@@ -50,7 +51,7 @@ __global__ void __launch_bounds__(256) unrelayout_kernel(const v4u* __restrict__
     const int n = (int)(i / kb), b = (int)(i % kb);
     const int rb = n / kRowBlock, r = n % kRowBlock, c = b / 16, j = b % 16;
     const v4u v = tiles[((size_t)rb * C + c) * kRowBlock + r];
-    const unsigned wd = v[j >> 2];
+    const unsigned wd = rotor_code(v[j >> 2]);
     dst[i] = (uint8_t)(wd >> (8 * (j & 3)));
 }
 

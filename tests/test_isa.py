@@ -7,6 +7,8 @@ can silently lose:
     compares that makes a per-lane buffer resource uniform, once per chunk);
   * no register spills (scratch) in the GEMV kernels (a spill of a value just loaded
     makes the wave wait for that load, serialising the prologue's loads);
+  * the GEMV expands weights with masks only and reads its activations for the dot
+    products with scalar loads;
   * the GEMM's main loop is free of scratch traffic and of waterfall loops.
 """
 import re
@@ -73,8 +75,23 @@ def test_gemv_kernels_scalar_descriptors_no_spills(gemv):
 
 def test_gemv_rows_reads_activations_with_scalar_loads(gemv):
     (n,) = [n for n in gemv if "gemv_rows_kernelILi1ELi0E" in n]
-    assert "s_load_dwordx16" in gemv[n] or "s_load_dwordx8" in gemv[n]
-    assert "global_load" not in gemv[n]
+    t = gemv[n]
+    assert "s_load_dwordx16" in t or "s_load_dwordx8" in t
+    # the only per-lane activation loads are the 16-byte ones of the sum-x pass (one
+    # round of 4 per token), issued before the weight loop
+    loads = re.findall(r"global_load\w*", t)
+    assert loads and set(loads) == {"global_load_dwordx4"} and len(loads) <= 4, loads
+    assert t.index("global_load_dwordx4") < t.index("buffer_load_dwordx4")
+
+
+def test_gemv_decodes_with_masks_only(gemv):
+    # device code g = w + 1: the chunk loop expands weights by shifts and masks (no
+    # v_perm lookup table) and reduces sum x with DPP adds
+    for n in [n for n in gemv if "gemv_rows_kernel" in n or "gemv_ksplit_kernel" in n]:
+        t = gemv[n]
+        assert "0x1ff00" not in t, n  # the lookup operand of the former v_perm decode
+        assert "0xc0c0c0c" in t and "0x3030303" in t, n
+        assert "row_bcast:31" in t, n
 
 
 def test_gemm_main_loop_clean(gemm):

@@ -95,18 +95,6 @@ __device__ __forceinline__ void chunk_step(const v4u v, XP* __restrict__ xc, con
     }
 }
 
-// Sum of v over the 64 lanes of the wave, returned to every lane: row_shr 1/2/4/8 leave
-// each 16-lane row's total in its lane 15, row_bcast 15 and 31 carry those into lane 63.
-__device__ __forceinline__ int wave_sum(int v) {
-    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
-    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
-    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
-    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
-    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
-    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
-    return __builtin_amdgcn_readlane(v, 63);
-}
-
 // sum x over activation dwords [d0, d1) (multiples of 4) of each of the MT rows at xq
 // (row stride ldx dwords): lane l takes the 16-byte units d0 / 4 + l + 64 i, all loads
 // issued before the first v_dot4 (against 0x01010101), then the wave adds the lanes up.

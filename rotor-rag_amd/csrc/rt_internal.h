@@ -142,6 +142,54 @@ struct GemmArgs {
 };
 
 constexpr int kBufDword3 = 0x00020000;  // buffer resource word 3 for gfx9 raw buffers
+
+// Wave64 reductions on the DPP network: row_shr 1, 2, 4, 8 leave each 16-lane row's
+// total in its lane 15, row_bcast 15 and 31 carry the row totals into lane 63, which
+// ends up holding op over all 64 lanes (the other lanes hold partial results).  A lane
+// whose DPP source does not exist takes `id`, op's identity.  Six dependent VALU steps,
+// where a butterfly of __shfl_xor is six LDS round trips.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ unsigned dpp_u32(unsigned v, unsigned id) {
+    return (unsigned)__builtin_amdgcn_update_dpp((int)id, (int)v, CTRL, ROWS, 0xf, false);
+}
+template <int CTRL, int ROWS, typename T>
+__device__ __forceinline__ T dpp_step(T v, T id) {
+    if constexpr (sizeof(T) == 8) {
+        const unsigned long long b = __builtin_bit_cast(unsigned long long, v),
+                                 i = __builtin_bit_cast(unsigned long long, id);
+        const unsigned lo = dpp_u32<CTRL, ROWS>((unsigned)b, (unsigned)i);
+        const unsigned hi = dpp_u32<CTRL, ROWS>((unsigned)(b >> 32), (unsigned)(i >> 32));
+        return __builtin_bit_cast(T, ((unsigned long long)hi << 32) | lo);
+    } else {
+        return __builtin_bit_cast(T, dpp_u32<CTRL, ROWS>(__builtin_bit_cast(unsigned, v),
+                                                         __builtin_bit_cast(unsigned, id)));
+    }
+}
+template <typename T, typename Op>
+__device__ __forceinline__ T wave_reduce63(T v, T id, Op op) {
+    v = op(v, dpp_step<0x111, 0xf>(v, id));  // row_shr:1
+    v = op(v, dpp_step<0x112, 0xf>(v, id));  // row_shr:2
+    v = op(v, dpp_step<0x114, 0xf>(v, id));  // row_shr:4
+    v = op(v, dpp_step<0x118, 0xf>(v, id));  // row_shr:8
+    v = op(v, dpp_step<0x142, 0xa>(v, id));  // row_bcast:15 into rows 1, 3
+    v = op(v, dpp_step<0x143, 0xc>(v, id));  // row_bcast:31 into rows 2, 3
+    return v;
+}
+// the lane-63 total, returned to every lane (through an SGPR)
+template <typename T>
+__device__ __forceinline__ T lane63(T v) {
+    if constexpr (sizeof(T) == 8) {
+        const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+        const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, 63);
+        const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), 63);
+        return __builtin_bit_cast(T, ((unsigned long long)hi << 32) | lo);
+    } else {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    }
+}
+__device__ __forceinline__ int wave_sum(int v) {
+    return lane63(wave_reduce63(v, 0, [](int a, int b) { return a + b; }));
+}
 constexpr int kGemvMaxM = 8;  // up to this many tokens: VALU GEMV; beyond: MFMA GEMM
 // qx layout.  Rows (M <= kGemvMaxM, read by the GEMV): row m at m * Kp.  Blocked
 // (M > kGemvMaxM, read by the MFMA GEMM): 16-row x 64-k blocks of 1 KiB, block

@@ -397,13 +397,11 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restri
     if (wave == 0) {
         float sc = lane < nk ? (((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane])) * scale)
                              : -INFINITY;
-        float mx = sc;
-        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        const float mx = lane63(wave_reduce63(sc, -INFINITY, [](float x, float y) { return fmaxf(x, y); }));
         const float p = lane < nk ? expf(sc - mx) : 0.0f;
-        float z = p;
-        for (int off = 32; off >= 1; off >>= 1) z += __shfl_xor(z, off, 64);
+        const float z = wave_reduce63(p, 0.0f, [](float x, float y) { return x + y; });
         pr[lane] = p;
-        if (lane == 0) {
+        if (lane == 63) {
             wp[HD] = mx;
             wp[HD + 1] = z;
         }
@@ -481,8 +479,8 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
     double ss = 0.0;
 #pragma unroll
     for (int i = 0; i < D / 256; ++i) ss += (double)xv[i] * (double)xv[i];
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    if (lane == 0) redd[wave] = ss;
+    ss = wave_reduce63(ss, 0.0, [](double x, double y) { return x + y; });
+    if (lane == 63) redd[wave] = ss;
     __syncthreads();
     ss = (redd[0] + redd[1]) + (redd[2] + redd[3]);
     const float norm = sqrtf((float)(ss / (double)D) + eps);
@@ -509,10 +507,8 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
                 }
         }
 #pragma unroll
-        for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-            for (int i = 0; i < RB; ++i) acc[i] += __shfl_xor(acc[i], off, 64);
-        if (lane == 0) {
+        for (int i = 0; i < RB; ++i) acc[i] = wave_reduce63(acc[i], 0.0f, [](float x, float y) { return x + y; });
+        if (lane == 63) {  // the lane holding the totals
 #pragma unroll
             for (int i = 0; i < RB; ++i) {
                 const int r = rb + i;
@@ -531,7 +527,7 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
         if (rb + 2 * RB < r1) load_batch(wa, rb + 2 * RB);
         batch_math(wb, rb + RB);
     }
-    if (lane == 0 && key) atomicMax(best, key);
+    if (lane == 63 && key) atomicMax(best, key);
 }
 
 // token = argmax; optionally also written to next_ids[0] (the next step's input) and,

@@ -28,17 +28,15 @@ struct RowSmem {   // reduction scratch in LDS (one slot per wave)
 
 // Workgroup reduction through one slot per wave.  Each slot array serves one reduction
 // per row_quantize call (sums in RowSmem::d, maxima in RowSmem::f), so no barrier is
-// needed before the slots are written.
+// needed before the slots are written.  Every use reduces values >= 0 (sums of squares,
+// maxima of |v|), so 0 is the identity of op.
 // `wave_live` (wave-uniform) false: the wave only contributes v (the identity) and
-// skips the shuffles.
+// skips the DPP steps.
 template <typename T, typename Op>
 __device__ __forceinline__ T block_reduce(T v, T* red, Op op, bool wave_live = true) {
-    if (wave_live) {
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
-    }
+    if (wave_live) v = wave_reduce63(v, T(0), op);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
-    if (lane == 0) red[wave] = v;
+    if (lane == 63) red[wave] = v;
     __syncthreads();
     T r = red[0];
     for (int w = 1; w < nw; ++w) r = op(r, red[w]);

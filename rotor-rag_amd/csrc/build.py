@@ -3,8 +3,8 @@
     python rotor-rag_amd/csrc/build.py          # or __graft_entry__.build()
 
 Every HIP translation unit is compiled for gfx950 only, with packed-FP32 code
-generation disabled (-Xclang -target-feature -Xclang -packed-fp32-ops), no
-fast-math (the quantiser relies on IEEE fp32 division), then linked into
+generation disabled (-Xclang -target-feature -Xclang -packed-fp32-ops), kernel-argument
+preloading on, no fast-math (the quantiser relies on IEEE fp32 division), then linked into
 rotor-rag_amd/rotor/lib/librotor_hip.so, next to the Python package that loads it.
 """
 from __future__ import annotations
@@ -24,9 +24,17 @@ SOURCES = ["rt_layout.hip", "rt_quant.hip", "rt_gemv.hip", "rt_gemm.hip", "rt_mo
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
+# Device code generation flags (also used by the code-generation tests):
+#   packed-fp32-ops off; kernel arguments preloaded into SGPRs at wave launch (up to 16
+#   dwords of leading scalar/pointer arguments; the code object keeps a fallback that
+#   loads them where the firmware does not preload).
+DEVICE_FLAGS = [
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
+]
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-command-line-argument",
-    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    *DEVICE_FLAGS,
 ]
 
 

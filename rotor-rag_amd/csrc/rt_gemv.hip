@@ -254,7 +254,19 @@ constexpr int kAttnMaxThreads = 640;
 // elements per thread (K % 64 == 0, K / 4 or K / 8 <= threads, 16-byte aligned sources);
 // 2 prologue combining decode-attention partials (kAttnNorm).
 template <int MT, int PRO>
-__global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024) gemv_ksplit_kernel(GemvArgs a) {
+__global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
+    gemv_ksplit_kernel(const float* pro_x, const float* pro_aux, const float* pro_aux2, int pro_K, int pro_mode,
+                       float pro_eps, GemvArgs a) {
+    // The prologue source's fields lead the argument list as scalars, so that the
+    // kernel-argument preload (-amdgpu-kernarg-preload-count) has them in SGPRs when the
+    // waves start: the row's loads then go out before any kernel-argument load returns.
+    QuantProb pro = a.pro;
+    pro.x = pro_x;
+    pro.aux = pro_aux;
+    pro.aux2 = pro_aux2;
+    pro.K = pro_K;
+    pro.mode = pro_mode;
+    pro.eps = pro_eps;
     constexpr int U = MT == 1 ? 4 : 2;
     extern __shared__ __attribute__((aligned(16))) int red[];
     const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
@@ -269,14 +281,14 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024) gemv_ksplit
     Regs rr;
     bool early = false;
     if constexpr (PRO == 1) {
-        early = row_fits1(a.pro, blockDim.x);
-        if (early) row_load1(a.pro, 0, rr);
+        early = row_fits1(pro, blockDim.x);
+        if (early) row_load1(pro, 0, rr);
     } else if constexpr (PRO >= 3) {
         early = true;  // the host launches PRO 3 / 4 only where K % 64 == 0 and K / E <= threads
-        row_loadE<E>(a.pro, rr);
+        row_loadE<E>(pro, rr);
     } else if constexpr (PRO == 2) {
-        early = attn_fits1(a.pro, blockDim.x);
-        if (early) attn_load1(a.pro, rr);
+        early = attn_fits1(pro, blockDim.x);
+        if (early) attn_load1(pro, rr);
     }
     const GemvProb P = find_prob(a, blockIdx.x);
     const int rb = blockIdx.x - P.wg_begin;
@@ -301,18 +313,18 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024) gemv_ksplit
     float sx_pro = -1.0f;
     if constexpr (PRO != 0) {
         v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
-        RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (a.pro.Kp >> 4));
+        RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (pro.Kp >> 4));
         sm->fac = (lfloat*)(sm + 1);  // kAttnNorm factors follow
         const QxRow qrow{lq, 4, 1};
-        if (!early) sx_pro = row_quantize<1>(a.pro, 0, qrow, nullptr, nullptr, sm);
-        else if constexpr (PRO == 1) sx_pro = row_finish1(a.pro, rr, qrow, nullptr, nullptr, sm);
-        else if constexpr (PRO >= 3) sx_pro = row_finishE<E>(a.pro, rr, lq, sm);
+        if (!early) sx_pro = row_quantize<1>(pro, 0, qrow, nullptr, nullptr, sm);
+        else if constexpr (PRO == 1) sx_pro = row_finish1(pro, rr, qrow, nullptr, nullptr, sm);
+        else if constexpr (PRO >= 3) sx_pro = row_finishE<E>(pro, rr, lq, sm);
         else {
             float v[4];
-            attn_combine1(a.pro, rr, v);
+            attn_combine1(pro, rr, v);
             const float w[4] = {rr.w[0], rr.w[1], rr.w[2], rr.w[3]};
             gemv_preload<U>(rsrc, lane * 16, cb, A, B, false);
-            sx_pro = attn_norm1(a.pro, v, w, rr.live, lq, sm);
+            sx_pro = attn_norm1(pro, v, w, rr.live, lq, sm);
         }
 #pragma unroll
         for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane * 16, cb + U + i);
@@ -373,28 +385,41 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
     } else if (a.has_pro) {  // single token, prologue-quantised input: KSPLIT shape only
         if (mt != 1 || a.M != 1 || !shape.ksplit) return hipErrorInvalidValue;
         const dim3 grid((unsigned)a.total_rb, 1);
+        const QuantProb& P = a.pro;
         const int nw = a.pro.mode == kAttnNorm ? std::min(shape.nw, kAttnMaxThreads / 64) : shape.nw;
         size_t lds = (size_t)nw * kRowBlock * sizeof(int) + (size_t)a.pro.Kp + sizeof(RowSmem);
         if (a.pro.mode == kAttnNorm) {
             lds += (size_t)(a.pro.K / a.pro.attn_hd) * (a.pro.attn_S + 1) * sizeof(float);
-            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 2>), grid, dim3((unsigned)(64 * nw)), lds, s, a);
+            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 2>), grid, dim3((unsigned)(64 * nw)), lds, s, P.x, P.aux, P.aux2,
+                               P.K, P.mode, P.eps, a);
         } else if (a.pro.K % 64 == 0 && aligned16(a.pro.x) && aligned16(a.pro.aux) && aligned16(a.pro.aux2) &&
                    a.pro.K / 4 <= (int)block.x) {
-            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 3>), grid, block, lds, s, a);
+            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 3>), grid, block, lds, s, P.x, P.aux, P.aux2, P.K, P.mode,
+                               P.eps, a);
         } else if (a.pro.K % 64 == 0 && aligned16(a.pro.x) && aligned16(a.pro.aux) && aligned16(a.pro.aux2) &&
                    a.pro.K / 8 <= (int)block.x) {
-            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 4>), grid, block, lds, s, a);
+            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 4>), grid, block, lds, s, P.x, P.aux, P.aux2, P.K, P.mode,
+                               P.eps, a);
         } else {
-            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 1>), grid, block, lds, s, a);
+            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 1>), grid, block, lds, s, P.x, P.aux, P.aux2, P.K, P.mode,
+                               P.eps, a);
         }
     } else if (shape.ksplit) {
         const dim3 grid((unsigned)a.total_rb, mblocks);
         const size_t lds = (size_t)shape.nw * mt * kRowBlock * sizeof(int);
         switch (mt) {
-            case 1: hipLaunchKernelGGL((gemv_ksplit_kernel<1, 0>), grid, block, lds, s, a); break;
-            case 2: hipLaunchKernelGGL((gemv_ksplit_kernel<2, 0>), grid, block, lds, s, a); break;
-            case 4: hipLaunchKernelGGL((gemv_ksplit_kernel<4, 0>), grid, block, lds, s, a); break;
-            case 8: hipLaunchKernelGGL((gemv_ksplit_kernel<8, 0>), grid, block, lds, s, a); break;
+            case 1:
+                hipLaunchKernelGGL((gemv_ksplit_kernel<1, 0>), grid, block, lds, s, nullptr, nullptr, nullptr, 0, 0, 0.0f, a);
+                break;
+            case 2:
+                hipLaunchKernelGGL((gemv_ksplit_kernel<2, 0>), grid, block, lds, s, nullptr, nullptr, nullptr, 0, 0, 0.0f, a);
+                break;
+            case 4:
+                hipLaunchKernelGGL((gemv_ksplit_kernel<4, 0>), grid, block, lds, s, nullptr, nullptr, nullptr, 0, 0, 0.0f, a);
+                break;
+            case 8:
+                hipLaunchKernelGGL((gemv_ksplit_kernel<8, 0>), grid, block, lds, s, nullptr, nullptr, nullptr, 0, 0, 0.0f, a);
+                break;
             default: return hipErrorInvalidValue;
         }
     } else {

@@ -14,14 +14,17 @@ can silently lose:
 import re
 import shutil
 import subprocess
+import sys
 from pathlib import Path
 
 import pytest
 
 CSRC = Path(__file__).resolve().parents[1] / "rotor-rag_amd" / "csrc"
+sys.path.insert(0, str(CSRC))
+from build import DEVICE_FLAGS  # noqa: E402  (the library's own device flags)
+
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "--cuda-device-only", "-S",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "--cuda-device-only", "-S", *DEVICE_FLAGS]
 
 
 def _asm(src, tmp_path):
@@ -34,7 +37,8 @@ def _asm(src, tmp_path):
 
 
 def _kernels(asm):
-    """kernel symbol -> its instruction text (label to s_endpgm)."""
+    """kernel symbol -> its instruction text (label to s_endpgm); "__meta__" -> {symbol:
+    its .amdhsa_kernel descriptor block}."""
     out, name, body = {}, None, []
     for line in asm.splitlines():
         m = re.match(r"^(_Z\S+):", line)
@@ -46,6 +50,8 @@ def _kernels(asm):
             if "s_endpgm" in line:
                 out[name] = "\n".join(body)
                 name = None
+    out["__meta__"] = {m.group(1): m.group(2)
+                       for m in re.finditer(r"\.amdhsa_kernel (\S+)\n(.*?)\.end_amdhsa_kernel", asm, re.S)}
     return out
 
 
@@ -71,6 +77,14 @@ def test_gemv_kernels_scalar_descriptors_no_spills(gemv):
         assert "flat_load" not in t, f"{n}: per-lane flat loads"
         assert _waterfalls(t) == 0, f"{n}: readfirstlane loop"
         assert "scratch_" not in t, f"{n}: register spills"
+
+
+def test_gemv_prologue_source_preloaded(gemv):
+    # the KSPLIT kernels with a prologue get their row source (x, aux, aux2, K, mode, eps:
+    # 9 dwords) in SGPRs at wave launch
+    for n in [n for n in gemv if "gemv_ksplit_kernel" in n]:
+        m = re.search(r"\.amdhsa_user_sgpr_kernarg_preload_length\s+(\d+)", gemv["__meta__"][n])
+        assert m and int(m.group(1)) >= 9, n
 
 
 def test_gemv_rows_reads_activations_with_scalar_loads(gemv):

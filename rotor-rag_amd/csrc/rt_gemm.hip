@@ -479,7 +479,9 @@ static hipError_t launch_tile_cfg(int cfg, const GemmGroupArgs& ga, int tiles, h
         case kTile128x128: return launch_tile<128, 128, 2, 4>(ga, tiles, s);
         case kTile256x128: return launch_tile<256, 128, 2, 4>(ga, tiles, s);
         case kTile256x256: return launch_tile<256, 256, 2, 4>(ga, tiles, s);
-        case kTile64x128: return launch_tile<64, 128, 1, 4>(ga, tiles, s);
+        // 64-row tiles do 4 MFMAs per wave per step: an 8-deep ring (64 KiB) keeps more
+        // steps of loads in flight (512-token prefill 4.87 -> 4.83 ms)
+        case kTile64x128: return launch_tile<64, 128, 1, 8>(ga, tiles, s);
         default: return hipErrorInvalidValue;
     }
 }

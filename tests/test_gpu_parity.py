@@ -108,17 +108,30 @@ def test_extreme_accumulators(hip):
     assert acc.tolist() == [[-128 * K, 128 * K, 0], [127 * K, -127 * K, 0]]
 
 
-def test_error_codes_in_weights_decode_to_zero(hip):
+@pytest.mark.parametrize("M", [3, 16, 100])  # GEMV, split-K GEMM, tile GEMM
+def test_error_codes_in_weights_decode_to_zero(hip, M):
     import torch
 
-    rng = np.random.default_rng(9)
+    rng = np.random.default_rng(9 + M)
     raw = rng.integers(0, 256, size=(70, 40), dtype=np.uint8)  # includes reserved 11 codes
     K = 160
     W = O.unpack_rotor(raw, K)
-    q = rng.integers(-128, 128, size=(3, K), dtype=np.int8)
+    q = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
     w = hip.upload(raw, K, 1.0)
     acc = hip.linear_i32(w, torch.from_numpy(q)).cpu().numpy()
     assert np.array_equal(acc.astype(np.int64), O.linear_i64(q, W))
+
+
+def test_download_canonicalises_reserved_codes(hip):
+    # the device holds w + 1, so the reserved rotor code 11 (value 0) comes back as 00;
+    # every other code, and the values, round-trip
+    rng = np.random.default_rng(11)
+    K = 157  # ragged: the last byte holds one element
+    raw = rng.integers(0, 256, size=(70, (K + 3) // 4), dtype=np.uint8)
+    back = hip.upload(raw, K, 1.0).download()
+    W = O.unpack_rotor(raw, K)
+    assert np.array_equal(O.unpack_rotor(back, K), W)
+    assert np.array_equal(back, O.pack_rotor(W))
 
 
 @pytest.mark.parametrize("N,K", [(2560, 2560), (77, 130), (1, 5), (640, 2560)])

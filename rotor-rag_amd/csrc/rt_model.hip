@@ -133,6 +133,7 @@ __global__ void __launch_bounds__(256) attention_kernel(const float* __restrict_
 // The 4 waves' (m, l, O) are merged through LDS at the end.  fp32 products, fp32 sums in
 // the matrix cores' order.
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <int HD>
 __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __restrict__ q,
@@ -174,52 +175,49 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
     float mrow = -INFINITY, lrow = 0.0f;
     const float* K = Kc + (size_t)kh * HD * Lmax;
     const float* V = Vc + (size_t)kh * Lmax * HD;
-    // Staging through registers, one buffer in use at a time: this block's V loads are in
-    // flight during its S^T MFMAs, the next block's K loads during its PV MFMAs.  Keys
-    // past Lmax read as zeros; keys past kend are masked below.
-    float4 stg[HD * BK / 4 / 64];
-    auto load_k = [&](int key0) {
+    // K and V blocks go global -> LDS directly (buffer loads with an LDS destination, range
+    // checked per head: keys past Lmax read as zeros).  A block's K loads are issued as
+    // soon as the previous block's K operands have been read out of the slice, its V loads
+    // as soon as the previous V operands have: each has a whole block of MFMAs to land.
+    // Keys past kend are masked below.
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)K, 0, (unsigned)(HD * Lmax * 4), kBufDword3);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)V, 0, (unsigned)(HD * Lmax * 4), kBufDword3);
+    constexpr int kBlkLoads = HD * BK / 4 / 64;  // 16-byte loads per lane per block (16)
+    auto load_k = [&](int key0) {  // Ks[d][j] = K[d][key0 + j], 8 dims per load
 #pragma unroll
-        for (int it = 0; it < HD * BK / 4 / 64; ++it) {
-            const int idx = it * 64 + lane, d = idx / (BK / 4), jq = 4 * (idx % (BK / 4));
-            stg[it] = key0 + jq + 3 < Lmax ? *reinterpret_cast<const float4*>(K + (size_t)d * Lmax + key0 + jq)
-                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int it = 0; it < kBlkLoads; ++it) {
+            const int d = 8 * it + (lane >> 3), j = 4 * (lane & 7);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(krs, (lds_void*)(Ks + 256 * it), 16, (d * Lmax + key0 + j) * 4, 0,
+                                                     0, 0);
         }
     };
-    auto store_k = [&]() {
+    auto load_v = [&](int key0) {  // Vs[j][d] = V[key0 + j][d], 2 keys per load
 #pragma unroll
-        for (int it = 0; it < HD * BK / 4 / 64; ++it) {
-            const int idx = it * 64 + lane, d = idx / (BK / 4), jq = 4 * (idx % (BK / 4));
-            *reinterpret_cast<float4*>(Ks + d * BK + jq) = stg[it];
+        for (int it = 0; it < kBlkLoads; ++it) {
+            const int j = 2 * it + (lane >> 5), dq = 4 * (lane & 31);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(vrs, (lds_void*)(Vs + 256 * it), 16, ((key0 + j) * HD + dq) * 4, 0,
+                                                     0, 0);
         }
     };
-    auto load_v = [&](int key0) {
-#pragma unroll
-        for (int it = 0; it < HD * BK / 4 / 64; ++it) {
-            const int idx = it * 64 + lane, j = idx / (HD / 4), dq = 4 * (idx % (HD / 4));
-            stg[it] = key0 + j < Lmax ? *reinterpret_cast<const float4*>(V + (size_t)(key0 + j) * HD + dq)
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    auto store_v = [&]() {
-#pragma unroll
-        for (int it = 0; it < HD * BK / 4 / 64; ++it) {
-            const int idx = it * 64 + lane, j = idx / (HD / 4), dq = 4 * (idx % (HD / 4));
-            *reinterpret_cast<float4*>(Vs + j * HD + dq) = stg[it];
-        }
-    };
-    if (wave < nblk) load_k(wave * BK);
+    if (wave < nblk) {
+        load_k(wave * BK);
+        load_v(wave * BK);
+    }
     for (int b = wave; b < nblk; b += 4) {
         const int key0 = b * BK;
-        store_k();
-        load_v(key0);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave reads back its own slice
+        const bool more = b + 4 < nblk;
+        // this block's K has landed (its V may still be in flight)
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kBlkLoads) : "memory");
         // S^T[key][row]; the 64 A operands are read from LDS ahead of the MFMA chain (read
         // one by one in front of each MFMA, every pair of MFMAs would wait for the LDS)
         float ka[64];
 #pragma unroll
         for (int st = 0; st < 64; ++st) ka[st] = Ks[(64 * hl + st) * BK + row];
-        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the chain
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // K slice read out: refill it
+        if (more) load_k((b + 4) * BK);
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads and loads ahead of the chain
         v16f sacc = v16f{};
 #pragma unroll
         for (int st = 0; st < 64; ++st) sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[st], qr[st], sacc, 0, 0, 0);
@@ -243,15 +241,17 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
         ls += __shfl_xor(ls, 32, 64);
         lrow = lrow * alpha + ls;
         mrow = mnew;
-        store_v();
-        if (b + 4 < nblk) load_k((b + 4) * BK);
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        // this block's V has landed (the next block's K may still be in flight)
+        if (more) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kBlkLoads) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         // O^T[dim][row] = alpha O^T + V^T P^T (A operands read ahead, as above)
         float va[HD / 32][16];
 #pragma unroll
         for (int nb = 0; nb < HD / 32; ++nb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) va[nb][r] = Vs[(8 * (r >> 2) + 4 * hl + (r & 3)) * HD + 32 * nb + row];
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // V slice read out: refill it
+        if (more) load_v((b + 4) * BK);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int nb = 0; nb < HD / 32; ++nb) {
@@ -260,7 +260,6 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
             for (int r = 0; r < 16; ++r) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(va[nb][r], pr[r], acc, 0, 0, 0);
             o[nb] = acc;
         }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the slice is refilled
     }
     // merge the waves: slice w becomes [32 rows][HD] of O^T, then (m, l) per row
     __syncthreads();

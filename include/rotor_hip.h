@@ -71,7 +71,10 @@ int rt_version(void);
 int rt_device_count(int* n);
 
 /* Create a context on `device`: checks the device is gfx950, makes it current and
- * uses the null stream until rt_ctx_set_stream.  Replaces GPUTernaryOps.__init__
+ * uses the null stream until rt_ctx_set_stream.  A context holds a scratch buffer for
+ * the activations of rt_linear_* calls, which grows when a call needs more rows than any
+ * before it (after a device synchronisation); calls on one context from several host
+ * threads must be serialised by the caller.  Replaces GPUTernaryOps.__init__
  * (src/rotor/gpu_ternary.py:78-110: platform scan, context, queue, kernel build). */
 int rt_ctx_create(int device, rt_ctx** out);
 int rt_ctx_destroy(rt_ctx* ctx);

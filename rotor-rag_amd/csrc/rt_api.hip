@@ -53,14 +53,18 @@ struct DeviceGuard {
     }
 };
 
-// Device buffer that only grows.
+// Device buffer that only grows.  Work enqueued earlier (on whichever stream the context
+// had then) may still read the old buffer, so the device is synchronised before it is
+// freed; growth happens only when a call needs more rows than any call before it.
 struct Scratch {
     void* p = nullptr;
     size_t bytes = 0;
     hipError_t ensure(size_t need) {
         if (need <= bytes) return hipSuccess;
         if (p) {
-            hipError_t e = hipFree(p);
+            hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess) return e;
+            e = hipFree(p);
             if (e != hipSuccess) return e;
             p = nullptr;
             bytes = 0;

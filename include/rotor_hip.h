@@ -50,11 +50,14 @@ typedef struct rt_act rt_act;         /* reusable quantised activations        *
 #define RT_SRC_RELU2MUL_NORM 4  /* q = quant(RMSNorm(relu(x)^2 * aux) * aux2)     */
 #define RT_SRC_ATTN_NORM 5      /* q = quant(RMSNorm(attention(x)) * aux): x = the workspace
                                    of rt_attention_decode_partials, combined per head */
+#define RT_SRC_RMSNORM_SSQ 6    /* as RT_SRC_RMSNORM, with sum_k x^2 given as K/32 f64 partial
+                                   sums: aux2 = (const float*) the `ssq` array written by an
+                                   rt_plan_create_gate_up plan (K % 64 == 0, K <= 8192) */
 typedef struct rt_src {
     int mode;           /* RT_SRC_*                                  */
     const float* x;     /* fp32 [K] (device); partials for ATTN_NORM */
     const float* aux;   /* fp32 [K]: norm weight or up (device)      */
-    const float* aux2;  /* fp32 [K]: norm weight (RELU2MUL_NORM)     */
+    const float* aux2;  /* fp32 [K]: norm weight (RELU2MUL_NORM); f64 [K/32] (RMSNORM_SSQ) */
     float eps;          /* RMSNorm epsilon                           */
     int attn_head_dim;  /* ATTN_NORM: head dimension (K = heads * head_dim) */
     int attn_max_len;   /* ATTN_NORM: Lmax given to rt_attention_decode_partials */
@@ -196,6 +199,22 @@ int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_
  * buffers named in src/y/residual must outlive the plan.  Run with rt_plan_run. */
 int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_src* src, float* const* y,
                          const float* const* residual, rt_plan** out);
+
+/* Fused decode plan for the gated FFN's gate and up projections (one token, one launch).
+ * w_gu holds both matrices [2F][K] interleaved in groups of 32 rows: row 64 j + r is gate
+ * row 32 j + r for r < 32 and up row 32 j + r - 32 otherwise (F % 32 == 0; build it from the
+ * two rotor matrices by interleaving their rows); s_gate and s_up are their weight scales
+ * (the scale stored with w_gu is not used).  Every workgroup
+ * quantises the input row as `src` says (QUANT, RMSNORM or RMSNORM_SSQ) and writes the FFN
+ * activation a[i] = relu(g_i)^2 * u_i (fp32 [F], device; g_i, u_i rounded as
+ * rt_plan_create_fused writes y) and, per group j of 32 outputs, ssq[j] = sum of
+ * (double)a_i^2 (f64 [F/32], device), which an RT_SRC_RMSNORM_SSQ plan for the down
+ * projection takes in place of reducing a again.  g_out / u_out (nullable, fp32 [F]) also
+ * receive g and u.  K % 64 == 0; 16-byte aligned sources.
+ * Fuses the elementwise gate of GatedFFN.forward (src/rotor/transformer.py:329-337,
+ * relu^2 in the BitNet configuration) into the projections that produce its inputs. */
+int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, float s_up, const rt_src* src,
+                           float* a, double* ssq, float* g_out, float* u_out, rt_plan** out);
 
 /* ---- kernels around the linears for BitNet-2B-shape inference ----------------------
  * Positions are read from device memory (`pos`: position of the first of the M tokens)

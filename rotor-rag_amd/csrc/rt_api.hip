@@ -119,6 +119,11 @@ struct rt_plan {
     // (run_shape); 0 a quantiser launch, then the GEMV
     int run_pro = 0;
     GemvShape run_shape{};
+    float* pair_a = nullptr;      // gate/up pair plan: relu(g)^2 * u [N / 2]
+    double* pair_ssq = nullptr;   // its sum of squares per 32 outputs
+    float* pair_g = nullptr;      // optional g, u [N / 2]
+    float* pair_u = nullptr;
+    float pair_sg = 1.0f, pair_su = 1.0f;  // gate and up scales
     int quant_maxK = 0;  // > 0: every quant problem takes the vectorised row kernel (largest K)
 };
 
@@ -632,6 +637,12 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
     if (plan->fused) {
         a.has_pro = 1;
         a.pro = plan->pro;
+        a.pair_a = plan->pair_a;
+        a.pair_ssq = plan->pair_ssq;
+        a.pair_g = plan->pair_g;
+        a.pair_u = plan->pair_u;
+        a.pair_sg = plan->pair_sg;
+        a.pair_su = plan->pair_su;
     }
     a.dev = plan->dev_probs;
     a.rb2p = plan->dev_rb2p;
@@ -912,15 +923,17 @@ int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const r
     if (G <= 0 || G > (1 << 16)) return fail(RT_EINVAL, "rt_plan_create_fused: G out of range");
     if (!src->x) return fail(RT_EINVAL, "rt_plan_create_fused: source x is NULL");
     if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRelu2Mul && src->mode != kRelu2MulNorm &&
-        src->mode != kAttnNorm)
+        src->mode != kAttnNorm && src->mode != kRmsNormSsq)
         return fail(RT_EINVAL, "rt_plan_create_fused: unknown source mode");
     if (src->mode == kAttnNorm && (src->attn_head_dim <= 0 || src->attn_head_dim % 16 || src->attn_max_len <= 0 ||
                                    !w[0] || w[0]->K % src->attn_head_dim))
         return fail(RT_EINVAL, "rt_plan_create_fused: attention source needs head_dim (multiple of 16) dividing K "
                                "and max_len");
-    if ((src->mode != kQuant && !src->aux) || (src->mode == kRelu2MulNorm && !src->aux2))
+    if ((src->mode != kQuant && !src->aux) || ((src->mode == kRelu2MulNorm || src->mode == kRmsNormSsq) && !src->aux2))
         return fail(RT_EINVAL, "rt_plan_create_fused: the source mode needs aux/aux2");
     const int K = w[0] ? w[0]->K : 0;
+    if (src->mode == kRmsNormSsq && (K % 64 || K > 8192))
+        return fail(RT_EINVAL, "rt_plan_create_fused: RMSNORM_SSQ needs K % 64 == 0 and K <= 8192");
     for (int g = 0; g < G; ++g) {
         if (!w[g] || !y[g]) return fail(RT_EINVAL, "rt_plan_create_fused: NULL entry in a pointer array");
         if (w[g]->K != K) return fail(RT_EINVAL, "rt_plan_create_fused: all weights must share K (one input)");
@@ -969,6 +982,50 @@ int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const r
         rt_plan_free(p);
         return hip_fail(e, "rt_plan_create_fused");
     }
+    *out = p;
+    return RT_OK;
+}
+
+int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, float s_up, const rt_src* src,
+                           float* a, double* ssq, float* g_out, float* u_out, rt_plan** out) {
+    const char* who = "rt_plan_create_gate_up";
+    if (!ctx || !w_gu || !src || !src->x || !a || !ssq || !out)
+        return fail(RT_EINVAL, std::string(who) + ": NULL argument");
+    *out = nullptr;
+    if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRmsNormSsq)
+        return fail(RT_EINVAL, std::string(who) + ": the source must be QUANT, RMSNORM or RMSNORM_SSQ");
+    if ((src->mode != kQuant && !src->aux) || (src->mode == kRmsNormSsq && !src->aux2))
+        return fail(RT_EINVAL, std::string(who) + ": the source mode needs aux/aux2");
+    if (w_gu->N % kRowBlock) return fail(RT_EINVAL, std::string(who) + ": the interleaved matrix needs N % 64 == 0");
+    if (w_gu->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": weights live on another device");
+    const int K = w_gu->K, Kp = round_up(K, kChunk), Nb = w_gu->Np / kRowBlock;
+    const GemvShape shape = gemv_shape_fused(Nb, w_gu->C);
+    // the 4-element prologue: K / 4 threads, 16-byte aligned rows
+    auto a16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+    if (K % 64 || K / 4 > 64 * shape.nw || !a16(src->x) || !a16(src->aux) || !a16(src->aux2))
+        return fail(RT_EINVAL, std::string(who) + ": needs K % 64 == 0, K / 4 <= the workgroup's threads and "
+                                                  "16-byte aligned sources");
+    DeviceGuard guard(ctx->device);
+    rt_plan* p = new rt_plan();
+    p->device = ctx->device;
+    p->G = 1;
+    p->M = 1;
+    p->mt = 1;
+    p->Mpad = 1;
+    p->U = 0;
+    p->fused = true;
+    p->pro = QuantProb{src->x, nullptr, nullptr, nullptr, nullptr, K, Kp, src->mode, src->aux, src->eps, nullptr,
+                       src->aux2, 0, 0};
+    p->probs = {GemvProb{w_gu->tiles, nullptr, nullptr, nullptr, nullptr, w_gu->scale, w_gu->N, w_gu->C, w_gu->N,
+                         0, nullptr}};
+    p->pair_sg = s_gate;
+    p->pair_su = s_up;
+    p->total_rb = Nb;
+    p->shape = shape;
+    p->pair_a = a;
+    p->pair_ssq = ssq;
+    p->pair_g = g_out;
+    p->pair_u = u_out;
     *out = p;
     return RT_OK;
 }

@@ -253,7 +253,12 @@ constexpr int kAttnMaxThreads = 640;
 // relu²·up + sub-norm), 16 elements per thread; 3 / 4 the same with 4 / 8 consecutive
 // elements per thread (K % 64 == 0, K / 4 or K / 8 <= threads, 16-byte aligned sources);
 // 2 prologue combining decode-attention partials (kAttnNorm).
-template <int MT, int PRO>
+// PAIR (PRO 3, gate/up of the decode FFN): the matrix interleaves gate and up in 32-row
+// groups (row 64 j + r: gate row 32 j + r for r < 32, up row 32 j + r - 32 otherwise), so a
+// workgroup's row block holds both inputs of 32 outputs: it writes the FFN activation
+// a = relu(g)^2 * u of those 32 (g and u rounded as emit rounds y) and their f64 sum of
+// squares, the two inputs of the down projection's sub-norm.
+template <int MT, int PRO, bool PAIR = false>
 __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     gemv_ksplit_kernel(const float* pro_x, const float* pro_aux, const float* pro_aux2, int pro_K, int pro_mode,
                        float pro_eps, GemvArgs a) {
@@ -290,6 +295,7 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
         early = attn_fits1(pro, blockDim.x);
         if (early) attn_load1(pro, rr);
     }
+    static_assert(!PAIR || (PRO == 3 && MT == 1), "the pair epilogue follows the 4-element prologue");
     const GemvProb P = find_prob(a, blockIdx.x);
     const int rb = blockIdx.x - P.wg_begin;
     const int C = P.C, ldx = C * 16;
@@ -337,6 +343,28 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
 #pragma unroll
     for (int m = 0; m < MT; ++m) red[(wave * MT + m) * kRowBlock + lane] = row_dot(accP[m], accQ[m], sx[m]);
     __syncthreads();
+    if constexpr (PAIR) {
+        if (threadIdx.x < kRowBlock) {  // wave 0; lanes 32.. only pad the reduction
+            const int r = threadIdx.x & 31, nu = rb * kRowBlock + 32 + r, i = rb * 32 + r;
+            int sg = 0, su = 0;
+            for (int w = 0; w < nw; ++w) {
+                sg += red[w * kRowBlock + r];
+                su += red[w * kRowBlock + 32 + r];
+            }
+            float av = 0.0f;
+            if (threadIdx.x < 32 && nu < P.N) {
+                const float g = ((float)sg * sx_pro) * a.pair_sg;
+                const float u = ((float)su * sx_pro) * a.pair_su;
+                av = g > 0.0f ? (g * g) * u : 0.0f;
+                a.pair_a[i] = av;
+                if (a.pair_g) a.pair_g[i] = g;
+                if (a.pair_u) a.pair_u[i] = u;
+            }
+            const double ss = wave_reduce63((double)av * (double)av, 0.0, [](double x, double y) { return x + y; });
+            if (threadIdx.x == kRowBlock - 1) a.pair_ssq[rb] = ss;
+        }
+        return;
+    }
     for (int idx = threadIdx.x; idx < MT * kRowBlock; idx += blockDim.x) {
         const int m = idx / kRowBlock, r = idx % kRowBlock;
         int s = 0;
@@ -382,6 +410,15 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
         const dim3 grid((unsigned)(a.total_rb / shape.nw), 1);
         const size_t lds = (size_t)a.pro.Kp + sizeof(RowSmem);  // pro.Kp: the largest Kp of the problems
         hipLaunchKernelGGL((gemv_rows_kernel<1, 1>), grid, block, lds, s, a);
+    } else if (a.has_pro && a.pair_a) {  // gate/up pair: the 4-element prologue only
+        const QuantProb& P = a.pro;
+        if (mt != 1 || a.M != 1 || !shape.ksplit || P.K % 64 || !aligned16(P.x) || !aligned16(P.aux) ||
+            !aligned16(P.aux2) || P.K / 4 > 64 * shape.nw)
+            return hipErrorInvalidValue;
+        const dim3 grid((unsigned)a.total_rb, 1);
+        const size_t lds = (size_t)shape.nw * kRowBlock * sizeof(int) + (size_t)P.Kp + sizeof(RowSmem);
+        hipLaunchKernelGGL((gemv_ksplit_kernel<1, 3, true>), grid, block, lds, s, P.x, P.aux, P.aux2, P.K, P.mode,
+                           P.eps, a);
     } else if (a.has_pro) {  // single token, prologue-quantised input: KSPLIT shape only
         if (mt != 1 || a.M != 1 || !shape.ksplit) return hipErrorInvalidValue;
         const dim3 grid((unsigned)a.total_rb, 1);

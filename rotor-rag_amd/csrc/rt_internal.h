@@ -66,7 +66,12 @@ __host__ __device__ inline unsigned rotor_code(unsigned g) {
 //   kRelu2MulNorm  v = RMSNorm(relu2mul(x, u)) * norm_w       (norm_w = aux2)
 //   kAttnNorm v = RMSNorm(combined decode-attention partials x) * norm_w (aux),
 //             partials [K/hd heads][S][hd + 2]  (one token only)
-enum QuantMode { kQuant = 0, kPermute = 1, kRmsNorm = 2, kRelu2Mul = 3, kRelu2MulNorm = 4, kAttnNorm = 5 };
+//   kRmsNormSsq  as kRmsNorm, with sum_k x^2 also given as K/32 f64 partial sums in aux2
+//             (cast; the `ssq` output of a gate/up pair plan): the 4- and 8-element
+//             prologues add those up instead of reducing x over the workgroup; every
+//             other path ignores them and reduces x itself
+enum QuantMode { kQuant = 0, kPermute = 1, kRmsNorm = 2, kRelu2Mul = 3, kRelu2MulNorm = 4, kAttnNorm = 5,
+                 kRmsNormSsq = 6 };
 
 struct QuantProb {
     const float* x;      // fp32 [M][K] (gate in kRelu2Mul)
@@ -115,6 +120,15 @@ struct GemvArgs {
     QuantProb pro;        // has_pro == 1: source row of the prologue (mode, x, aux, aux2, eps, K, Kp)
     int ninl;             // > 0: the G = ninl problems are inl[] (dev and rb2p unused)
     GemvProb inl[kInlineProbs];
+    // gate/up pair (KSPLIT, has_pro == 1, one problem whose rows interleave gate and up in
+    // groups of 32): row block j writes, instead of y, pair_a[32 j + r] = relu(g)^2 * u of
+    // its rows r and 32 + r, pair_ssq[j] = sum over those 32 of (double) a^2, and g, u to
+    // pair_g, pair_u when they are not null
+    float* pair_a;
+    double* pair_ssq;
+    float* pair_g;
+    float* pair_u;
+    float pair_sg, pair_su;  // the gate and up scales
 };
 
 struct GemvShape {

@@ -80,7 +80,7 @@ __device__ __forceinline__ void load_group(const float* __restrict__ xr, int g, 
 }
 
 __device__ __forceinline__ bool has_norm(const QuantProb& P) {
-    return P.mode == kRmsNorm || P.mode == kRelu2MulNorm || P.mode == kAttnNorm;
+    return P.mode == kRmsNorm || P.mode == kRelu2MulNorm || P.mode == kAttnNorm || P.mode == kRmsNormSsq;
 }
 __device__ __forceinline__ bool has_relu2(const QuantProb& P) { return P.mode == kRelu2Mul || P.mode == kRelu2MulNorm; }
 __device__ __forceinline__ const float* norm_weight(const QuantProb& P) {
@@ -310,7 +310,8 @@ __device__ __forceinline__ void scatter_q(const float (&v)[E], float sc, v4u* lq
 template <int E>
 struct RowRegsE {
     float v[E], u[E], w[E];
-    bool live;  // wave-uniform: some lane of this wave owns elements
+    double ssq[4];  // kRmsNormSsq: partial sums of squares l, l + 64, .. of this lane
+    bool live;      // wave-uniform: some lane of this wave owns elements
 };
 
 template <int E>
@@ -334,6 +335,15 @@ __device__ __forceinline__ void row_loadE(const QuantProb& P, RowRegsE<E>& r) {
         if (has_relu2(P)) loadE<E>(P.aux + E * t, r.u);
         if (has_norm(P)) loadE<E>(norm_weight(P) + E * t, r.w);
     }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.ssq[i] = 0.0;
+    if (P.mode == kRmsNormSsq) {  // K / 32 <= 256 partials (K <= 8192): up to four per lane
+        const double* pp = reinterpret_cast<const double*>(P.aux2);
+        const int lane = threadIdx.x & 63, n = K >> 5;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (lane + 64 * i < n) r.ssq[i] = pp[lane + 64 * i];
+    }
 }
 
 template <int E>
@@ -349,9 +359,13 @@ __device__ __forceinline__ float row_finishE(const QuantProb& P, RowRegsE<E>& r,
     }
     if (has_norm(P)) {
         double ss = 0.0;
+        if (P.mode == kRmsNormSsq) {  // every wave adds the given partials, in one order
+            ss = lane63(wave_reduce63((r.ssq[0] + r.ssq[1]) + (r.ssq[2] + r.ssq[3]), 0.0, dadd_op));
+        } else {
 #pragma unroll
-        for (int j = 0; j < E; ++j) ss += (double)v[j] * (double)v[j];
-        ss = block_reduce(ss, sm->d, dadd_op, r.live);
+            for (int j = 0; j < E; ++j) ss += (double)v[j] * (double)v[j];
+            ss = block_reduce(ss, sm->d, dadd_op, r.live);
+        }
         const float norm = sqrtf((float)(ss / (double)K) + P.eps);
         if (mine) {
 #pragma unroll

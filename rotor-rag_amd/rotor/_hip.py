@@ -22,7 +22,7 @@ class RtSrc(ctypes.Structure):
                 ("eps", ctypes.c_float), ("attn_head_dim", ctypes.c_int), ("attn_max_len", ctypes.c_int)]
 
 
-SRC_QUANT, SRC_RMSNORM, SRC_RELU2MUL, SRC_RELU2MUL_NORM, SRC_ATTN_NORM = 0, 2, 3, 4, 5
+SRC_QUANT, SRC_RMSNORM, SRC_RELU2MUL, SRC_RELU2MUL_NORM, SRC_ATTN_NORM, SRC_RMSNORM_SSQ = 0, 2, 3, 4, 5, 6
 
 # name -> (restype, argtypes); every entry point of include/rotor_hip.h
 _P = ctypes.c_void_p
@@ -63,6 +63,7 @@ SIGNATURES = {
                                 ctypes.POINTER(_P)]),
     "rt_plan_create_fused": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(RtSrc), ctypes.POINTER(_P),
                                   ctypes.POINTER(_P), ctypes.POINTER(_P)]),
+    "rt_plan_create_gate_up": (_I, [_P, _P, _F, _F, ctypes.POINTER(RtSrc), _P, _P, _P, _P, ctypes.POINTER(_P)]),
     "rt_embed": (_I, [_P, _P, _I, _I, _P, _I, _P]),
     "rt_rope_kv_append": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "rt_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),

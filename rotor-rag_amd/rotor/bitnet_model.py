@@ -201,6 +201,11 @@ class _DeviceModel:
         # kernel and gives o_proj a plain RMSNorm prologue (one more launch per layer,
         # ~0.04 ms/token slower at 30 layers)
         self.attn_in_prologue = True
+        # decode FFN: True (default, when the shapes allow) computes relu(g)^2 * u and its
+        # per-block sums of squares in the gate/up GEMV's epilogue, so the down GEMV's
+        # prologue only normalises and quantises; False runs the gate/up plan and lets the
+        # down prologue form relu(g)^2 * u and reduce it
+        self.ffn_pair = D % 64 == 0 and F % 64 == 0 and F <= 8192
 
     def _state(self, M):
         st = self.state.get(M)
@@ -211,7 +216,8 @@ class _DeviceModel:
         dev, D, F, H, Hkv, hd = self.device, self.D, self.F, self.H, self.Hkv, self.hd
         e = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)
         st = {"h": e(M, D), "q": e(M, H * hd), "k": e(M, Hkv * hd), "v": e(M, Hkv * hd), "o": e(M, H * hd),
-              "g": e(M, F), "u": e(M, F)}
+              "g": e(M, F), "u": e(M, F), "a": e(F),
+              "ssq": torch.empty(F // 32, dtype=torch.float64, device=dev)}
         st["qkv"], st["gu"], st["o_plan"], st["d_plan"] = [], [], [], []
         hip, eps = self.hip, self.m.eps
         for L in self.layers:
@@ -228,6 +234,15 @@ class _DeviceModel:
                                                        eps=eps, ys=[h], residuals=[h]))
                 else:
                     st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_QUANT, o, ys=[h], residuals=[h]))
+                if L["ffn_sub_norm"] is not None and self.ffn_pair:
+                    if "gate_up" not in L:  # the interleaved copy the pair plan runs (decode only)
+                        L["gate_up"] = hip.interleave_gate_up(L["gate_proj"], L["up_proj"])
+                    w_gu, scales = L["gate_up"]
+                    st["gu"].append(hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM, h, L["post_norm"], eps=eps,
+                                                     a=st["a"], ssq=st["ssq"]))
+                    st["d_plan"].append(hip.plan_fused([L["down_proj"]], _hip.SRC_RMSNORM_SSQ, st["a"],
+                                                       L["ffn_sub_norm"], st["ssq"], eps=eps, ys=[h], residuals=[h]))
+                    continue
                 st["gu"].append(hip.plan_fused([L["gate_proj"], L["up_proj"]], _hip.SRC_RMSNORM, h, L["post_norm"],
                                                eps=eps, ys=[g, u]))
                 if L["ffn_sub_norm"] is not None:

@@ -391,9 +391,7 @@ class HIPTernaryOps:
         for w, y in zip(weights, ys):
             if w.in_features != K or y.numel() != w.out_features or not y.is_contiguous():
                 raise ValueError("plan_fused: shapes do not match")
-        for t in ((x if mode != _hip.SRC_ATTN_NORM else None), aux, aux2):
-            if t is not None and (t.numel() < K or not t.is_contiguous() or t.device != self.device):
-                raise ValueError("plan_fused: source tensors must be contiguous device tensors of >= K elements")
+        self._check_src(mode, K, x, aux, aux2, "plan_fused")
         if mode == _hip.SRC_ATTN_NORM:
             need = self.lib.rt_attention_decode_workspace(K // max(attn_head_dim, 1), attn_head_dim, attn_max_len)
             if attn_head_dim <= 0 or x.numel() * x.element_size() < need:
@@ -409,6 +407,55 @@ class HIPTernaryOps:
         _hip.check(self.lib.rt_plan_create_fused(self.ctx, G, wa, ctypes.byref(src), ya, ra, ctypes.byref(h)),
                    "rt_plan_create_fused")
         return LinearPlan(self, h, (list(weights), [x, aux, aux2], list(ys), list(residuals or [])))
+
+    def _check_src(self, mode, K, x, aux, aux2, who):
+        for t in ((x if mode != _hip.SRC_ATTN_NORM else None), aux,
+                  (aux2 if mode != _hip.SRC_RMSNORM_SSQ else None)):
+            if t is not None and (t.numel() < K or not t.is_contiguous() or t.device != self.device):
+                raise ValueError(f"{who}: source tensors must be contiguous device tensors of >= K elements")
+        if mode == _hip.SRC_RMSNORM_SSQ:
+            t = aux2
+            if (t is None or t.dtype != _torch().float64 or t.numel() < K // 32 or not t.is_contiguous()
+                    or t.device != self.device):
+                raise ValueError(f"{who}: RMSNORM_SSQ needs aux2 = float64 device partial sums [K/32]")
+
+    def interleave_gate_up(self, w_gate, w_up):
+        """The matrix rt_plan_create_gate_up runs: gate and up [F, K] interleaved in groups
+        of 32 rows (rows 64 j .. 64 j + 31 = gate rows 32 j .., the next 32 = up rows 32 j ..),
+        uploaded once; returns (matrix, (gate scale, up scale))."""
+        F, K = w_gate.out_features, w_gate.in_features
+        if (w_up.out_features, w_up.in_features) != (F, K) or F % 32:
+            raise ValueError("interleave_gate_up: gate and up must have the same shape with F % 32 == 0")
+        g, u = w_gate.download(), w_up.download()
+        gu = np.stack([g.reshape(F // 32, 32, -1), u.reshape(F // 32, 32, -1)], axis=1).reshape(2 * F, -1)
+        return self.upload(gu, K, 1.0), (w_gate.scale, w_up.scale)
+
+    def plan_gate_up(self, w_gu, scales, mode: int, x, aux=None, aux2=None, eps: float = 1e-6, a=None, ssq=None,
+                     g_out=None, u_out=None):
+        """One-token gate/up plan of the gated FFN (rt_plan_create_gate_up) on the matrix of
+        interleave_gate_up: a[i] = relu(g_i)^2 * u_i (fp32 [F]) and ssq[j] (float64 [F/32]) =
+        sum of a^2 over outputs 32 j .. 32 j + 31, the input of an SRC_RMSNORM_SSQ plan."""
+        torch = _torch()
+        N, K = w_gu.out_features, w_gu.in_features
+        F = N // 2
+        if N % 64:
+            raise ValueError("plan_gate_up: the interleaved matrix needs N % 64 == 0")
+        self._check_src(mode, K, x, aux, aux2, "plan_gate_up")
+        if a is None or a.numel() < F or a.dtype != torch.float32 or not a.is_contiguous():
+            raise ValueError("plan_gate_up: a must be a contiguous float32 device tensor of F elements")
+        if ssq is None or ssq.numel() < F // 32 or ssq.dtype != torch.float64 or not ssq.is_contiguous():
+            raise ValueError("plan_gate_up: ssq must be a contiguous float64 device tensor of F/32 elements")
+        for t in (g_out, u_out):
+            if t is not None and (t.numel() < F or t.dtype != torch.float32 or not t.is_contiguous()):
+                raise ValueError("plan_gate_up: g_out / u_out must be float32 device tensors of F elements")
+        ptr = lambda t: t.data_ptr() if t is not None else None
+        src = _hip.RtSrc(int(mode), x.data_ptr(), ptr(aux), ptr(aux2), float(eps), 0, 0)
+        h = ctypes.c_void_p()
+        s_gate, s_up = scales
+        _hip.check(self.lib.rt_plan_create_gate_up(self.ctx, w_gu.handle, float(s_gate), float(s_up), ctypes.byref(src),
+                                                   a.data_ptr(), ssq.data_ptr(), ptr(g_out), ptr(u_out),
+                                                   ctypes.byref(h)), "rt_plan_create_gate_up")
+        return LinearPlan(self, h, ([w_gu], [x, aux, aux2], [a, ssq], [g_out, u_out]))
 
     def __del__(self):
         try:

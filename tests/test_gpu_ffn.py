@@ -206,3 +206,51 @@ def test_fused_plan_equals_act_path(hip, mode, K, N):
            4: O.rms_norm_f64acc(O.relu2_gate(xn, an)[None], a2n)[0]}[mode]
     qo, so = O.quant_rows(src[None])
     assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(s.cpu().numpy(), so)
+
+
+@pytest.mark.parametrize("D,F", [(2560, 6912), (256, 320), (4096, 640), (128, 96)])
+def test_gate_up_pair_plan(hip, D, F):
+    """The gate/up pair plan (gate and up interleaved in 32-row groups) writes g and u
+    exactly as the two-problem fused plan does, a = relu(g)^2 * u with the fp32 operations
+    of oracle.relu2_gate, and per 32 outputs the f64 sum of a^2; a down-projection plan fed
+    (a, ssq) through RMSNORM_SSQ gives exactly the RELU2MUL_NORM plan's output on (g, u)."""
+    import torch
+
+    from rotor import _hip
+
+    rng = np.random.default_rng(D + F)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    h, nw, nwf = d(rng.standard_normal(D) * 2), d(rng.uniform(0.5, 1.5, D)), d(rng.uniform(0.5, 1.5, F))
+    (Wg, sg), (Wu, su), (Wd, sd) = O.make_ternary(rng, F, D), O.make_ternary(rng, F, D), O.make_ternary(rng, D, F)
+    wg, wu, wd = hip.upload(O.pack_rotor(Wg), D, sg), hip.upload(O.pack_rotor(Wu), D, su), hip.upload(O.pack_rotor(Wd), F, sd)
+    g, u = torch.empty(F, device="cuda"), torch.empty(F, device="cuda")
+    hip.plan_fused([wg, wu], _hip.SRC_RMSNORM, h, nw, eps=1e-6, ys=[g, u]).run()
+    w_gu, scales = hip.interleave_gate_up(wg, wu)
+    a = torch.full((F,), float("nan"), device="cuda")
+    ssq = torch.full((F // 32,), float("nan"), dtype=torch.float64, device="cuda")
+    g2, u2 = torch.empty(F, device="cuda"), torch.empty(F, device="cuda")
+    hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM, h, nw, eps=1e-6, a=a, ssq=ssq, g_out=g2, u_out=u2).run()
+    gn, un, an = _np(g), _np(u), _np(a)
+    assert np.array_equal(_np(g2), gn) and np.array_equal(_np(u2), un)
+    assert np.array_equal(an, O.relu2_gate(gn, un))
+    np.testing.assert_allclose(_np(ssq), (an.astype(np.float64).reshape(-1, 32) ** 2).sum(1), rtol=1e-12, atol=0)
+    if F % 64 == 0 and F <= 8192:
+        y1, y2 = torch.empty(D, device="cuda"), torch.empty(D, device="cuda")
+        hip.plan_fused([wd], _hip.SRC_RELU2MUL_NORM, g, u, nwf, eps=1e-6, ys=[y1]).run()
+        hip.plan_fused([wd], _hip.SRC_RMSNORM_SSQ, a, nwf, ssq, eps=1e-6, ys=[y2]).run()
+        assert torch.equal(y1, y2)
+
+
+def test_gate_up_pair_plan_rejects_shapes(hip):
+    import torch
+
+    from rotor import _hip
+
+    rng = np.random.default_rng(5)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    h, nw = d(rng.standard_normal(100)), d(np.ones(100))
+    w1, w2 = (hip.upload(O.pack_rotor(O.make_ternary(rng, 64, 100)[0]), 100, 1.0) for _ in range(2))
+    w_gu, scales = hip.interleave_gate_up(w1, w2)
+    a, ssq = torch.empty(64, device="cuda"), torch.empty(2, dtype=torch.float64, device="cuda")
+    with pytest.raises(RuntimeError, match="K % 64"):
+        hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM, h, nw, a=a, ssq=ssq)

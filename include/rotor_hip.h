@@ -67,7 +67,7 @@ typedef struct rt_src {
  * exception text (src/rotor/gpu_layers.py:21-24). */
 const char* rt_last_error(void);
 
-/* ABI version (major*100 + minor). */
+/* ABI version (major*100 + minor): 101 = 100 + rt_plan_create_gate_up and RT_SRC_RMSNORM_SSQ. */
 int rt_version(void);
 
 /* Number of visible HIP devices (0 when none); RT_OK even when 0. */

@@ -342,7 +342,10 @@ def main():
         plan.run()
         e1.record()
     torch.cuda.synchronize()
-    run_avg = float(np.mean([e0.elapsed_time(e1) for e0, e1 in ev]))
+    run_ms = np.array([e0.elapsed_time(e1) for e0, e1 in ev])
+    run_avg = float(np.mean(run_ms))
+    run_dist = {"p10": round(float(np.percentile(run_ms, 10)), 5), "p50": round(float(np.median(run_ms)), 5),
+                "p90": round(float(np.percentile(run_ms, 90)), 5), "n": int(run_ms.size)}
     bytes_step = G * gemv_bytes_fused(1, N_OUT, K_IN)
     value = bytes_step / (step_ms * 1e-3) / 1e9
     achieved = bytes_step / (run_avg * 1e-3) / 1e9
@@ -422,6 +425,7 @@ def main():
             "kernel": "rt::gemv_rows_kernel<1, 1>",
             "bytes_per_launch": bytes_step,
             "avg_launch_ms": round(run_avg, 5),
+            "launch_ms_dist": run_dist,
         },
         "two_launch_form": {
             "quant_kernel_avg_ms": round(quant_avg, 5),

@@ -120,10 +120,13 @@ def test_ffn_block_cfg1_bit_exact(hip, M):
         blk.load(nw, (O.pack_rotor(Wg), sg), (O.pack_rotor(Wu), su), (O.pack_rotor(Wd), sd))
         y = blk.forward(x)
         y2 = blk.forward(x)  # buffers and plans are reused
+        assert blk.launches(M) == (2 if M == 1 else 4)
+        blk.pair_ok = False  # the four-launch form gives the same bits for one token too
+        y4 = blk.forward(x)
     finally:
         gpu_layers._gpu_instance = None
     yo, it = O.ffn_block_w2a8(x, nw, Wg, sg, Wu, su, Wd, sd)
-    assert np.array_equal(y, yo) and np.array_equal(y2, yo)
+    assert np.array_equal(y, yo) and np.array_equal(y2, yo) and np.array_equal(y4, yo)
     y_ref, _ = O.ffn_block(x, nw, Wg, sg, Wu, su, Wd, sd)
     assert np.abs(y - y_ref).max() < 0.05 * max(1.0, np.abs(y_ref).max())
 

@@ -105,6 +105,8 @@ int rt_weights_upload_device(rt_ctx* ctx, const uint8_t* rotor_dev, int N, int K
 int rt_weights_download(rt_ctx* ctx, const rt_weights* w, uint8_t* rotor_host);
 
 int rt_weights_info(const rt_weights* w, int* N, int* K, float* scale);
+/* The *_free calls synchronise the device first, so objects may be freed with launches
+ * that use them still enqueued (not during stream capture); NULL is a no-op. */
 int rt_weights_free(rt_weights* w);
 
 /* Per-row (per-token) absmax int8 quantiser on x fp32 [M][K] (device):

@@ -281,6 +281,7 @@ int rt_weights_info(const rt_weights* w, int* N, int* K, float* scale) {
 int rt_weights_free(rt_weights* w) {
     if (!w) return RT_OK;
     DeviceGuard g(w->device);
+    (void)hipDeviceSynchronize();  // launches still enqueued may read the tiles
     if (w->tiles) (void)hipFree(w->tiles);
     delete w;
     return RT_OK;
@@ -424,6 +425,7 @@ int rt_linear_f32_rowscale(rt_ctx* ctx, const rt_weights* w, const float* x, int
 int rt_plan_free(rt_plan* plan) {
     if (!plan) return RT_OK;
     DeviceGuard g(plan->device);
+    (void)hipDeviceSynchronize();  // launches still enqueued may read the descriptors
     if (plan->dev_probs) (void)hipFree(plan->dev_probs);
     if (plan->dev_rb2p) (void)hipFree(plan->dev_rb2p);
     if (plan->dev_gemms) (void)hipFree(plan->dev_gemms);
@@ -692,6 +694,7 @@ int rt_act_create(rt_ctx* ctx, int M, int K, rt_act** out) {
 int rt_act_free(rt_act* act) {
     if (!act) return RT_OK;
     DeviceGuard g(act->device);
+    (void)hipDeviceSynchronize();  // launches still enqueued may read the activations
     if (act->mem) (void)hipFree(act->mem);
     delete act;
     return RT_OK;

@@ -186,9 +186,14 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmGroupArgs ga) {
     char* const lds_b = reinterpret_cast<char*>(lds);
     float* const sx_lds = reinterpret_cast<float*>(lds_b + T::SX_OFF);
 
+    // Activations hold gemm_bm(M) = 256-row padding (M > 128).  A 192-row tile can end past
+    // it: its rows there re-read the last padded row (their outputs fall outside the
+    // output buffer range and are dropped).
+    constexpr bool kClamp = 256 % BM != 0;
+    const int last_row = kClamp ? ((a.M + 255) & ~255) - 1 : 0;
     // row scales of the tile into LDS (sx holds the padded rows), published by the
     // barrier before the epilogue; column scales into registers
-    if (!a.out_i32 && t < BM) sx_lds[t] = a.sx[m0 + t];
+    if (!a.out_i32 && t < BM) sx_lds[t] = a.sx[kClamp ? min(m0 + t, last_row) : m0 + t];
     const int mrow = wm * T::WM + 4 * g, nb = n0 + wn * T::WN + r32;
     float swv[FJ];
 #pragma unroll
@@ -199,7 +204,8 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmGroupArgs ga) {
 #pragma unroll
     for (int k = 0; k < LA; ++k) {
         const int f = wave + 4 * k;  // 16-row block f
-        a_src[k] = a.qx + ((size_t)((m0 >> 4) + f) * C) * 1024 + lane * 16;  // blocked qx
+        const int blk = kClamp ? min((m0 >> 4) + f, last_row >> 4) : (m0 >> 4) + f;
+        a_src[k] = a.qx + ((size_t)blk * C) * 1024 + lane * 16;  // blocked qx
     }
     // weight row block of this wave's slot: clamped to a valid block (a wave past the
     // tile's blocks, or past N, loads data nobody reads)
@@ -479,6 +485,7 @@ static hipError_t launch_tile_cfg(int cfg, const GemmGroupArgs& ga, int tiles, h
         case kTile128x128: return launch_tile<128, 128, 2, 4>(ga, tiles, s);
         case kTile256x128: return launch_tile<256, 128, 2, 4>(ga, tiles, s);
         case kTile256x256: return launch_tile<256, 256, 2, 4>(ga, tiles, s);
+        case kTile192x128: return launch_tile<192, 128, 2, 4>(ga, tiles, s);
         // 64-row tiles do 4 MFMAs per wave per step: an 8-deep ring (64 KiB) keeps more
         // steps of loads in flight (512-token prefill 4.87 -> 4.83 ms)
         case kTile64x128: return launch_tile<64, 128, 1, 8>(ga, tiles, s);
@@ -489,12 +496,15 @@ static hipError_t launch_tile_cfg(int cfg, const GemmGroupArgs& ga, int tiles, h
 int gemm_tile_cfg(int M, const int* N, int G) {
     if (gemm_bm(M) == 128) return kTile128x128;
     const long long mt = (M + 255) / 256;
-    long long t256 = 0, t128 = 0;
+    const long long mt192 = (M + 191) / 192;
+    long long t256 = 0, t128 = 0, t192 = 0;
     for (int g = 0; g < G; ++g) {
         t256 += mt * ((N[g] + 255) / 256);
         t128 += mt * ((N[g] + 127) / 128);
+        t192 += mt192 * ((N[g] + 127) / 128);
     }
     if (t256 >= kGemmFillTiles) return kTile256x256;
+    if (t192 >= kGemm192Min && t192 <= kGemm192Max) return kTile192x128;
     if (t128 >= kGemmHalfTiles) return kTile256x128;
     return 2 * t128 >= kGemmHalfTiles ? kTile128x128 : kTile64x128;
 }
@@ -512,7 +522,7 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.M <= 0 || a.N <= 0) return hipSuccess;
     // byte offsets inside one tile's rows are 32-bit
     if ((long long)gemm_bm(a.M) * a.ldo * 4 >= (1ll << 31)) return hipErrorInvalidValue;
-    // the row tile divides gemm_bm(M), which sized the activation padding
+    // gemm_bm(M) sized the activation padding; the row tile divides it or clamps its loads
     const int bm = gemm_bm(a.M);
     if (bm == 64) {
         GemmArgs one = a;

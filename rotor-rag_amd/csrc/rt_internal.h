@@ -229,13 +229,18 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 // Tile shapes of the MFMA GEMM for M > 64 (rows x columns per workgroup).  A launch over
 // one or several problems (same M) takes 256 x 256 when that yields kGemmFillTiles tiles,
-// else 256 x 128 when that yields kGemmHalfTiles (measured: 2048 x 2560 x 6912 runs 50 us
-// as 160 tiles of 256 x 128, 57 us as 320 of 128 x 128), else 128 x 128 when that does,
-// else 64 x 128 (measured on the 512-token prefill's projections: 4.95 ms against 5.30 ms
-// with 128 x 128): a few large tiles leave most CUs idle.
-enum GemmTileCfg { kTile128x128 = 0, kTile256x128 = 1, kTile256x256 = 2, kTile64x128 = 3 };
-constexpr int kGemmFillTiles = 192, kGemmHalfTiles = 128;
-inline int gemm_tile_bm(int cfg) { return cfg == kTile64x128 ? 64 : cfg == kTile128x128 ? 128 : 256; }
+// else 192 x 128 when that yields kGemm192Min..kGemm192Max tiles (one round on the 256
+// CUs: 2048 x 2560 x 6912 as 220 tiles runs 46.3 us against 49.5 us as 160 tiles of
+// 256 x 128), else 256 x 128 when that yields kGemmHalfTiles (57 us as 320 tiles of
+// 128 x 128), else 128 x 128 when that does, else 64 x 128 (measured on the 512-token
+// prefill's projections: 4.95 ms against 5.30 ms with 128 x 128): a few large tiles leave
+// most CUs idle.  192-row tiles do not divide the activations' 256-row padding: their
+// loads of rows past it re-read the last padded block (see gemm_kernel).
+enum GemmTileCfg { kTile128x128 = 0, kTile256x128 = 1, kTile256x256 = 2, kTile64x128 = 3, kTile192x128 = 4 };
+constexpr int kGemmFillTiles = 192, kGemmHalfTiles = 128, kGemm192Min = 200, kGemm192Max = 256;
+inline int gemm_tile_bm(int cfg) {
+    return cfg == kTile64x128 ? 64 : cfg == kTile128x128 ? 128 : cfg == kTile192x128 ? 192 : 256;
+}
 inline int gemm_tile_bn(int cfg) { return cfg == kTile256x256 ? 256 : 128; }
 int gemm_tile_cfg(int M, const int* N, int G);
 long long gemm_tile_count(int cfg, int M, int N);

@@ -38,6 +38,9 @@ LINEAR_CASES = [
     (256, 6912, 2560),
     (512, 2560, 6912),
     (2048, 6912, 2560),  # cfg 3 (gate/up)
+    (2048, 2560, 6912),  # cfg 3 (down): 192-row tiles
+    (2000, 2560, 640),   # 192-row tiles, the last one past the 256-row padding
+    (200, 13824, 256),   # the same with two row tiles
 ]
 
 

@@ -44,7 +44,6 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr unsigned kLut = 0x000100FFu;  // v_perm_b32 src1: device code 0,1,2,(3) -> FF, 00, 01, 00
-constexpr int kXcds = 8;
 
 // one dword of device code (16 weights, byte b holds elements 4b..4b+3 at bits 2i) -> 16
 // int8 weights in the qx order of a 16-group: output byte 4i + b = element 4b + i
@@ -177,8 +176,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmGroupArgs ga) {
     // tile of this workgroup: the tiles of all problems in one order (each problem's
     // m-major), dealt to the XCDs in contiguous ranges; then its problem and local tile
     const int tiles = (int)gridDim.x;
-    const int L = blockIdx.x, xcd = L % kXcds, base = tiles / kXcds, rem = tiles % kXcds;
-    const int tile = xcd * base + min(xcd, rem) + L / kXcds;
+    const int tile = xcd_order((int)blockIdx.x, tiles);
     const GemmArgs a = find_gemm(ga, tile);
     const int C = a.C, Nb = a.Np / kRowBlock;
     const int nT = (a.N + BN - 1) / BN, lt = tile - a.wg_begin;

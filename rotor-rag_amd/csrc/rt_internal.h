@@ -43,6 +43,15 @@ constexpr size_t kTileSlack = 16384;
 
 inline int round_up(int a, int b) { return (a + b - 1) / b * b; }
 
+// MI355X: 8 XCDs, each with its own L2; workgroups are dealt to them round-robin by
+// blockIdx.  xcd_order maps blockIdx.x to a workgroup index such that each XCD runs one
+// contiguous range of indices (a bijection on [0, gridDim.x)).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_order(int L, int n) {
+    const int xcd = L % kXcds, base = n / kXcds, rem = n % kXcds;
+    return xcd * base + min(xcd, rem) + L / kXcds;
+}
+
 // Rotor code (per 2-bit field: high bit = bit0, low bit = bit1, w = bit0 - bit1;
 // src/rotor/core.py:99-108) <-> device code g = w + 1, 16 fields per dword at once.
 // Rotor 00 -> 01, 10 -> 10, 01 -> 00 and the reserved 11 (w = 0) -> 01; back, 01 -> 00,

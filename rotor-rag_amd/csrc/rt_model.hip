@@ -325,9 +325,14 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restri
     __shared__ float part[4][BL];
     __shared__ float pr[BL];
     __shared__ float ored[256];
-    const int h = blockIdx.x, s = blockIdx.y, S = gridDim.y, t = threadIdx.x;
+    // Workgroup (h, s) from an XCD-ordered index whose fastest part is the query head within
+    // its KV group: the G heads that read one key block run on one XCD and share its L2
+    // (decode 1.235 -> 1.218 ms/token against one workgroup per (blockIdx.x, blockIdx.y))
+    const int S = gridDim.y, Gq = H / Hkv;
+    const int w = xcd_order((int)(blockIdx.x + gridDim.x * blockIdx.y), (int)(gridDim.x * gridDim.y));
+    const int kh = w / (Gq * S), s = (w / Gq) % S, h = kh * Gq + w % Gq, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
-    const int kh = h / (H / Hkv), j0 = s * BL;
+    const int j0 = s * BL;
     // The block's keys and values do not depend on the position: their loads go out first
     // (wave w: dims [w HD/4, (w+1) HD/4) of key j0 + lane; thread (d, g): value dim d of
     // keys g, g + G, ..), together with the position's.  Keys past Lmax re-read the last

@@ -67,7 +67,8 @@ typedef struct rt_src {
  * exception text (src/rotor/gpu_layers.py:21-24). */
 const char* rt_last_error(void);
 
-/* ABI version (major*100 + minor): 101 = 100 + rt_plan_create_gate_up and RT_SRC_RMSNORM_SSQ. */
+/* ABI version (major*100 + minor): 101 = 100 + rt_plan_create_gate_up and RT_SRC_RMSNORM_SSQ;
+ * 102 = 101 + rt_plan_describe. */
 int rt_version(void);
 
 /* Number of visible HIP devices (0 when none); RT_OK even when 0. */
@@ -150,6 +151,15 @@ int rt_plan_run(rt_ctx* ctx, const rt_plan* plan);
 int rt_plan_quantize(rt_ctx* ctx, const rt_plan* plan);
 int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan);
 int rt_plan_free(rt_plan* plan);
+
+/* The launch rt_plan_gemv makes for a plan (no counterpart in the reference, which has no
+ * prepared launches; for tests and tuning): *kind = RT_LAUNCH_*, *tile_m x *tile_n = tokens x
+ * output rows per workgroup, *units = workgroups.  Any output pointer may be NULL. */
+#define RT_LAUNCH_GEMV 0        /* VALU GEMV, M <= 8 (tile_m = tokens per workgroup)      */
+#define RT_LAUNCH_GEMV_FUSED 1  /* M = 1 GEMV quantising its input row in the prologue     */
+#define RT_LAUNCH_SPLITK 2      /* int8-MFMA GEMM, 8 < M <= 64, waves split K              */
+#define RT_LAUNCH_TILES 3       /* int8-MFMA GEMM, M > 64, tile_m x tile_n workgroup tiles */
+int rt_plan_describe(const rt_plan* plan, int* kind, int* tile_m, int* tile_n, int* units);
 
 /* ---- reusable quantised activations ---------------------------------------------
  * An rt_act holds up to M tokens of K int8 activations (device layout) and their

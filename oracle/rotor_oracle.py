@@ -331,20 +331,24 @@ def causal_gqa_attention(q, K, V, pos0):
     return out.astype(np.float32)
 
 
-def bitnet_forward(params, cfg, ids, cache):
+def bitnet_forward(params, cfg, ids, cache, attn_in=None, attn_ref=None):
     """One forward of the cfg-4 model on token ids [M] at position len(cache)
     (cache: dict with per-layer K/V lists, updated in place).  Returns the final-normed
     hidden states [M, D] and the logits of the last token [V] (f64 accumulation).
 
     Layer: x += Wo(subnorm(attn(rope(Wq a), rope(Wk a), Wv a))), a = norm(x);
            x += Wd(subnorm(relu(Wg f)^2 * Wu f)), f = norm(x)  -- every linear W2A8.
+
+    attn_in (optional, per layer [M, H*hd] fp32): attention outputs to continue each layer
+    with in place of the ones computed here (teacher forcing: every other operation is
+    reproducible bit for bit, attention only to fp32 summation order); attn_ref (optional
+    list) receives the attention outputs computed here, layer by layer.
     """
     H, Hkv, eps = cfg["n_heads"], cfg["n_kv_heads"], cfg.get("rms_norm_eps", 1e-6)
     D = cfg["d_model"]
     hd = D // H
     pos0 = cache.get("len", 0)
-    emb = bf16_to_f32(params["embed"])
-    x = emb[np.asarray(ids)].astype(np.float32)
+    x = bf16_to_f32(params["embed"][np.asarray(ids)]).astype(np.float32)
     M = x.shape[0]
     table = params["rope"]
     for li, L in enumerate(params["layers"]):
@@ -359,6 +363,10 @@ def bitnet_forward(params, cfg, ids, cache):
         kv["k"] = np.concatenate([kv["k"], k.transpose(1, 0, 2)], axis=1)
         kv["v"] = np.concatenate([kv["v"], v.reshape(M, Hkv, hd).transpose(1, 0, 2)], axis=1)
         o = causal_gqa_attention(q, kv["k"], kv["v"], pos0).reshape(M, H * hd)
+        if attn_ref is not None:
+            attn_ref.append(o)
+        if attn_in is not None:
+            o = np.asarray(attn_in[li], np.float32).reshape(M, H * hd)
         on = rms_norm_f64acc(o, L["attn_sub_norm"], eps) if L.get("attn_sub_norm") is not None else o
         qo, so = quant_rows(on)
         x = x + w2a8_linear_from_q(qo, so, L["o_proj"][0], L["o_proj"][1])[0]
@@ -373,7 +381,12 @@ def bitnet_forward(params, cfg, ids, cache):
         x = x + w2a8_linear_from_q(qd, sd, L["down_proj"][0], L["down_proj"][1])[0]
     cache["len"] = pos0 + M
     hn = rms_norm_f64acc(x, params["final_norm"], eps)
-    logits = emb.astype(np.float64) @ hn[-1].astype(np.float64)
+    # the tied head in f64 (products of two f32 values are exact); the f64 copy of the
+    # embedding is made once per parameter set (2.6 GB at V = 128256, D = 2560)
+    e64 = params.get("_embed_f64")
+    if e64 is None:
+        e64 = params["_embed_f64"] = bf16_to_f32(params["embed"]).astype(np.float64)
+    logits = e64 @ hn[-1].astype(np.float64)
     return hn, logits
 
 

@@ -144,7 +144,7 @@ extern "C" {
 
 const char* rt_last_error(void) { return g_err.c_str(); }
 
-int rt_version(void) { return 101; }
+int rt_version(void) { return 102; }
 
 int rt_device_count(int* n) {
     if (!n) return fail(RT_EINVAL, "rt_device_count: n is NULL");
@@ -356,6 +356,7 @@ static bool prologue_launch(const GemvShape& base, int U, const int* Nb, int G, 
 static int launch_matrix(rt_ctx* ctx, const rt_weights* w, const int8_t* qx, const float* sx, int M,
                          const float* row_scale, void* out, bool out_i32, const float* res = nullptr) {
     if (M > kGemvMaxM) {
+        if (!gemm_ldo_ok(M, w->N)) return fail(RT_EINVAL, "N too large for the GEMM's 32-bit output offsets at this M");
         GemmArgs a{w->tiles, qx, sx, row_scale, out, w->scale, M, w->N, w->Np, w->C, w->N, out_i32 ? 1 : 0, res};
         RT_HIP(launch_gemm(a, ctx->stream));
         return RT_OK;
@@ -479,6 +480,8 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
     for (int g = 0; g < G; ++g) {
         if (!w[g] || !x[g] || !y[g]) return fail(RT_EINVAL, "rt_plan_create: NULL entry in a pointer array");
         if (w[g]->device != ctx->device) return fail(RT_EINVAL, "rt_plan_create: weights live on another device");
+        if (M > kGemvMaxM && !gemm_ldo_ok(M, w[g]->N))
+            return fail(RT_EINVAL, "rt_plan_create: N too large for the GEMM's 32-bit output offsets at this M");
     }
     DeviceGuard guard(ctx->device);
     rt_plan* p = new rt_plan();
@@ -586,6 +589,39 @@ int rt_plan_create(rt_ctx* ctx, int G, const rt_weights* const* w, const float* 
         return hip_fail(e, "rt_plan_create");
     }
     *out = p;
+    return RT_OK;
+}
+
+int rt_plan_describe(const rt_plan* plan, int* kind, int* tile_m, int* tile_n, int* units) {
+    if (!plan) return fail(RT_EINVAL, "rt_plan_describe: plan is NULL");
+    int k, tm, tn, u;
+    if (plan->dev_tile2p) {
+        k = RT_LAUNCH_TILES;
+        tm = gemm_tile_bm(plan->gemm_cfg);
+        tn = gemm_tile_bn(plan->gemm_cfg);
+        u = plan->gemm_tiles;
+    } else if (plan->dev_gemms) {
+        k = RT_LAUNCH_SPLITK;
+        tm = 64;
+        tn = kRowBlock;
+        u = plan->total_rb;
+    } else if (plan->fused || plan->run_pro) {
+        k = RT_LAUNCH_GEMV_FUSED;
+        const GemvShape sh = plan->fused ? plan->shape : plan->run_shape;
+        tm = 1;
+        tn = sh.ksplit ? kRowBlock : kRowBlock * sh.nw;
+        u = sh.ksplit ? plan->total_rb : plan->total_rb / sh.nw;
+    } else {
+        k = RT_LAUNCH_GEMV;
+        tm = plan->mt;
+        tn = plan->shape.ksplit ? kRowBlock : kRowBlock * plan->shape.nw;
+        u = (plan->shape.ksplit ? plan->total_rb : (plan->total_rb + plan->shape.nw - 1) / plan->shape.nw) *
+            ((plan->M + plan->mt - 1) / plan->mt);
+    }
+    if (kind) *kind = k;
+    if (tile_m) *tile_m = tm;
+    if (tile_n) *tile_n = tn;
+    if (units) *units = u;
     return RT_OK;
 }
 
@@ -770,6 +806,8 @@ int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_
         if (M <= 0 || M > act[g]->Mcap) return fail(RT_EINVAL, "rt_plan_create_act: M exceeds an activation capacity");
         if (w[g]->device != ctx->device || act[g]->device != ctx->device)
             return fail(RT_EINVAL, "rt_plan_create_act: operands live on another device");
+        if (M > kGemvMaxM && !gemm_ldo_ok(M, w[g]->N))
+            return fail(RT_EINVAL, "rt_plan_create_act: N too large for the GEMM's 32-bit output offsets at this M");
     }
     DeviceGuard guard(ctx->device);
     rt_plan* p = new rt_plan();

@@ -524,7 +524,7 @@ hipError_t launch_gemm_tiles(const GemmArgs* dev, const int* tile2p, int total_t
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.M <= 0 || a.N <= 0) return hipSuccess;
     // byte offsets inside one tile's rows are 32-bit
-    if ((long long)gemm_bm(a.M) * a.ldo * 4 >= (1ll << 31)) return hipErrorInvalidValue;
+    if (!gemm_ldo_ok(a.M, a.ldo)) return hipErrorInvalidValue;
     // gemm_bm(M) sized the activation padding; the row tile divides it or clamps its loads
     const int bm = gemm_bm(a.M);
     if (bm == 64) {

@@ -223,6 +223,9 @@ inline bool qx_blocked(int M) { return M > kGemvMaxM; }
 
 // rows of the GEMM workgroup tile for M tokens (the activations are zero-padded to it)
 inline int gemm_bm(int M) { return M <= 64 ? 64 : M <= 128 ? 128 : 256; }
+// The GEMM epilogues address one row tile of the output (and residual) with 32-bit byte
+// offsets and buffer ranges: a tile of gemm_bm(M) rows of ldo floats must span < 2^31 bytes.
+inline bool gemm_ldo_ok(int M, int ldo) { return (long long)gemm_bm(M) * ldo * 4 < (1ll << 31); }
 
 // Launchers (return hipSuccess or the launch error).
 hipError_t launch_relayout(const uint8_t* src, int N, int K, v4u* tiles, hipStream_t s);

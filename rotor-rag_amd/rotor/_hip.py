@@ -15,6 +15,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "librotor_hip.so"
+ABI_VERSION = 102  # rt_version() of the library this table binds
 
 class RtSrc(ctypes.Structure):
     """rt_src of include/rotor_hip.h"""
@@ -23,6 +24,7 @@ class RtSrc(ctypes.Structure):
 
 
 SRC_QUANT, SRC_RMSNORM, SRC_RELU2MUL, SRC_RELU2MUL_NORM, SRC_ATTN_NORM, SRC_RMSNORM_SSQ = 0, 2, 3, 4, 5, 6
+LAUNCH_GEMV, LAUNCH_GEMV_FUSED, LAUNCH_SPLITK, LAUNCH_TILES = 0, 1, 2, 3
 
 # name -> (restype, argtypes); every entry point of include/rotor_hip.h
 _P = ctypes.c_void_p
@@ -51,6 +53,7 @@ SIGNATURES = {
     "rt_plan_quantize": (_I, [_P, _P]),
     "rt_plan_gemv": (_I, [_P, _P]),
     "rt_plan_free": (_I, [_P]),
+    "rt_plan_describe": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I)]),
     "rt_act_create": (_I, [_P, _I, _I, ctypes.POINTER(_P)]),
     "rt_act_free": (_I, [_P]),
     "rt_act_quantize": (_I, [_P, _P, _I, _P]),
@@ -98,6 +101,9 @@ def load():
         fn = getattr(lib, name)  # AttributeError here = ABI mismatch, let it surface
         fn.restype = res
         fn.argtypes = args
+    if lib.rt_version() != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI version {lib.rt_version()}, this binding expects {ABI_VERSION} "
+                           "(rebuild the library)")
     _lib = lib
     return lib
 

@@ -46,11 +46,17 @@ def rope_table(max_len: int, head_dim: int, theta: float) -> np.ndarray:
 
 
 class KVCache:
-    """Handle to the device KV cache of a model: `length` tokens are cached."""
+    """Handle to the device KV cache of a model: `length` tokens of one sequence are cached.
 
-    def __init__(self, model: "BitNetModel", length: int):
+    The cache memory belongs to the model and holds one sequence at a time: a forward that
+    starts a new sequence (no past cache) or a generate_greedy call overwrites it, which
+    makes every older handle stale; passing a stale handle raises ValueError.  A handle of
+    the current sequence may be reused to continue (or rewind) from its length."""
+
+    def __init__(self, model: "BitNetModel", length: int, epoch: int):
         self.model = model
         self.length = length
+        self.epoch = epoch
 
     def __len__(self):
         return self.length
@@ -134,9 +140,16 @@ class BitNetModel:
             if ids.shape[0] != 1:
                 raise ValueError("batch size 1 only")
             ids = ids[0]
-        start = past_kv_cache.length if past_kv_cache is not None else 0
+        if past_kv_cache is not None:
+            if past_kv_cache.model is not self or past_kv_cache.epoch != self._dev.epoch:
+                raise ValueError("stale KV cache: the model's device cache now holds a newer sequence")
+            start = past_kv_cache.length
+        else:
+            start = 0
+            self._dev._check_ids(ids, 0)  # a rejected input leaves the cache (and its handles) as they were
+            self._dev.epoch += 1  # a new sequence overwrites the device cache
         out = self._dev.forward(ids.astype(np.int32), start, return_logits)
-        cache = KVCache(self, start + len(ids)) if use_cache else None
+        cache = KVCache(self, start + len(ids), self._dev.epoch) if use_cache else None
         if not squeeze:
             out = out[None]
         return out, cache
@@ -157,6 +170,10 @@ class _DeviceModel:
         import torch
 
         self.m = model
+        self.epoch = 0  # sequence counter of the device KV cache (see KVCache)
+        # when a dict: multi-token forwards append a device copy of every layer's attention
+        # output to trace["attn"] (for checking a forward layer by layer; off by default)
+        self.trace = None
         hip = self.hip = model.gpu
         dev = self.device = hip.device
         D, F, H, Hkv, hd = model.d_model, model.d_ff, model.n_heads, model.n_kv_heads, model.head_dim
@@ -288,6 +305,8 @@ class _DeviceModel:
                                           self.Lmax, self.pos.data_ptr()), "rt_rope_kv_append")
                 chk(lib.rt_attention(ctx, q.data_ptr(), L["kc"].data_ptr(), L["vc"].data_ptr(), o.data_ptr(), M,
                                      self.H, self.Hkv, self.hd, self.Lmax, self.pos.data_ptr()), "rt_attention")
+                if self.trace is not None:  # per-layer attention outputs of a multi-token forward
+                    self.trace.setdefault("attn", []).append(o.clone())
             if fused:
                 st["o_plan"][li].run()
                 st["gu"][li].run()
@@ -358,6 +377,7 @@ class _DeviceModel:
         import torch
 
         self._check_ids(prompt, 0)
+        self.epoch += 1  # the prompt overwrites the device cache
         P = len(prompt)
         if P + n > self.Lmax:
             raise ValueError("prompt + new tokens exceed max_seq_len")

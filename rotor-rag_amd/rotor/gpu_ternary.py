@@ -91,6 +91,13 @@ class LinearPlan:
         b._bind_stream()
         _hip.check(_hip.load().rt_plan_gemv(b.ctx, self.handle), "rt_plan_gemv")
 
+    def describe(self):
+        """(kind, tile_m, tile_n, workgroups) of the launch the plan makes (rt_plan_describe);
+        kind is one of _hip.LAUNCH_*."""
+        v = [ctypes.c_int() for _ in range(4)]
+        _hip.check(_hip.load().rt_plan_describe(self.handle, *[ctypes.byref(x) for x in v]), "rt_plan_describe")
+        return tuple(x.value for x in v)
+
     def free(self) -> None:
         if self.handle:
             _hip.load().rt_plan_free(self.handle)

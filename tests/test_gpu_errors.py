@@ -57,13 +57,23 @@ def test_weights_upload_accepts_largest_k_bound(hip, lib):
 
 
 def test_null_arguments(hip, lib):
+    import torch
+
     ctx = hip.ctx
     w = hip.upload(O.pack_rotor(np.ones((64, 64), np.int8)), 64, 1.0)
-    y = P(1 << 20)  # never dereferenced: the NULL x is rejected first
-    assert lib.rt_linear_f32(ctx, w.handle, None, 1, y) == RT_EINVAL
+    # every operand that is not the one under test is a real buffer of the right size, so a
+    # call that got past its checks would still stay in bounds
+    x = torch.zeros((1, 64), dtype=torch.float32, device="cuda")
+    q = torch.zeros((1, 64), dtype=torch.int8, device="cuda")
+    y = torch.zeros((1, 64), dtype=torch.float32, device="cuda")
+    acc = torch.zeros((1, 64), dtype=torch.int32, device="cuda")
+    assert lib.rt_linear_f32(ctx, w.handle, None, 1, y.data_ptr()) == RT_EINVAL
     assert "rt_linear_f32" in _err(lib)
-    assert lib.rt_linear_f32(None, w.handle, y, 1, y) == RT_EINVAL
-    assert lib.rt_linear_i32(ctx, None, y, 1, y) == RT_EINVAL
+    assert lib.rt_linear_f32(ctx, w.handle, x.data_ptr(), 1, None) == RT_EINVAL
+    assert lib.rt_linear_f32(None, w.handle, x.data_ptr(), 1, y.data_ptr()) == RT_EINVAL
+    assert lib.rt_linear_i32(ctx, None, q.data_ptr(), 1, acc.data_ptr()) == RT_EINVAL
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(y).item() == 0 and torch.count_nonzero(acc).item() == 0
     assert lib.rt_sync(None) == RT_EINVAL
     assert lib.rt_weights_info(None, None, None, None) == RT_EINVAL
     assert lib.rt_weights_free(None) == RT_OK  # like free(NULL)

@@ -46,7 +46,8 @@ def test_embed_exact(hip):
 # blocks, G = H / Hkv of 1, 4, 8, Lmax not a multiple of 32); the rest the general kernel
 ATTN_CASES = [(1, 0, 20, 5, 128, 64), (1, 37, 20, 5, 128, 64), (7, 3, 8, 2, 64, 64), (16, 0, 4, 4, 64, 64),
               (100, 50, 20, 5, 128, 256), (70, 0, 8, 4, 64, 128), (130, 5, 4, 4, 64, 192), (33, 20, 6, 2, 64, 64),
-              (40, 10, 8, 8, 128, 128), (50, 0, 16, 2, 128, 68), (200, 300, 20, 5, 128, 520)]
+              (40, 10, 8, 8, 128, 128), (50, 0, 16, 2, 128, 68), (200, 300, 20, 5, 128, 520),
+              (130, 0, 4, 2, 128, 192), (20, 0, 4, 2, 128, 192), (130, 0, 8, 2, 64, 192)]
 
 
 @pytest.mark.parametrize("M,pos0,H,Hkv,hd,Lmax", ATTN_CASES)
@@ -206,9 +207,10 @@ def test_lm_head_argmax(hip, V, D):
     np.testing.assert_allclose(lg, ref, atol=1e-3 * np.abs(ref).max(), rtol=1e-4)
 
 
-def _write_checkpoint(path, params, cfg, max_len):
+def _state_dict(params):
+    """The reference's checkpoint tensor names (src/rotor/bitnet_model.py:100-188) -> torch
+    tensors of the oracle parameters (rotor bytes, per-tensor scales, bf16 embedding)."""
     import torch
-    from safetensors.torch import save_file
 
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a))
     st = {"model.embed_tokens.weight": t(params["embed"].view(np.int16)).view(torch.bfloat16),
@@ -224,7 +226,13 @@ def _write_checkpoint(path, params, cfg, max_len):
             W, s = L[name]
             st[f"{p}.{grp}.{name}.weight"] = t(O.pack_rotor(W))
             st[f"{p}.{grp}.{name}.weight_scale"] = t(np.array([s], np.float32))
-    save_file(st, str(path / "model.safetensors"))
+    return st
+
+
+def _write_checkpoint(path, params, cfg, max_len):
+    from safetensors.torch import save_file
+
+    save_file(_state_dict(params), str(path / "model.safetensors"))
     hf = {"vocab_size": cfg["vocab_size"], "hidden_size": cfg["d_model"], "num_hidden_layers": cfg["n_layers"],
           "num_attention_heads": cfg["n_heads"], "num_key_value_heads": cfg["n_kv_heads"],
           "intermediate_size": cfg["d_ff"], "rope_theta": cfg["rope_theta"], "rms_norm_eps": 1e-6,
@@ -293,3 +301,168 @@ def test_model_rejects_bad_input(small_model):
         model.forward(np.array([1000], np.int32))  # id out of range
     with pytest.raises(ValueError):
         model.generate_greedy(np.zeros(60, np.int32), 10)  # exceeds max_seq_len
+
+
+def test_stale_kv_cache_rejected(small_model):
+    """The device cache holds one sequence: a handle from before a new sequence (a forward
+    without past cache, or generate_greedy) is refused; a current one continues."""
+    model, _ = small_model
+    _, c1 = model.forward(np.array([1, 2, 3], np.int32), use_cache=True)
+    _, c2 = model.forward(np.array([4], np.int32), past_kv_cache=c1, use_cache=True)
+    _, c3 = model.forward(np.array([5], np.int32), past_kv_cache=c2, use_cache=True)
+    assert len(c3) == 5
+    with pytest.raises(ValueError):  # rejected ids: the cache and its handles stay valid
+        model.forward(np.array([SMALL["vocab_size"]], np.int32), use_cache=True)
+    model.forward(np.array([6], np.int32), past_kv_cache=c3)
+    model.forward(np.array([7, 8], np.int32), use_cache=True)  # a new sequence
+    with pytest.raises(ValueError, match="stale"):
+        model.forward(np.array([6], np.int32), past_kv_cache=c3)
+    _, d1 = model.forward(np.array([7], np.int32), use_cache=True)
+    model.generate_greedy(np.array([1, 2], np.int32), 2)
+    with pytest.raises(ValueError, match="stale"):
+        model.forward(np.array([6], np.int32), past_kv_cache=d1)
+
+
+# ---- prompts longer than the GEMV's 8 tokens: the prefill runs the quantiser launches, the
+# grouped split-K / tile GEMM plans, residual-aliased linears and rt_attention (the MFMA
+# prefill kernel for head_dim 128) -------------------------------------------------------
+HD128 = dict(vocab_size=1000, d_model=512, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=1024, rope_theta=500000.0)
+
+
+def _prefill_vs_oracle(model, params, cfg, ids):
+    """A multi-token forward checked layer by layer.  Every operation of a layer is
+    reproducible bit for bit except attention, which sums in fp32 where the oracle sums in
+    f64; a last-ulp difference there can flip one int8 value of the next quantisation and
+    from then on every element differs a little.  So the oracle runs teacher-forced: each
+    layer continues from the GPU's own attention output, which must be within 2e-5 of the
+    oracle's attention on the same (bit-exact) q, k, v; the final hidden states must then
+    equal the oracle's bit for bit.  Returns (hn, cache, oracle cache, oracle last logits)."""
+    model._dev.trace = {}
+    try:
+        hn, cache = model.forward(ids, return_logits=False, use_cache=True)
+    finally:
+        trace, model._dev.trace = model._dev.trace, None
+    attn = [a.cpu().numpy() for a in trace["attn"]]
+    assert len(attn) == cfg["n_layers"]
+    oc, ref = {}, []
+    hn_o, logits_o = O.bitnet_forward(params, cfg, ids, oc, attn_in=attn, attn_ref=ref)
+    for li, (a, r) in enumerate(zip(attn, ref)):
+        np.testing.assert_allclose(a, r, atol=2e-5, rtol=1e-4, err_msg=f"attention of layer {li}")
+    assert hn.shape == hn_o.shape == (len(ids), cfg["d_model"])
+    assert np.array_equal(hn, hn_o), f"max |diff| {np.abs(hn - hn_o).max()}"
+    return hn, cache, oc, logits_o
+
+
+LONG_CFGS = {"small_hd64": SMALL, "hd128": HD128}
+
+
+def _device_model(hip, params, cfg, max_len, max_tokens=512):
+    from rotor import gpu_layers
+    from rotor.bitnet_model import BitNetModel
+
+    conf = dict(cfg, rms_norm_eps=1e-6, max_seq_len=max_len, max_batch_tokens=max_tokens)
+    gpu_layers._gpu_instance = hip
+    try:
+        model = BitNetModel(conf, use_gpu=True)
+        model.load_state(_state_dict(params))
+    finally:
+        gpu_layers._gpu_instance = None
+    return model
+
+
+@pytest.fixture(scope="module")
+def long_models(hip):
+    out = {}
+    for name, cfg in LONG_CFGS.items():
+        params = O.make_bitnet_params(23 + len(name), cfg, 192)
+        out[name] = (_device_model(hip, params, cfg, 192), params, cfg)
+    return out
+
+
+@pytest.mark.parametrize("name", list(LONG_CFGS))
+@pytest.mark.parametrize("P", [20, 130])
+def test_long_prompt_forward_matches_oracle(long_models, name, P):
+    model, params, cfg = long_models[name]
+    ids = np.random.default_rng(P).integers(0, cfg["vocab_size"], P).astype(np.int32)
+    hn, cache, oc, _ = _prefill_vs_oracle(model, params, cfg, ids)
+    # a decode step after the long prefill (fused decode plans + LM head kernel)
+    logits, cache = model.forward(np.array([42], np.int32), past_kv_cache=cache, use_cache=True)
+    _, logits_o = O.bitnet_forward(params, cfg, [42], oc)
+    np.testing.assert_allclose(logits[0], logits_o, atol=0.05 * np.abs(logits_o).max(), rtol=0)
+    assert len(cache) == P + 1
+
+
+@pytest.mark.parametrize("name", list(LONG_CFGS))
+def test_long_prompt_greedy_matches_oracle(long_models, name):
+    model, params, cfg = long_models[name]
+    prompt = np.random.default_rng(5).integers(0, cfg["vocab_size"], 130).astype(np.int32)
+    n = 8
+    toks, ref, gaps = _greedy_vs_oracle(model, params, cfg, prompt, n)
+    for i in range(n):
+        if gaps[i] < 0.05:
+            break
+        assert toks[i] == ref[i], f"step {i}: {toks[i]} != {ref[i]} (gap {gaps[i]:.3f})"
+    assert i >= 3, "oracle gaps too small to compare"
+
+
+def _greedy_vs_oracle(model, params, cfg, prompt, n):
+    """generate_greedy (prefill, then graph-replayed decode steps) beside the oracle's greedy
+    protocol (src/rotor/generation.py:244-279: argmax, one token per step), the oracle's
+    prefill teacher-forced on the GPU prefill's attention outputs (see _prefill_vs_oracle).
+    Returns (GPU tokens, oracle tokens, oracle top-2 gaps)."""
+    model._dev.trace = {}
+    try:
+        toks = model.generate_greedy(prompt, n, graph=True)
+    finally:
+        trace, model._dev.trace = model._dev.trace, None
+    attn = [a.cpu().numpy() for a in trace["attn"]]
+    oc = {}
+    _, lg = O.bitnet_forward(params, cfg, prompt, oc, attn_in=attn)
+    ref, gaps = [], []
+    for i in range(n):
+        srt = np.sort(lg)
+        ref.append(int(np.argmax(lg)))
+        gaps.append(float(srt[-1] - srt[-2]))
+        if i + 1 < n:
+            _, lg = O.bitnet_forward(params, cfg, [ref[-1]], oc)
+    return toks, ref, gaps
+
+
+# ---- cfg 4 at its own widths: hidden 2560, ffn 6912, 20 / 5 heads x 128, vocab 128256,
+# RoPE theta 500000, bf16 tied head; two layers (the oracle's time), a 400-token prompt so
+# that the prefill runs the grouped tile GEMMs including the 256 x 128 tile (gate/up at
+# 384 < M <= 512), then graph-replayed greedy decode steps -------------------------------
+CFG4_WIDE = dict(vocab_size=128256, d_model=2560, n_layers=2, n_heads=20, n_kv_heads=5, d_ff=6912,
+                 rope_theta=500000.0)
+
+
+@pytest.mark.timeout(600)
+def test_cfg4_full_width_matches_oracle(hip):
+    """The reference path this replaces: BitNetModel.forward (src/rotor/bitnet_model.py:190-244)
+    driven by TextGenerator's greedy protocol (src/rotor/generation.py:244-279)."""
+    cfg, P, n, Lmax = CFG4_WIDE, 400, 6, 512
+    params = O.make_bitnet_params(4, cfg, Lmax)
+    model = _device_model(hip, params, cfg, Lmax)
+    prompt = np.random.default_rng(4).integers(0, cfg["vocab_size"], P).astype(np.int32)
+    # the prefill's gate/up plan is the 256 x 128 tile launch
+    st = model._dev._state(P)
+    assert st["gu"][0].describe() == (3, 256, 128, 216)
+    # prefill hidden states, then one decode step through the fused LM head over 128256 rows
+    hn, cache, oc, logits_o = _prefill_vs_oracle(model, params, cfg, prompt)
+    t0 = int(np.argmax(logits_o))
+    logits, _ = model.forward(np.array([t0], np.int32), past_kv_cache=cache, use_cache=True)
+    _, logits1_o = O.bitnet_forward(params, cfg, [t0], oc)
+    err = float(np.abs(logits[0] - logits1_o).max())
+    assert err <= 0.02 * np.abs(logits1_o).max(), err
+    # greedy decode: prefill + (n - 1) graph replays, tokens equal wherever the oracle's top-2
+    # gap exceeds four times the logit deviation just measured
+    toks, ref, gaps = _greedy_vs_oracle(model, params, cfg, prompt, n)
+    assert ref[0] == t0
+    tol = max(0.05, 4 * err)
+    compared = 0
+    for i in range(n):
+        if gaps[i] < tol:
+            break
+        assert toks[i] == ref[i], f"step {i}: {toks[i]} != {ref[i]} (gap {gaps[i]:.3f}, tol {tol:.3f})"
+        compared += 1
+    assert compared >= 4, f"only {compared} steps had a top-2 gap above {tol:.3f}: {gaps}"

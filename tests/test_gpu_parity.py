@@ -160,11 +160,17 @@ def test_ternary_matmul_duck_type(hip):
     assert y.shape == (300,)
 
 
+# launch each plan of test_plan_matches_single_calls makes: (kind, tile_m, tile_n, workgroups)
+# (two distinct inputs at M = 1: the GEMV runs after a quantiser launch, 16-wave K split)
+PLAN_LAUNCH = {1: (0, 1, 64, 100), 16: (2, 64, 64, 100), 37: (2, 64, 64, 100), 64: (2, 64, 64, 100),
+               130: (3, 64, 128, 150), 300: (3, 128, 128, 150), 600: (3, 192, 128, 200)}
+
+
 @pytest.mark.parametrize("M", [1, 16, 37, 64, 130, 300, 600])
 def test_plan_matches_single_calls(hip, M):
     """A plan launches its problems together: one grid over all row blocks for M <= 64, one
-    grid over all tiles above (M = 300: 128 x 128 tiles, M = 600: 256 x 128, while the
-    single calls pick their own shapes)."""
+    grid over all tiles above (M = 130: 64 x 128 tiles, M = 300: 128 x 128, M = 600: 192 x 128,
+    as rt_plan_describe reports), while the single calls pick their own shapes."""
     import torch
 
     rng = np.random.default_rng(12 + M)
@@ -178,11 +184,61 @@ def test_plan_matches_single_calls(hip, M):
         xs.append(x)
         ys.append(torch.empty((M, N), dtype=torch.float32, device="cuda"))
     plan = hip.plan(ws, xs, ys)
+    assert plan.describe() == PLAN_LAUNCH[M]
     for _ in range(2):  # replays give the same answer
         plan.run()
         torch.cuda.synchronize()
         for w, x, y in zip(ws, xs, ys):
             assert torch.equal(y, hip.linear_device(w, x))
+
+
+# Tile-GEMM plans (M > 64) and the tile shape each must take, checked bit-exact against the
+# oracle problem by problem: name -> (M, [(N, K, input index)], (tile_m, tile_n, tiles)).
+TILE_PLANS = {
+    # the 512-token prefill's gate/up (two 6912-row problems sharing x): 256 x 128 tiles
+    "gate_up_m512": (512, [(6912, 2560, 0), (6912, 2560, 0)], (256, 128, 216)),
+    # one 13824-row problem at 384 < M <= 512: 256 x 128 as well
+    "wide_m400": (400, [(13824, 2560, 0)], (256, 128, 216)),
+    # the 512-token prefill's q/k/v and down: 64 x 128 tiles
+    "qkv_m512": (512, [(2560, 2560, 0), (640, 2560, 0), (640, 2560, 0)], (64, 128, 240)),
+    "down_m512": (512, [(2560, 6912, 0)], (64, 128, 160)),
+    # cfg 3: 256 x 256 (gate/up) and 192 x 128 (down) tiles
+    "cfg3_gate_up": (2048, [(6912, 2560, 0)], (256, 256, 216)),
+    "cfg3_down": (2048, [(2560, 6912, 0)], (192, 128, 220)),
+    # M = 100 (128-row activation padding): 128 x 128
+    "m100": (100, [(2560, 2560, 0), (640, 2560, 1)], (128, 128, 25)),
+}
+
+
+@pytest.mark.parametrize("name", list(TILE_PLANS))
+def test_tile_plan_shapes_vs_oracle(hip, name):
+    import torch
+
+    M, shapes, (tm, tn, tiles) = TILE_PLANS[name]
+    rng = np.random.default_rng(sum(map(ord, name)))
+    inputs = {}
+    ws, xs, ys, Ws = [], [], [], []
+    for N, K, xi in shapes:
+        if xi not in inputs:
+            inputs[xi] = rng.standard_normal((M, K), dtype=np.float32)
+        W, scale = O.make_ternary(rng, N, K)
+        Ws.append((W, scale))
+        ws.append(hip.upload(O.pack_rotor(W), K, scale))
+        xs.append(torch.from_numpy(inputs[xi]).cuda())
+        ys.append(torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda"))
+    # problems sharing an input must share the tensor (one quantisation)
+    by_idx = {}
+    xs = [by_idx.setdefault(xi, x) for (_, _, xi), x in zip(shapes, xs)]
+    plan = hip.plan(ws, xs, ys)
+    from rotor import _hip as H_
+
+    assert plan.describe() == (H_.LAUNCH_TILES, tm, tn, tiles)
+    plan.run()
+    torch.cuda.synchronize()
+    for (W, scale), (_, _, xi), y in zip(Ws, shapes, ys):
+        y_ref, q, s, acc = O.ternary_linear(inputs[xi], W, scale)
+        y_exact = (acc.astype(np.float32) * s[:, None]) * np.float32(scale)
+        assert np.array_equal(y.cpu().numpy(), y_exact)
 
 
 # M = 1 plans whose one launch quantises in the GEMV prologue: (N, K) per problem.

@@ -328,6 +328,33 @@ def test_rope_properties():
     assert abs(a - b) < 1e-4
 
 
+@pytest.mark.parametrize("hd,theta", [(128, 500000.0), (64, 10000.0), (8, 10000.0)])
+def test_rope_frequency_kat(hd, theta):
+    """Known answer for the frequencies (which the invariants above leave free): at position
+    p, pair i of the rotate-half layout (dims i and i + hd/2) turns by exactly
+    p * theta^(-2i/hd) radians.  The angles here come from exp/log in float64, not from the
+    power the table uses, and the rotation is applied to unit vectors, so a wrong exponent
+    (i/hd, 2i/(hd/2), a dropped minus) or a swapped cos/sin fails."""
+    from rotor.bitnet_model import rope_table as product_table
+
+    tab = O.rope_table(8, hd, theta)
+    i = np.arange(hd // 2)
+    for p in (1, 3, 7):
+        ang = p * np.exp(-(2.0 * i / hd) * np.log(theta))
+        np.testing.assert_allclose(tab[p, :, 0], np.cos(ang), rtol=0, atol=1e-7)
+        np.testing.assert_allclose(tab[p, :, 1], np.sin(ang), rtol=0, atol=1e-7)
+        # e_i (first half) rotates to (cos, sin) in dims (i, i + hd/2)
+        x = np.zeros((1, 1, hd), np.float32)
+        x[0, 0, 1] = 1.0
+        r = O.apply_rope(x, tab, p)[0, 0]
+        assert abs(r[1] - np.cos(ang[1])) < 1e-6 and abs(r[1 + hd // 2] - np.sin(ang[1])) < 1e-6
+    # pair 0 turns by exactly p radians, the last pair by p * theta^(-(hd-2)/hd)
+    assert abs(np.arctan2(tab[1, 0, 1], tab[1, 0, 0]) - 1.0) < 1e-7
+    assert abs(np.arctan2(tab[1, -1, 1], tab[1, -1, 0]) - theta ** (-(hd - 2) / hd)) < 1e-7
+    # the table the product uploads is the same
+    assert np.array_equal(product_table(8, hd, theta), tab)
+
+
 def test_attention_closed_forms():
     rng = np.random.default_rng(1)
     hd = 8

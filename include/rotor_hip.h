@@ -68,7 +68,7 @@ typedef struct rt_src {
 const char* rt_last_error(void);
 
 /* ABI version (major*100 + minor): 101 = 100 + rt_plan_create_gate_up and RT_SRC_RMSNORM_SSQ;
- * 102 = 101 + rt_plan_describe. */
+ * 102 = 101 + rt_plan_describe; 103 = 102 + rt_linear_f32_noalloc. */
 int rt_version(void);
 
 /* Number of visible HIP devices (0 when none); RT_OK even when 0. */
@@ -126,6 +126,20 @@ int rt_linear_i32(rt_ctx* ctx, const rt_weights* w, const int8_t* q, int M, int3
  * Replaces TernaryLinear.forward (src/rotor/transformer.py:111-155; the op at :150)
  * and, per token, GPUTernaryOps.ternary_matmul (src/rotor/gpu_ternary.py:138-202). */
 int rt_linear_f32(rt_ctx* ctx, const rt_weights* w, const float* x, int M, float* y);
+
+/* rt_linear_f32 without any device allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Results equal rt_linear_f32's bit for bit.  Where
+ * rt_linear_f32 stages the quantised activations in the context's buffer (allocated and
+ * grown on demand), this entry point stages them in a static device buffer of
+ * RT_NOALLOC_SCRATCH_BYTES (16 MiB) that every device holds from the library's load until
+ * the process ends; M = 1 needs none (one launch quantises in the GEMV prologue).  Inputs
+ * whose staged activations, Mpad * round_up(K, 64) + 4 * Mpad bytes (Mpad = M rounded up to
+ * the GEMV token group or GEMM tile: 2048 x 6912 fits), exceed the buffer are rejected with
+ * RT_EINVAL.  All calls on one device share its buffer: calls that overlap on one GPU (two
+ * streams, two host threads) race, so the caller serialises them. */
+#define RT_NOALLOC_SCRATCH_BYTES (16u << 20)
+int rt_linear_f32_noalloc(rt_ctx* ctx, const rt_weights* w, const float* x, int M, float* y);
 
 /* As rt_linear_f32 with a per-output-row scale vector row_scale fp32 [N] (device)
  * in place of s_w: y[m][n] = ((float)acc * s_x[m]) * row_scale[n].  This is the

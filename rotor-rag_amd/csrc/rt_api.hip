@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -83,10 +84,43 @@ struct Scratch {
 
 }  // namespace
 
+// ---- static scratch of the allocation-free entry point ----------------------------------
+// rt_linear_f32_noalloc stages its quantised activations here instead of in a context's
+// growing buffer, for callers that cannot allocate.  Every device holds its own copy from
+// the module load until the process ends.  In host code `scratch` is only a stand-in
+// symbol, not a device address: the address is resolved per device with
+// hipGetSymbolAddress (device current) and only that pointer is used.
+static_assert(RT_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size");
+static __device__ __align__(256) unsigned char scratch[RT_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+// The device address of `scratch` on the current device `dev`, resolved once per device.
+hipError_t noalloc_scratch(int dev, void** out) {
+    static std::mutex mu;
+    static void* addr[kMaxDevices] = {};
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return hipSuccess;
+}
+
+}  // namespace
+
 struct rt_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     Scratch act;  // qx [Mpad][Kp] followed by sx [Mpad]
+    int8_t* noalloc = nullptr;  // this device's `scratch` (rt_linear_f32_noalloc)
 };
 
 struct rt_weights {
@@ -144,7 +178,7 @@ extern "C" {
 
 const char* rt_last_error(void) { return g_err.c_str(); }
 
-int rt_version(void) { return 102; }
+int rt_version(void) { return 103; }
 
 int rt_device_count(int* n) {
     if (!n) return fail(RT_EINVAL, "rt_device_count: n is NULL");
@@ -166,8 +200,11 @@ int rt_ctx_create(int device, rt_ctx** out) {
         return fail(RT_ENODEV, std::string("rt_ctx_create: device is ") + prop.gcnArchName +
                                    ", this library is built for gfx950 only");
     RT_HIP(hipSetDevice(device));
+    void* sp = nullptr;
+    RT_HIP(noalloc_scratch(device, &sp));
     rt_ctx* c = new rt_ctx();
     c->device = device;
+    c->noalloc = static_cast<int8_t*>(sp);
     *out = c;
     return RT_OK;
 }
@@ -375,6 +412,26 @@ static int launch_matrix(rt_ctx* ctx, const rt_weights* w, const int8_t* qx, con
     return RT_OK;
 }
 
+// M = 1 over fp32 x: ONE launch whose GEMV quantises x in its prologue, when the row fits
+// the prologue's LDS (*launched = false otherwise; nothing is enqueued then).
+static int linear_m1_prologue(rt_ctx* ctx, const rt_weights* w, const float* x, const float* row_scale, void* out,
+                              bool* launched) {
+    GemvArgs a{};
+    a.G = 1;
+    a.M = 1;
+    a.total_rb = w->Np / kRowBlock;
+    a.p = GemvProb{w->tiles, nullptr, nullptr, row_scale, out, w->scale, w->N, w->C, w->N, 0, nullptr, x, w->K};
+    const QuantProb src{x, nullptr, nullptr, nullptr, nullptr, w->K, w->Kp, kQuant, nullptr, 0.0f, nullptr,
+                        nullptr, 0, 0, 0};
+    const int nb = a.total_rb;
+    GemvShape shape;
+    *launched = false;
+    if (!prologue_launch(gemv_shape(a.total_rb, 1, w->C), 1, &nb, 1, w->Kp, src, &a, &shape)) return RT_OK;
+    RT_HIP(launch_gemv(a, 1, shape, ctx->stream));
+    *launched = true;
+    return RT_OK;
+}
+
 static int run_linear(rt_ctx* ctx, const rt_weights* w, const float* x, const int8_t* q, int M,
                       const float* row_scale, void* out, bool out_i32, const char* who) {
     if (!w) return fail(RT_EINVAL, std::string(who) + ": weights are NULL");
@@ -384,19 +441,9 @@ static int run_linear(rt_ctx* ctx, const rt_weights* w, const float* x, const in
     if (w->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": weights live on another device");
     DeviceGuard g(ctx->device);
     if (M == 1 && x && !out_i32) {  // one launch: the GEMV quantises x in its prologue
-        GemvArgs a{};
-        a.G = 1;
-        a.M = 1;
-        a.total_rb = w->Np / kRowBlock;
-        a.p = GemvProb{w->tiles, nullptr, nullptr, row_scale, out, w->scale, w->N, w->C, w->N, 0, nullptr, x, w->K};
-        const QuantProb src{x, nullptr, nullptr, nullptr, nullptr, w->K, w->Kp, kQuant, nullptr, 0.0f, nullptr,
-                            nullptr, 0, 0, 0};
-        const int nb = a.total_rb;
-        GemvShape shape;
-        if (prologue_launch(gemv_shape(a.total_rb, 1, w->C), 1, &nb, 1, w->Kp, src, &a, &shape)) {
-            RT_HIP(launch_gemv(a, 1, shape, ctx->stream));
-            return RT_OK;
-        }
+        bool launched = false;
+        rc = linear_m1_prologue(ctx, w, x, row_scale, out, &launched);
+        if (rc || launched) return rc;
     }
     int8_t* qx;
     float* sx;
@@ -413,6 +460,41 @@ int rt_linear_i32(rt_ctx* ctx, const rt_weights* w, const int8_t* q, int M, int3
 int rt_linear_f32(rt_ctx* ctx, const rt_weights* w, const float* x, int M, float* y) {
     if (!x) return fail(RT_EINVAL, "rt_linear_f32: x is NULL");
     return run_linear(ctx, w, x, nullptr, M, nullptr, y, false, "rt_linear_f32");
+}
+
+int rt_linear_f32_noalloc(rt_ctx* ctx, const rt_weights* w, const float* x, int M, float* y) {
+    const char* who = "rt_linear_f32_noalloc";
+    if (!w) return fail(RT_EINVAL, std::string(who) + ": weights are NULL");
+    int rc = check_act(ctx, M, w->K, who);
+    if (rc) return rc;
+    if (!x || !y) return fail(RT_EINVAL, std::string(who) + ": NULL pointer");
+    if (w->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": weights live on another device");
+    if (!ctx->noalloc) return fail(RT_EINVAL, std::string(who) + ": the context has no static scratch");
+    DeviceGuard g(ctx->device);
+    if (M == 1) {
+        bool launched = false;
+        rc = linear_m1_prologue(ctx, w, x, nullptr, y, &launched);
+        if (rc || launched) return rc;
+    }
+    // the activations of the GEMV / GEMM tile rows: int8 [Mpad][Kp], then fp32 scales [Mpad];
+    // the quantiser writes every byte of both (padding rows as zeros), so what an earlier call
+    // left in the buffer is never read
+    const int Mpad = act_rows(M);
+    const size_t qbytes = (size_t)Mpad * w->Kp, need = qbytes + (size_t)Mpad * sizeof(float);
+    if (need > RT_NOALLOC_SCRATCH_BYTES)
+        return fail(RT_EINVAL, std::string(who) + ": M = " + std::to_string(M) + ", K = " + std::to_string(w->K) +
+                                   " needs " + std::to_string(need) + " bytes of activation scratch, more than the " +
+                                   std::to_string(RT_NOALLOC_SCRATCH_BYTES) + " of the static buffer");
+    int8_t* qx = ctx->noalloc;
+    float* sx = reinterpret_cast<float*>(ctx->noalloc + qbytes);
+    QuantArgs a{};
+    a.U = 1;
+    a.M = M;
+    a.Mpad = Mpad;
+    a.p = QuantProb{x, nullptr, qx, sx, nullptr, w->K, w->Kp, kQuant, nullptr, 0.0f, nullptr, nullptr, 0, 0,
+                    qx_blocked(M)};
+    RT_HIP(launch_quant(a, ctx->stream, quant_rows_ok(a.p) ? w->K : 0));
+    return launch_matrix(ctx, w, qx, sx, M, nullptr, y, false);
 }
 
 int rt_linear_f32_rowscale(rt_ctx* ctx, const rt_weights* w, const float* x, int M, const float* row_scale,

@@ -15,7 +15,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "librotor_hip.so"
-ABI_VERSION = 102  # rt_version() of the library this table binds
+ABI_VERSION = 103  # rt_version() of the library this table binds
 
 class RtSrc(ctypes.Structure):
     """rt_src of include/rotor_hip.h"""
@@ -47,6 +47,7 @@ SIGNATURES = {
     "rt_linear_i32": (_I, [_P, _P, _P, _I, _P]),
     "rt_linear_f32": (_I, [_P, _P, _P, _I, _P]),
     "rt_linear_f32_rowscale": (_I, [_P, _P, _P, _I, _P, _P]),
+    "rt_linear_f32_noalloc": (_I, [_P, _P, _P, _I, _P]),
     "rt_plan_create": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(_P), _I, ctypes.POINTER(_P),
                             ctypes.POINTER(_P)]),
     "rt_plan_run": (_I, [_P, _P]),

@@ -111,6 +111,62 @@ def test_live_reference_core_if_built():
         assert np.array_equal(b0, o0) and np.array_equal(b1, o1)
 
 
+def _cpubase():
+    p = ROOT / "oracle" / "libcpubase.so"
+    if not p.exists():
+        pytest.skip("oracle/libcpubase.so not built (make -C oracle)")
+    lib = ctypes.CDLL(str(p))
+    sz, vp = ctypes.c_size_t, ctypes.c_void_p
+    lib.cb_unpack_planes.argtypes = [vp, vp, sz, sz, vp]
+    lib.cb_unpack_planes.restype = None
+    lib.cb_sign_matvec.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
+    lib.cb_sign_matvec.restype = None
+    return lib
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (3, 7), (11, 129), (65, 640), (4, 2560)])
+def test_cpu_baseline_unpack_planes(rows, cols):
+    """The timed CPU baseline's unpack equals the oracle's rotor_unpack_weights (and so the
+    reference core's, which the oracle is pinned to)."""
+    lib = _cpubase()
+    rng = np.random.default_rng(rows * cols)
+    W = rng.choice(np.array([-1, 0, 1], np.int8), size=(rows, cols))
+    b0, b1 = O.bitnet_to_rotor(O.pack_rotor(W), cols)
+    out = np.zeros((rows, cols), np.int8)
+    lib.cb_unpack_planes(b0.ctypes.data, b1.ctypes.data, rows, cols, out.ctypes.data)
+    assert np.array_equal(out, W)
+    assert np.array_equal(out, O.rotor_unpack_weights(b0, b1, rows, cols))
+
+
+@pytest.mark.parametrize("m,n", [(1, 1), (5, 33), (64, 2560), (7, 8160)])
+def test_cpu_baseline_sign_matvec(m, n):
+    """The 1-bit-activation mat-vec of the reference core (rotor_matvec): y = W sign(x),
+    brute force, with zeros in x mapping to 0; equal to the reference core's own output when
+    oracle/_ref is built (n <= 8160 keeps its 8-bit lane sums exact)."""
+    lib = _cpubase()
+    rng = np.random.default_rng(m + n)
+    W = rng.choice(np.array([-1, 0, 1], np.int8), size=(m, n))
+    x = rng.standard_normal(n).astype(np.float32)
+    x[::7] = 0.0
+    wb0, wb1 = (W == 1).astype(np.uint8), (W == -1).astype(np.uint8)
+    y = np.zeros(m, np.int32)
+    s0, s1 = np.zeros(n, np.uint8), np.zeros(n, np.uint8)
+    lib.cb_sign_matvec(wb0.ctypes.data, wb1.ctypes.data, x.ctypes.data, m, n, s0.ctypes.data, s1.ctypes.data,
+                       y.ctypes.data)
+    brute = [sum(int(W[i, k]) * (1 if x[k] > 0 else -1 if x[k] < 0 else 0) for k in range(n)) for i in range(min(m, 3))]
+    assert y[:len(brute)].tolist() == brute
+    assert np.array_equal(y, W.astype(np.int64) @ np.sign(x).astype(np.int64))
+    ref = ROOT / "oracle" / "_ref" / "librotor_core.so"
+    if ref.exists():
+        rl = ctypes.CDLL(str(ref))
+        sz, vp = ctypes.c_size_t, ctypes.c_void_p
+        rl.rotor_matvec.argtypes = [vp, vp, vp, sz, sz, vp]
+        rl.rotor_matvec.restype = None
+        yr = np.zeros(m, np.int32)
+        rl.rotor_matvec(wb0.ctypes.data, wb1.ctypes.data, x.ctypes.data, m, n, yr.ctypes.data)
+        assert np.array_equal(y, yr)
+
+
 # ---------------------------------------------------------------- quantiser
 
 

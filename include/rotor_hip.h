@@ -53,6 +53,12 @@ typedef struct rt_act rt_act;         /* reusable quantised activations        *
 #define RT_SRC_RMSNORM_SSQ 6    /* as RT_SRC_RMSNORM, with sum_k x^2 given as K/32 f64 partial
                                    sums: aux2 = (const float*) the `ssq` array written by an
                                    rt_plan_create_gate_up plan (K % 64 == 0, K <= 8192) */
+#define RT_SRC_RMSNORM_STATS 7  /* as RT_SRC_RMSNORM, with the row's statistics given: aux2 =
+                                   (const float*) the RT_ROWSTAT_BYTES * K / 32 bytes written by
+                                   the plan that produced x (rt_plan_set_row_stats); the decode
+                                   GEMV then needs no workgroup-wide reduction (K % 64 == 0,
+                                   K <= 8192, 16-byte aligned x, aux and records) */
+#define RT_ROWSTAT_BYTES 32     /* statistics of 32 consecutive row elements */
 typedef struct rt_src {
     int mode;           /* RT_SRC_*                                  */
     const float* x;     /* fp32 [K] (device); partials for ATTN_NORM */
@@ -68,7 +74,8 @@ typedef struct rt_src {
 const char* rt_last_error(void);
 
 /* ABI version (major*100 + minor): 101 = 100 + rt_plan_create_gate_up and RT_SRC_RMSNORM_SSQ;
- * 102 = 101 + rt_plan_describe; 103 = 102 + rt_linear_f32_noalloc. */
+ * 102 = 101 + rt_plan_describe; 103 = 102 + rt_linear_f32_noalloc; 104 = 103 + rt_plan_set_row_stats
+ * and RT_SRC_RMSNORM_STATS. */
 int rt_version(void);
 
 /* Number of visible HIP devices (0 when none); RT_OK even when 0. */
@@ -241,6 +248,17 @@ int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const r
  * relu^2 in the BitNet configuration) into the projections that produce its inputs. */
 int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, float s_up, const rt_src* src,
                            float* a, double* ssq, float* g_out, float* u_out, rt_plan** out);
+
+/* Let a one-problem fused decode plan (rt_plan_create_fused with G = 1, or a gate/up pair
+ * plan) also write the statistics that the NEXT plan's RMSNorm + quantiser needs of its
+ * output row y (the output after the residual; the pair plan's a): per 32 consecutive
+ * outputs, RT_ROWSTAT_BYTES at `stats` (N / 32 records, device, 16-byte aligned), taken
+ * against next_norm_w fp32 [N] (device), the weight of that RMSNorm.  A plan with source
+ * RT_SRC_RMSNORM_STATS, x = y, aux = next_norm_w and aux2 = stats then quantises exactly as
+ * RT_SRC_RMSNORM would, with no workgroup-wide reduction in its prologue.  NULL, NULL
+ * detaches.  Fuses the norm statistics of the next RMSNorm (src/rotor/transformer.py:24-36)
+ * into the linear that produces its input (:329-339, :396-411). */
+int rt_plan_set_row_stats(rt_plan* plan, const float* next_norm_w, void* stats);
 
 /* ---- kernels around the linears for BitNet-2B-shape inference ----------------------
  * Positions are read from device memory (`pos`: position of the first of the M tokens)

@@ -91,6 +91,8 @@ struct Scratch {
 // symbol, not a device address: the address is resolved per device with
 // hipGetSymbolAddress (device current) and only that pointer is used.
 static_assert(RT_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size");
+static_assert(sizeof(RowStat) == RT_ROWSTAT_BYTES && kStatRows == 32 && RT_SRC_RMSNORM_STATS == kRmsNormStats,
+              "statistics records of the C ABI");
 static __device__ __align__(256) unsigned char scratch[RT_NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -158,6 +160,8 @@ struct rt_plan {
     float* pair_g = nullptr;      // optional g, u [N / 2]
     float* pair_u = nullptr;
     float pair_sg = 1.0f, pair_su = 1.0f;  // gate and up scales
+    RowStat* stat_out = nullptr;  // rt_plan_set_row_stats: the epilogue's statistics records
+    const float* stat_w = nullptr;  // and the next RMSNorm's weight they are taken against
     int quant_maxK = 0;  // > 0: every quant problem takes the vectorised row kernel (largest K)
 };
 
@@ -178,7 +182,7 @@ extern "C" {
 
 const char* rt_last_error(void) { return g_err.c_str(); }
 
-int rt_version(void) { return 103; }
+int rt_version(void) { return 104; }
 
 int rt_device_count(int* n) {
     if (!n) return fail(RT_EINVAL, "rt_device_count: n is NULL");
@@ -708,6 +712,7 @@ int rt_plan_describe(const rt_plan* plan, int* kind, int* tile_m, int* tile_n, i
 }
 
 // Plans of up to kInlineProbs problems pass their descriptors as kernel arguments.
+// (launch_gemv fills the leading weight-stream table from them.)
 static void inline_probs(const rt_plan* plan, GemvArgs* a) {
     if (plan->G > kInlineProbs) return;
     a->ninl = plan->G;
@@ -763,6 +768,8 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
         a.pair_u = plan->pair_u;
         a.pair_sg = plan->pair_sg;
         a.pair_su = plan->pair_su;
+        a.stat_out = plan->stat_out;
+        a.stat_w = plan->stat_w;
     }
     a.dev = plan->dev_probs;
     a.rb2p = plan->dev_rb2p;
@@ -1046,17 +1053,21 @@ int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const r
     if (G <= 0 || G > (1 << 16)) return fail(RT_EINVAL, "rt_plan_create_fused: G out of range");
     if (!src->x) return fail(RT_EINVAL, "rt_plan_create_fused: source x is NULL");
     if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRelu2Mul && src->mode != kRelu2MulNorm &&
-        src->mode != kAttnNorm && src->mode != kRmsNormSsq)
+        src->mode != kAttnNorm && src->mode != kRmsNormSsq && src->mode != kRmsNormStats)
         return fail(RT_EINVAL, "rt_plan_create_fused: unknown source mode");
     if (src->mode == kAttnNorm && (src->attn_head_dim <= 0 || src->attn_head_dim % 16 || src->attn_max_len <= 0 ||
                                    !w[0] || w[0]->K % src->attn_head_dim))
         return fail(RT_EINVAL, "rt_plan_create_fused: attention source needs head_dim (multiple of 16) dividing K "
                                "and max_len");
-    if ((src->mode != kQuant && !src->aux) || ((src->mode == kRelu2MulNorm || src->mode == kRmsNormSsq) && !src->aux2))
+    if ((src->mode != kQuant && !src->aux) ||
+        ((src->mode == kRelu2MulNorm || src->mode == kRmsNormSsq || src->mode == kRmsNormStats) && !src->aux2))
         return fail(RT_EINVAL, "rt_plan_create_fused: the source mode needs aux/aux2");
     const int K = w[0] ? w[0]->K : 0;
-    if (src->mode == kRmsNormSsq && (K % 64 || K > 8192))
-        return fail(RT_EINVAL, "rt_plan_create_fused: RMSNORM_SSQ needs K % 64 == 0 and K <= 8192");
+    if ((src->mode == kRmsNormSsq || src->mode == kRmsNormStats) && (K % 64 || K > 8192))
+        return fail(RT_EINVAL, "rt_plan_create_fused: RMSNORM_SSQ / RMSNORM_STATS need K % 64 == 0 and K <= 8192");
+    auto a16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
+    if (src->mode == kRmsNormStats && !(a16(src->x) && a16(src->aux) && a16(src->aux2)))
+        return fail(RT_EINVAL, "rt_plan_create_fused: RMSNORM_STATS needs 16-byte aligned x, aux and statistics");
     for (int g = 0; g < G; ++g) {
         if (!w[g] || !y[g]) return fail(RT_EINVAL, "rt_plan_create_fused: NULL entry in a pointer array");
         if (w[g]->K != K) return fail(RT_EINVAL, "rt_plan_create_fused: all weights must share K (one input)");
@@ -1094,6 +1105,11 @@ int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const r
     }
     p->total_rb = wg;
     p->shape = gemv_shape_fused(wg, minC);
+    if (src->mode == kRmsNormStats && !stats_shape_ok(Kp, p->shape.nw)) {
+        rt_plan_free(p);
+        return fail(RT_EINVAL, "rt_plan_create_fused: too few row blocks for the RMSNORM_STATS prologue "
+                               "(at most 8 chunks of 64 inputs per wave)");
+    }
     std::vector<int> rb2p(wg);
     for (int g = 0; g < G; ++g)
         for (int r = 0; r < w[g]->Np / kRowBlock; ++r) rb2p[p->probs[g].wg_begin + r] = g;
@@ -1115,9 +1131,9 @@ int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, fl
     if (!ctx || !w_gu || !src || !src->x || !a || !ssq || !out)
         return fail(RT_EINVAL, std::string(who) + ": NULL argument");
     *out = nullptr;
-    if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRmsNormSsq)
-        return fail(RT_EINVAL, std::string(who) + ": the source must be QUANT, RMSNORM or RMSNORM_SSQ");
-    if ((src->mode != kQuant && !src->aux) || (src->mode == kRmsNormSsq && !src->aux2))
+    if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRmsNormSsq && src->mode != kRmsNormStats)
+        return fail(RT_EINVAL, std::string(who) + ": the source must be QUANT, RMSNORM, RMSNORM_SSQ or RMSNORM_STATS");
+    if ((src->mode != kQuant && !src->aux) || ((src->mode == kRmsNormSsq || src->mode == kRmsNormStats) && !src->aux2))
         return fail(RT_EINVAL, std::string(who) + ": the source mode needs aux/aux2");
     if (w_gu->N % kRowBlock) return fail(RT_EINVAL, std::string(who) + ": the interleaved matrix needs N % 64 == 0");
     if (w_gu->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": weights live on another device");
@@ -1125,8 +1141,10 @@ int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, fl
     const GemvShape shape = gemv_shape_fused(Nb, w_gu->C);
     // the 4-element prologue: K / 4 threads, 16-byte aligned rows
     auto a16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
-    if (K % 64 || K / 4 > 64 * shape.nw || !a16(src->x) || !a16(src->aux) || !a16(src->aux2))
-        return fail(RT_EINVAL, std::string(who) + ": needs K % 64 == 0, K / 4 <= the workgroup's threads and "
+    const bool fits = src->mode == kRmsNormStats ? stats_shape_ok(Kp, shape.nw) : K / 4 <= 64 * shape.nw;
+    if (K % 64 || !fits || !a16(src->x) || !a16(src->aux) || !a16(src->aux2))
+        return fail(RT_EINVAL, std::string(who) + ": needs K % 64 == 0, K / 4 <= the workgroup's threads (at most "
+                                                  "8 chunks of 64 inputs per wave with RMSNORM_STATS) and "
                                                   "16-byte aligned sources");
     DeviceGuard guard(ctx->device);
     rt_plan* p = new rt_plan();
@@ -1150,6 +1168,24 @@ int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, fl
     p->pair_g = g_out;
     p->pair_u = u_out;
     *out = p;
+    return RT_OK;
+}
+
+int rt_plan_set_row_stats(rt_plan* plan, const float* next_norm_w, void* stats) {
+    const char* who = "rt_plan_set_row_stats";
+    if (!plan) return fail(RT_EINVAL, std::string(who) + ": plan is NULL");
+    if (!next_norm_w != !stats) return fail(RT_EINVAL, std::string(who) + ": give both the weight and the records, "
+                                                                          "or neither");
+    if (stats) {
+        if (!plan->fused || plan->G != 1)
+            return fail(RT_EINVAL, std::string(who) + ": only one-problem fused decode plans "
+                                                      "(rt_plan_create_fused with G = 1, rt_plan_create_gate_up)");
+        const int rows = plan->pair_a ? plan->probs[0].N / 2 : plan->probs[0].N;
+        if (rows % kStatRows) return fail(RT_EINVAL, std::string(who) + ": the plan's outputs must be a multiple of 32");
+        if (((uintptr_t)stats & 15u) != 0) return fail(RT_EINVAL, std::string(who) + ": records must be 16-byte aligned");
+    }
+    plan->stat_out = static_cast<RowStat*>(stats);
+    plan->stat_w = next_norm_w;
     return RT_OK;
 }
 

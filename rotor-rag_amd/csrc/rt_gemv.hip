@@ -63,6 +63,44 @@ __device__ __forceinline__ GemvProb find_prob(const GemvArgs& a, int rbg) {
     return GemvProb{q->w, q->qx, q->sx, q->rs, q->out, q->s_w, q->N, q->C, q->ldo, q->wg_begin, q->res, q->xs, q->K};
 }
 
+// floor(a / nw) from m = ceil(2^31 / nw), for 1 <= nw <= 16 and 0 <= a < 2^23 (a = wave * C
+// with C <= 2^16: weights hold K <= 2^22): with m nw = 2^31 + e, 0 <= e < nw, the quotient is
+// exact while a e < 2^31.  SALU multiplies only: a division by the kernel argument nw runs on
+// the VALU, and chunk bounds left in VGPRs put the buffer resource in VGPRs (a readfirstlane
+// loop around every weight load).  (An inline-asm readfirstlane is no way out: the compiler
+// inserts no wait states before an asm statement that reads a VGPR its previous VALU
+// instruction wrote, and the asm can read the stale value.)
+__device__ __forceinline__ int div_nw(int a, unsigned m) {
+    return (int)(((unsigned long long)(unsigned)a * m) >> 31);
+}
+static unsigned nw_reciprocal(int nw) { return (unsigned)(((1ull << 31) + (unsigned)nw - 1) / (unsigned)nw); }
+
+// The weight stream of global row block rbg, before anything else: for inline problems from
+// the leading table of the arguments (one scalar load, then selects: no branch, no second
+// load); otherwise from the row-block table and the descriptor.
+struct WStream {
+    const v4u* w;
+    int C, wg_begin;
+    int j;  // inline problems: the problem's index
+};
+// ninl: a.ninl, passed separately where it is a preloaded kernel argument.
+__device__ __forceinline__ WStream find_stream(const GemvArgs& a, int ninl, int rbg) {
+    if (ninl > 0) {
+        WStream s{a.inw[0].w, a.inw[0].C, a.inw[0].wg_begin, 0};
+#pragma unroll
+        for (int j = 1; j < kInlineProbs; ++j) {
+            const bool t = j < ninl && rbg >= a.inw[j].wg_begin;
+            s.w = t ? a.inw[j].w : s.w;
+            s.C = t ? a.inw[j].C : s.C;
+            s.wg_begin = t ? a.inw[j].wg_begin : s.wg_begin;
+            s.j = t ? j : s.j;
+        }
+        return s;
+    }
+    const GemvProb P = find_prob(a, rbg);
+    return WStream{P.w, P.C, P.wg_begin, 0};
+}
+
 // The plain absmax quantisation of problem P's own input row (has_pro == 2).
 __device__ __forceinline__ QuantProb own_source(const GemvProb& P) {
     return QuantProb{P.xs, nullptr, nullptr, nullptr, nullptr, P.K, P.C * kChunk, kQuant, nullptr, 0.0f, nullptr,
@@ -175,6 +213,18 @@ __device__ __forceinline__ void gemv_body(__amdgpu_buffer_rsrc_t rsrc, const int
     }
 }
 
+// The fp32 output of row r of row block rb for one token (M = 1, fp32 output): stored, and
+// returned for the statistics epilogue (0 for rows past N, which are not stored).
+__device__ __forceinline__ float emit1(const GemvProb& P, int rb, int r, int acc, float sx_pro) {
+    const int n = rb * kRowBlock + r;
+    if (n >= P.N) return 0.0f;
+    const float sw = P.rs ? P.rs[n] : P.s_w;
+    const float y = ((float)acc * sx_pro) * sw;
+    const float o = P.res ? P.res[n] + y : y;
+    static_cast<float*>(P.out)[n] = o;
+    return o;
+}
+
 // sx_pro: the token scale computed by a prologue (used instead of P.sx when >= 0)
 __device__ __forceinline__ void emit(const GemvArgs& a, const GemvProb& P, int rb, int m0, int m, int r, int acc,
                                      float sx_pro = -1.0f) {
@@ -259,7 +309,11 @@ constexpr int kAttnMaxThreads = 640;
 // PRO: 0 no prologue; 1 prologue quantising a row source (plain, RMSNorm, relu²·up,
 // relu²·up + sub-norm), 16 elements per thread; 3 / 4 the same with 4 / 8 consecutive
 // elements per thread (K % 64 == 0, K / 4 or K / 8 <= threads, 16-byte aligned sources);
-// 2 prologue combining decode-attention partials (kAttnNorm).
+// 2 prologue combining decode-attention partials (kAttnNorm); 5 RMSNorm from the row's
+// statistics (kRmsNormStats): every wave quantises only its own chunks, with no
+// workgroup barrier before the dot products.
+// With a.stat_out (M = 1, one problem) the epilogue also writes the RowStat records of
+// the outputs for the next plan's kRmsNormStats prologue.
 // PAIR (PRO 3, gate/up of the decode FFN): the matrix interleaves gate and up in 32-row
 // groups (row 64 j + r: gate row 32 j + r for r < 32, up row 32 j + r - 32 otherwise), so a
 // workgroup's row block holds both inputs of 32 outputs: it writes the FFN activation
@@ -268,10 +322,15 @@ constexpr int kAttnMaxThreads = 640;
 template <int MT, int PRO, bool PAIR = false>
 __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     gemv_ksplit_kernel(const float* pro_x, const float* pro_aux, const float* pro_aux2, int pro_K, int pro_mode,
-                       float pro_eps, GemvArgs a) {
-    // The prologue source's fields lead the argument list as scalars, so that the
-    // kernel-argument preload (-amdgpu-kernarg-preload-count) has them in SGPRs when the
-    // waves start: the row's loads then go out before any kernel-argument load returns.
+                       float pro_eps, unsigned shape, unsigned nw_m, const v4u* w1, GemvArgs a) {
+    // The prologue source's fields, the launch shape word (waves per workgroup nw in bits
+    // 0-4, inline problem count in bits 5-7, the chunks per row C1 of a one-problem launch
+    // from bit 8), nw_m = ceil(2^31 / nw) and the weight tiles w1 of a one-problem launch
+    // (null otherwise) lead the argument list as scalars: the kernel-argument preload
+    // (-amdgpu-kernarg-preload-count; 14 dwords fit, these are 13) has them in SGPRs when
+    // the waves start, so the row's loads and the first weight loads go out before any
+    // kernel-argument load returns (blockDim would be one more load).
+    const int ninl = (int)((shape >> 5) & 7u), C1 = (int)(shape >> 8);
     QuantProb pro = a.pro;
     pro.x = pro_x;
     pro.aux = pro_aux;
@@ -281,7 +340,7 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     pro.eps = pro_eps;
     constexpr int U = MT == 1 ? 4 : 2;
     extern __shared__ __attribute__((aligned(16))) int red[];
-    const int lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, nw = (int)(shape & 31u);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m0 = blockIdx.y * MT;
     // With a prologue whose row fits one group per thread, the row's loads go out first
@@ -289,10 +348,17 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     // first weight batches, which stream in during the prologue's arithmetic.
     constexpr int E = PRO == 4 ? 8 : 4;  // elements per thread of PRO 3 / 4
     using Regs = typename std::conditional<
-        PRO == 2, AttnRegs, typename std::conditional<PRO >= 3, RowRegsE<E>, RowRegs>::type>::type;
+        PRO == 5, StatRegs,
+        typename std::conditional<PRO == 2, AttnRegs,
+                                  typename std::conditional<(PRO >= 3), RowRegsE<E>, RowRegs>::type>::type>::type;
     Regs rr;
     bool early = false;
-    if constexpr (PRO == 1) {
+    if constexpr (PRO == 5) {
+        // the wave's chunks (every problem of a fused plan has the prologue row's K), so the
+        // records and the wave's elements are requested before anything else
+        const int C5 = (pro.K + 63) >> 6;  // from the preloaded K (Kp would be another load)
+        stat_load(pro, div_nw(wave * C5, nw_m), div_nw((wave + 1) * C5, nw_m), rr);
+    } else if constexpr (PRO == 1) {
         early = row_fits1(pro, blockDim.x);
         if (early) row_load1(pro, 0, rr);
     } else if constexpr (PRO >= 3) {
@@ -302,19 +368,39 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
         early = attn_fits1(pro, blockDim.x);
         if (early) attn_load1(pro, rr);
     }
-    static_assert(!PAIR || (PRO == 3 && MT == 1), "the pair epilogue follows the 4-element prologue");
-    const GemvProb P = find_prob(a, blockIdx.x);
-    const int rb = blockIdx.x - P.wg_begin;
-    const int C = P.C, ldx = C * 16;
-    // wave-uniform, kept in SGPRs (the buffer resource must not be per-lane)
-    const int cb = __builtin_amdgcn_readfirstlane((wave * C) / nw);
-    const int ce = __builtin_amdgcn_readfirstlane(((wave + 1) * C) / nw);
+    static_assert(!PAIR || ((PRO == 3 || PRO == 5) && MT == 1),
+                  "the pair epilogue follows the 4-element or the statistics prologue");
+    const WStream ws = w1 ? WStream{w1, C1, 0, 0} : find_stream(a, ninl, blockIdx.x);
+    const int rb = blockIdx.x - ws.wg_begin;
+    const int C = ws.C, ldx = C * 16;
+    // the wave's chunks [cb, ce): wave-uniform, in SGPRs (the buffer resource must not be
+    // per-lane)
+    const int cb = div_nw(wave * C, nw_m);
+    const int ce = div_nw((wave + 1) * C, nw_m);
     const __amdgpu_buffer_rsrc_t rsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(P.w + (size_t)rb * C * kRowBlock), 0, ce * 1024, kBufDword3);
+        __builtin_amdgcn_make_buffer_rsrc((void*)(ws.w + (size_t)rb * C * kRowBlock), 0, ce * 1024, kBufDword3);
     v4u A[U], B[U];
     int accP[MT], accQ[MT], sx[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accQ[m] = 0;
+    // the statistics prologue's weight batches go out before anything that waits for a
+    // load (the scheduler would otherwise hoist the record reductions above them)
+    if constexpr (PRO == 5) {
+        gemv_preload<U>(rsrc, lane * 16, cb, A, B, true);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // The rest of the descriptor (epilogue): for inline problems the one at the index the
+    // stream lookup chose; otherwise the table lookup.
+    const int pj = __builtin_amdgcn_readfirstlane(ws.j);
+    GemvProb P;
+    if (ninl > 0) {
+        P = a.inl[0];
+#pragma unroll
+        for (int j = 1; j < kInlineProbs; ++j)
+            if (pj == j) P = a.inl[j];
+    } else {
+        P = find_prob(a, blockIdx.x);
+    }
     // sum x of the wave's slice: without a prologue its activation loads go out before
     // the weights (waiting for them then does not wait for the weight batches)
     cint* xq = (cint*)(reinterpret_cast<const int*>(P.qx) + (size_t)m0 * ldx);
@@ -322,9 +408,16 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     // With a prologue only the first batch is in flight during it (register budget); the
     // attention prologue holds its partials in registers first and issues it after their
     // combine.
-    if (PRO != 2 || !early) gemv_preload<U>(rsrc, lane * 16, cb, A, B, PRO == 0);
+    if (PRO != 5 && (PRO != 2 || !early)) gemv_preload<U>(rsrc, lane * 16, cb, A, B, PRO == 0);
     float sx_pro = -1.0f;
-    if constexpr (PRO != 0) {
+    if constexpr (PRO == 5) {
+        // the wave's own activations: no barrier between the prologue and the dot products
+        v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
+        int qsum = 0;
+        sx_pro = stat_finish(pro, cb, ce, rr, lq, qsum);
+        sx[0] = qsum;
+        gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accQ, A, B);
+    } else if constexpr (PRO != 0) {
         v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
         RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (pro.Kp >> 4));
         sm->fac = (lfloat*)(sm + 1);  // kAttnNorm factors follow
@@ -359,7 +452,8 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
                 su += red[w * kRowBlock + 32 + r];
             }
             float av = 0.0f;
-            if (threadIdx.x < 32 && nu < P.N) {
+            const bool valid = threadIdx.x < 32 && nu < P.N;
+            if (valid) {
                 const float g = ((float)sg * sx_pro) * a.pair_sg;
                 const float u = ((float)su * sx_pro) * a.pair_su;
                 av = g > 0.0f ? (g * g) * u : 0.0f;
@@ -369,6 +463,18 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
             }
             const double ss = wave_reduce63((double)av * (double)av, 0.0, [](double x, double y) { return x + y; });
             if (threadIdx.x == kRowBlock - 1) a.pair_ssq[rb] = ss;
+            if (a.stat_out) write_row_stats(av, valid ? a.stat_w[i] : 0.0f, valid, a.stat_out, rb, 1);
+        }
+        return;
+    }
+    if (MT == 1 && PRO != 0 && a.stat_out) {  // one token, one problem: outputs and their statistics
+        if (threadIdx.x < kRowBlock) {
+            const int r = threadIdx.x, n = rb * kRowBlock + r;
+            int s = 0;
+            for (int w = 0; w < nw; ++w) s += red[w * kRowBlock + r];
+            const float o = emit1(P, rb, r, s, sx_pro);
+            const bool valid = n < P.N;
+            write_row_stats(o, valid ? a.stat_w[n] : 0.0f, valid, a.stat_out, 2 * rb, 2);
         }
         return;
     }
@@ -408,8 +514,36 @@ GemvShape gemv_shape(int total_rb, int m_blocks, int min_C) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s) {
-    if (a.total_rb <= 0 || a.M <= 0) return hipSuccess;
+bool stats_shape_ok(int Kp, int nw) {
+    const int C = Kp / kChunk;
+    return nw >= 1 && Kp <= 8192 && (C + nw - 1) / nw <= 4 * kStatSteps;
+}
+
+// One KSPLIT launch of nw waves per workgroup; the leading scalar arguments are the
+// prologue source's fields (zeros without a prologue), the shape word (nw <= 16, the inline
+// problem count and the chunks per row of a one-problem launch, C <= 2^16), nw's reciprocal
+// and the weight tiles of a one-problem launch (null otherwise).
+static_assert(kInlineProbs <= 7, "the inline problem count takes 3 bits of the shape word");
+template <int MT, int PRO, bool PAIR = false>
+static void launch_ksplit(dim3 grid, int nw, size_t lds, hipStream_t s, const GemvArgs& a) {
+    const QuantProb& P = a.pro;
+    const bool one = a.ninl == 1;
+    const unsigned shape = (unsigned)nw | ((unsigned)a.ninl << 5) | (one ? (unsigned)a.inl[0].C << 8 : 0u);
+    hipLaunchKernelGGL((gemv_ksplit_kernel<MT, PRO, PAIR>), grid, dim3((unsigned)(64 * nw)), lds, s, P.x, P.aux, P.aux2,
+                       P.K, P.mode, P.eps, shape, nw_reciprocal(nw), one ? a.inl[0].w : nullptr, a);
+}
+
+hipError_t launch_gemv(const GemvArgs& args, int mt, GemvShape shape, hipStream_t s) {
+    if (args.total_rb <= 0 || args.M <= 0) return hipSuccess;
+    // the leading weight-stream table: the inline problems, or the one problem of a
+    // single-problem launch as an inline problem
+    GemvArgs a = args;
+    if (a.ninl == 0 && !a.dev) {
+        a.ninl = 1;
+        a.inl[0] = a.p;
+    }
+    for (int j = 0; j < kInlineProbs; ++j)
+        a.inw[j] = j < a.ninl ? GemvWeights{a.inl[j].w, a.inl[j].C, a.inl[j].wg_begin} : GemvWeights{nullptr, 0, 0};
     const unsigned mblocks = (unsigned)((a.M + mt - 1) / mt);
     const dim3 block((unsigned)(64 * shape.nw));
     if (a.has_pro == 2) {  // single token, each problem's own row quantised in the prologue: ROWS
@@ -417,53 +551,44 @@ hipError_t launch_gemv(const GemvArgs& a, int mt, GemvShape shape, hipStream_t s
         const dim3 grid((unsigned)(a.total_rb / shape.nw), 1);
         const size_t lds = (size_t)a.pro.Kp + sizeof(RowSmem);  // pro.Kp: the largest Kp of the problems
         hipLaunchKernelGGL((gemv_rows_kernel<1, 1>), grid, block, lds, s, a);
-    } else if (a.has_pro && a.pair_a) {  // gate/up pair: the 4-element prologue only
+    } else if (a.has_pro && a.pair_a) {  // gate/up pair: the 4-element or the statistics prologue
         const QuantProb& P = a.pro;
+        const bool stats = P.mode == kRmsNormStats;
         if (mt != 1 || a.M != 1 || !shape.ksplit || P.K % 64 || !aligned16(P.x) || !aligned16(P.aux) ||
-            !aligned16(P.aux2) || P.K / 4 > 64 * shape.nw)
+            !aligned16(P.aux2) || (stats ? !stats_shape_ok(P.Kp, shape.nw) : P.K / 4 > 64 * shape.nw))
             return hipErrorInvalidValue;
         const dim3 grid((unsigned)a.total_rb, 1);
         const size_t lds = (size_t)shape.nw * kRowBlock * sizeof(int) + (size_t)P.Kp + sizeof(RowSmem);
-        hipLaunchKernelGGL((gemv_ksplit_kernel<1, 3, true>), grid, block, lds, s, P.x, P.aux, P.aux2, P.K, P.mode,
-                           P.eps, a);
+        if (stats) launch_ksplit<1, 5, true>(grid, shape.nw, lds, s, a);
+        else launch_ksplit<1, 3, true>(grid, shape.nw, lds, s, a);
     } else if (a.has_pro) {  // single token, prologue-quantised input: KSPLIT shape only
         if (mt != 1 || a.M != 1 || !shape.ksplit) return hipErrorInvalidValue;
         const dim3 grid((unsigned)a.total_rb, 1);
         const QuantProb& P = a.pro;
         const int nw = a.pro.mode == kAttnNorm ? std::min(shape.nw, kAttnMaxThreads / 64) : shape.nw;
         size_t lds = (size_t)nw * kRowBlock * sizeof(int) + (size_t)a.pro.Kp + sizeof(RowSmem);
-        if (a.pro.mode == kAttnNorm) {
+        const bool vec = P.K % 64 == 0 && aligned16(P.x) && aligned16(P.aux) && aligned16(P.aux2);
+        if (a.pro.mode == kRmsNormStats) {
+            if (!vec || !stats_shape_ok(P.Kp, nw)) return hipErrorInvalidValue;
+            launch_ksplit<1, 5>(grid, nw, lds, s, a);
+        } else if (a.pro.mode == kAttnNorm) {
             lds += (size_t)(a.pro.K / a.pro.attn_hd) * (a.pro.attn_S + 1) * sizeof(float);
-            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 2>), grid, dim3((unsigned)(64 * nw)), lds, s, P.x, P.aux, P.aux2,
-                               P.K, P.mode, P.eps, a);
-        } else if (a.pro.K % 64 == 0 && aligned16(a.pro.x) && aligned16(a.pro.aux) && aligned16(a.pro.aux2) &&
-                   a.pro.K / 4 <= (int)block.x) {
-            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 3>), grid, block, lds, s, P.x, P.aux, P.aux2, P.K, P.mode,
-                               P.eps, a);
-        } else if (a.pro.K % 64 == 0 && aligned16(a.pro.x) && aligned16(a.pro.aux) && aligned16(a.pro.aux2) &&
-                   a.pro.K / 8 <= (int)block.x) {
-            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 4>), grid, block, lds, s, P.x, P.aux, P.aux2, P.K, P.mode,
-                               P.eps, a);
+            launch_ksplit<1, 2>(grid, nw, lds, s, a);
+        } else if (vec && P.K / 4 <= (int)block.x) {
+            launch_ksplit<1, 3>(grid, nw, lds, s, a);
+        } else if (vec && P.K / 8 <= (int)block.x) {
+            launch_ksplit<1, 4>(grid, nw, lds, s, a);
         } else {
-            hipLaunchKernelGGL((gemv_ksplit_kernel<1, 1>), grid, block, lds, s, P.x, P.aux, P.aux2, P.K, P.mode,
-                               P.eps, a);
+            launch_ksplit<1, 1>(grid, nw, lds, s, a);
         }
     } else if (shape.ksplit) {
         const dim3 grid((unsigned)a.total_rb, mblocks);
         const size_t lds = (size_t)shape.nw * mt * kRowBlock * sizeof(int);
         switch (mt) {
-            case 1:
-                hipLaunchKernelGGL((gemv_ksplit_kernel<1, 0>), grid, block, lds, s, nullptr, nullptr, nullptr, 0, 0, 0.0f, a);
-                break;
-            case 2:
-                hipLaunchKernelGGL((gemv_ksplit_kernel<2, 0>), grid, block, lds, s, nullptr, nullptr, nullptr, 0, 0, 0.0f, a);
-                break;
-            case 4:
-                hipLaunchKernelGGL((gemv_ksplit_kernel<4, 0>), grid, block, lds, s, nullptr, nullptr, nullptr, 0, 0, 0.0f, a);
-                break;
-            case 8:
-                hipLaunchKernelGGL((gemv_ksplit_kernel<8, 0>), grid, block, lds, s, nullptr, nullptr, nullptr, 0, 0, 0.0f, a);
-                break;
+            case 1: launch_ksplit<1, 0>(grid, shape.nw, lds, s, a); break;
+            case 2: launch_ksplit<2, 0>(grid, shape.nw, lds, s, a); break;
+            case 4: launch_ksplit<4, 0>(grid, shape.nw, lds, s, a); break;
+            case 8: launch_ksplit<8, 0>(grid, shape.nw, lds, s, a); break;
             default: return hipErrorInvalidValue;
         }
     } else {

@@ -79,8 +79,30 @@ __host__ __device__ inline unsigned rotor_code(unsigned g) {
 //             (cast; the `ssq` output of a gate/up pair plan): the 4- and 8-element
 //             prologues add those up instead of reducing x over the workgroup; every
 //             other path ignores them and reduces x itself
+//   kRmsNormStats  as kRmsNorm, with the row's statistics given in aux2 (cast; RowStat[K/32],
+//             written by the producer of x): the decode GEMV prologue then needs no
+//             workgroup reduction (kernels other than that prologue reduce x themselves)
 enum QuantMode { kQuant = 0, kPermute = 1, kRmsNorm = 2, kRelu2Mul = 3, kRelu2MulNorm = 4, kAttnNorm = 5,
-                 kRmsNormSsq = 6 };
+                 kRmsNormSsq = 6, kRmsNormStats = 7 };
+
+// Statistics of a row y that the next RMSNorm + absmax quantiser needs, per group of 32
+// consecutive elements, with w the next RMSNorm's weight:
+//   ssq    sum of (double) y_k^2;
+//   tmax   max of t_k = |y_k| |w_k|, in f64 (exact: a product of two floats);
+//   ncand  the number of k with t_k >= tmax (1 - kStatDelta), cx / cw = y_k, w_k of the
+//          first of them.
+// The quantiser's absmax is max_k fl(fl(|y_k| / n) |w_k|) (n the RMSNorm divisor); each of
+// the two roundings moves a value by at most a factor 1 +- 2^-24, so only the k with
+// t_k >= max_j t_j (1 - 2^-22) can hold that maximum: with kStatDelta = 2^-20 they are all
+// among the recorded candidates of the groups whose tmax reaches the threshold, and a
+// group with one candidate needs no other element.
+struct RowStat {
+    double ssq, tmax;
+    float cx, cw;
+    int ncand, pad;
+};
+constexpr int kStatRows = 32;
+constexpr double kStatDelta = 0x1p-20;
 
 struct QuantProb {
     const float* x;      // fp32 [M][K] (gate in kRelu2Mul)
@@ -118,7 +140,18 @@ struct GemvProb {
 // problems' wg_begin, with no dependent loads from a descriptor table.
 constexpr int kInlineProbs = 4;
 
+// What a GEMV workgroup needs before it can issue its first weight loads: its problem's
+// weight tiles, chunks per row and first global row block.
+struct GemvWeights {
+    const v4u* w;
+    int C, wg_begin;
+};
+
 struct GemvArgs {
+    // the weight streams of the inline problems and their count lead the arguments, so one
+    // scalar load brings in all a workgroup needs to start streaming its weights
+    GemvWeights inw[kInlineProbs];
+    int ninl;             // > 0: the G = ninl problems are inl[] (dev and rb2p unused)
     const GemvProb* dev;  // device descriptor array [G] (plans) or nullptr -> p
     const int* rb2p;      // [total_rb] problem index of every global row block (plans)
     int G, M, out_i32;
@@ -127,7 +160,6 @@ struct GemvArgs {
     int has_pro;          // M = 1: every workgroup quantises its input row into LDS first:
                           // 1 the shared row `pro` (KSPLIT), 2 its problem's xs (ROWS, plain absmax)
     QuantProb pro;        // has_pro == 1: source row of the prologue (mode, x, aux, aux2, eps, K, Kp)
-    int ninl;             // > 0: the G = ninl problems are inl[] (dev and rb2p unused)
     GemvProb inl[kInlineProbs];
     // gate/up pair (KSPLIT, has_pro == 1, one problem whose rows interleave gate and up in
     // groups of 32): row block j writes, instead of y, pair_a[32 j + r] = relu(g)^2 * u of
@@ -138,6 +170,11 @@ struct GemvArgs {
     float* pair_g;
     float* pair_u;
     float pair_sg, pair_su;  // the gate and up scales
+    // M = 1 KSPLIT launches over one problem: when stat_out is set, the epilogue also writes
+    // the RowStat of every 32 outputs (y after the residual, or the pair's a) against the
+    // next RMSNorm's weight stat_w [N] (stat_out [N / 32])
+    RowStat* stat_out;
+    const float* stat_w;
 };
 
 struct GemvShape {
@@ -198,17 +235,33 @@ __device__ __forceinline__ T wave_reduce63(T v, T id, Op op) {
     v = op(v, dpp_step<0x143, 0xc>(v, id));  // row_bcast:31 into rows 2, 3
     return v;
 }
+// The first five steps of wave_reduce63 (up to row_bcast 15): lane 31 holds op over
+// lanes 0..31 and lane 63 op over lanes 32..63.
+template <typename T, typename Op>
+__device__ __forceinline__ T half_reduce31(T v, T id, Op op) {
+    v = op(v, dpp_step<0x111, 0xf>(v, id));  // row_shr:1
+    v = op(v, dpp_step<0x112, 0xf>(v, id));  // row_shr:2
+    v = op(v, dpp_step<0x114, 0xf>(v, id));  // row_shr:4
+    v = op(v, dpp_step<0x118, 0xf>(v, id));  // row_shr:8
+    v = op(v, dpp_step<0x142, 0xa>(v, id));  // row_bcast:15 into rows 1, 3
+    return v;
+}
+// value of v in lane `lane` (wave-uniform), returned to every lane (through an SGPR)
+template <typename T>
+__device__ __forceinline__ T read_lane(T v, int lane) {
+    if constexpr (sizeof(T) == 8) {
+        const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+        const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, lane);
+        const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), lane);
+        return __builtin_bit_cast(T, ((unsigned long long)hi << 32) | lo);
+    } else {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+    }
+}
 // the lane-63 total, returned to every lane (through an SGPR)
 template <typename T>
 __device__ __forceinline__ T lane63(T v) {
-    if constexpr (sizeof(T) == 8) {
-        const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
-        const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)b, 63);
-        const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(b >> 32), 63);
-        return __builtin_bit_cast(T, ((unsigned long long)hi << 32) | lo);
-    } else {
-        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-    }
+    return read_lane(v, 63);
 }
 __device__ __forceinline__ int wave_sum(int v) {
     return lane63(wave_reduce63(v, 0, [](int a, int b) { return a + b; }));
@@ -288,5 +341,8 @@ inline int gemv_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 GemvShape gemv_shape(int total_rb, int m_blocks, int min_C);
 // Launch shape of a plan whose GEMV quantises its input in the prologue (M = 1).
 GemvShape gemv_shape_fused(int total_rb, int min_C);
+// The kRmsNormStats prologue fits a row of Kp bytes over nw waves (K / 32 <= 256 records,
+// at most 8 chunks per wave).
+bool stats_shape_ok(int Kp, int nw);
 
 }  // namespace rt

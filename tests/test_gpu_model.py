@@ -405,6 +405,30 @@ def test_long_prompt_greedy_matches_oracle(long_models, name):
     assert i >= 3, "oracle gaps too small to compare"
 
 
+def test_decode_row_stats_handoff_bit_exact(hip):
+    """Decode with the row-statistics hand-off (each RMSNorm input row's statistics written by
+    the plan that produces the row, consumed by the next plan's prologue) gives the same
+    logits, bit for bit, and the same graph-replayed greedy tokens as decode with every
+    prologue reducing its row itself."""
+    params = O.make_bitnet_params(21, SMALL, 64)
+    prompt = np.array([3, 14, 15, 92, 65], np.int32)
+    runs = []
+    for stats in (False, True):
+        model = _device_model(hip, params, SMALL, 64)
+        model._dev.row_stats = stats
+        _, cache = model.forward(prompt, return_logits=False, use_cache=True)
+        tok, lgs = 7, []
+        for _ in range(4):
+            lg, cache = model.forward(np.array([tok], np.int32), past_kv_cache=cache, use_cache=True)
+            lgs.append(lg[0].copy())
+            tok = int(np.argmax(lg[0]))
+        toks = model.generate_greedy(prompt, 6, graph=True)
+        runs.append((np.stack(lgs), toks, "s_h1" in model._dev.state[1]))
+    assert not runs[0][2] and runs[1][2], "the second model must run the statistics plans"
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert list(runs[0][1]) == list(runs[1][1])
+
+
 def _greedy_vs_oracle(model, params, cfg, prompt, n):
     """generate_greedy (prefill, then graph-replayed decode steps) beside the oracle's greedy
     protocol (src/rotor/generation.py:244-279: argmax, one token per step), the oracle's

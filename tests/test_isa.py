@@ -9,7 +9,11 @@ can silently lose:
     makes the wave wait for that load, serialising the prologue's loads);
   * the GEMV expands weights with masks only and reads its activations for the dot
     products with scalar loads;
-  * the GEMM's main loop is free of scratch traffic and of waterfall loops.
+  * the GEMM's main loop is free of scratch traffic and of waterfall loops;
+  * no lane read (v_readfirstlane / v_readlane) is written as inline asm: the compiler
+    inserts no wait states before an asm statement that reads a VGPR its previous VALU
+    instruction wrote, and such a read can return the stale value (it did, for the GEMV's
+    chunk bounds, with wrong sums as the result).
 """
 import re
 import shutil
@@ -80,11 +84,20 @@ def test_gemv_kernels_scalar_descriptors_no_spills(gemv):
 
 
 def test_gemv_prologue_source_preloaded(gemv):
-    # the KSPLIT kernels with a prologue get their row source (x, aux, aux2, K, mode, eps:
-    # 9 dwords) in SGPRs at wave launch
+    # the KSPLIT kernels get their row source (x, aux, aux2, K, mode, eps: 9 dwords), the
+    # inline problem count, nw and its reciprocal in SGPRs at wave launch
     for n in [n for n in gemv if "gemv_ksplit_kernel" in n]:
         m = re.search(r"\.amdhsa_user_sgpr_kernarg_preload_length\s+(\d+)", gemv["__meta__"][n])
-        assert m and int(m.group(1)) >= 9, n
+        assert m and int(m.group(1)) >= 12, n
+
+
+def test_no_inline_asm_lane_reads(gemv, gemm):
+    for kernels in (gemv, gemm):
+        for n, t in kernels.items():
+            if n == "__meta__":
+                continue
+            for block in re.findall(r";;#ASMSTART(.*?);;#ASMEND", t, re.S):
+                assert "v_readfirstlane" not in block and "v_readlane" not in block, f"{n}: inline-asm lane read"
 
 
 def test_gemv_rows_reads_activations_with_scalar_loads(gemv):

@@ -1139,11 +1139,12 @@ int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, fl
     if (w_gu->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": weights live on another device");
     const int K = w_gu->K, Kp = round_up(K, kChunk), Nb = w_gu->Np / kRowBlock;
     const GemvShape shape = gemv_shape_fused(Nb, w_gu->C);
-    // the 4-element prologue: K / 4 threads, 16-byte aligned rows
+    // an E-element prologue (K / 16 <= threads at least), 16-byte aligned rows
     auto a16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
-    const bool fits = src->mode == kRmsNormStats ? stats_shape_ok(Kp, shape.nw) : K / 4 <= 64 * shape.nw;
+    const bool fits =
+        src->mode == kRmsNormStats ? stats_shape_ok(Kp, shape.nw) : vec_elements(K, 64 * shape.nw) != 0;
     if (K % 64 || !fits || !a16(src->x) || !a16(src->aux) || !a16(src->aux2))
-        return fail(RT_EINVAL, std::string(who) + ": needs K % 64 == 0, K / 4 <= the workgroup's threads (at most "
+        return fail(RT_EINVAL, std::string(who) + ": needs K % 64 == 0, K / 16 <= the workgroup's threads (at most "
                                                   "8 chunks of 64 inputs per wave with RMSNORM_STATS) and "
                                                   "16-byte aligned sources");
     DeviceGuard guard(ctx->device);

@@ -25,7 +25,8 @@
 // accP and 4 sum g x into accQ, and, with g = w + 1,
 //     sum w x = accP + accQ / 4 - sum x.
 // sum x over the same k range (padding activations are 0) is the same for every lane:
-// each wave computes it once from the activation row (slice_sums).
+// each wave computes it once from the activation row (slice_sums), or, where a prologue
+// quantised the row, the prologue leaves the row's total and one wave subtracts it.
 #include <algorithm>
 #include <type_traits>
 
@@ -346,11 +347,12 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     // With a prologue whose row fits one group per thread, the row's loads go out first
     // (they do not depend on the problem); then the problem, the weight resource and the
     // first weight batches, which stream in during the prologue's arithmetic.
-    constexpr int E = PRO == 4 ? 8 : 4;  // elements per thread of PRO 3 / 4
+    constexpr bool VEC = PRO == 3 || PRO == 4 || PRO == 6;  // the E-element prologues
+    constexpr int E = PRO == 4 ? 8 : PRO == 6 ? 16 : 4;      // elements per thread of PRO 3 / 4 / 6
     using Regs = typename std::conditional<
         PRO == 5, StatRegs,
         typename std::conditional<PRO == 2, AttnRegs,
-                                  typename std::conditional<(PRO >= 3), RowRegsE<E>, RowRegs>::type>::type>::type;
+                                  typename std::conditional<VEC, RowRegsE<E>, RowRegs>::type>::type>::type;
     Regs rr;
     bool early = false;
     if constexpr (PRO == 5) {
@@ -361,15 +363,15 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     } else if constexpr (PRO == 1) {
         early = row_fits1(pro, blockDim.x);
         if (early) row_load1(pro, 0, rr);
-    } else if constexpr (PRO >= 3) {
-        early = true;  // the host launches PRO 3 / 4 only where K % 64 == 0 and K / E <= threads
+    } else if constexpr (VEC) {
+        early = true;  // the host launches PRO 3 / 4 / 6 only where K % 64 == 0 and K / E <= threads
         row_loadE<E>(pro, rr);
     } else if constexpr (PRO == 2) {
         early = attn_fits1(pro, blockDim.x);
         if (early) attn_load1(pro, rr);
     }
-    static_assert(!PAIR || ((PRO == 3 || PRO == 5) && MT == 1),
-                  "the pair epilogue follows the 4-element or the statistics prologue");
+    static_assert(!PAIR || ((VEC || PRO == 5) && MT == 1),
+                  "the pair epilogue follows an E-element or the statistics prologue");
     const WStream ws = w1 ? WStream{w1, C1, 0, 0} : find_stream(a, ninl, blockIdx.x);
     const int rb = blockIdx.x - ws.wg_begin;
     const int C = ws.C, ldx = C * 16;
@@ -424,7 +426,7 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
         const QxRow qrow{lq, 4, 1};
         if (!early) sx_pro = row_quantize<1>(pro, 0, qrow, nullptr, nullptr, sm);
         else if constexpr (PRO == 1) sx_pro = row_finish1(pro, rr, qrow, nullptr, nullptr, sm);
-        else if constexpr (PRO >= 3) sx_pro = row_finishE<E>(pro, rr, lq, sm);
+        else if constexpr (VEC) sx_pro = row_finishE<E>(pro, rr, lq, sm);
         else {
             float v[4];
             attn_combine1(pro, rr, v);
@@ -435,7 +437,15 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
 #pragma unroll
         for (int i = 0; i < U; ++i) B[i] = gemv_load<U>(rsrc, lane * 16, cb + U + i);
         __syncthreads();
-        slice_sums<MT, lint>((lint*)lq, ldx, cb * 16, ce * 16, sx);
+        if (VEC || (PRO == 2 && early)) {
+            // the prologue left each (live) wave's sum of quantised values in RowSmem::qs:
+            // wave 0 subtracts the row's total, the other waves nothing (the epilogue adds
+            // the waves)
+            const int nq = VEC ? (pro.K / E + 63) >> 6 : nw;
+            sx[0] = wave == 0 ? slots_reduce(sm->qs, nq, [](int x, int y) { return x + y; }) : 0;
+        } else {
+            slice_sums<MT, lint>((lint*)lq, ldx, cb * 16, ce * 16, sx);
+        }
         gemv_body<MT, U, lint>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accQ, A, B);
     } else {
         gemv_body<MT, U, cint>(rsrc, lane * 16, xq, ldx, cb, ce, accP, accQ, A, B);
@@ -514,6 +524,16 @@ GemvShape gemv_shape(int total_rb, int m_blocks, int min_C) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+int vec_elements(int K, int threads) {
+    // the smallest E whose live waves stay within kVecLiveWaves (per-element work is the same
+    // for every E; each live wave adds the prologue's per-wave work: reductions, norm, scale),
+    // else the E with the fewest live waves
+    if (K <= 0 || K % 64) return 0;
+    for (int E : {4, 8, 16})
+        if (K / E <= threads && (K / E + 63) / 64 <= kVecLiveWaves) return E;
+    return K / 16 <= threads ? 16 : 0;
+}
+
 bool stats_shape_ok(int Kp, int nw) {
     const int C = Kp / kChunk;
     return nw >= 1 && Kp <= 8192 && (C + nw - 1) / nw <= 4 * kStatSteps;
@@ -551,16 +571,19 @@ hipError_t launch_gemv(const GemvArgs& args, int mt, GemvShape shape, hipStream_
         const dim3 grid((unsigned)(a.total_rb / shape.nw), 1);
         const size_t lds = (size_t)a.pro.Kp + sizeof(RowSmem);  // pro.Kp: the largest Kp of the problems
         hipLaunchKernelGGL((gemv_rows_kernel<1, 1>), grid, block, lds, s, a);
-    } else if (a.has_pro && a.pair_a) {  // gate/up pair: the 4-element or the statistics prologue
+    } else if (a.has_pro && a.pair_a) {  // gate/up pair: an E-element or the statistics prologue
         const QuantProb& P = a.pro;
         const bool stats = P.mode == kRmsNormStats;
+        const int E = stats ? 0 : vec_elements(P.K, 64 * shape.nw);
         if (mt != 1 || a.M != 1 || !shape.ksplit || P.K % 64 || !aligned16(P.x) || !aligned16(P.aux) ||
-            !aligned16(P.aux2) || (stats ? !stats_shape_ok(P.Kp, shape.nw) : P.K / 4 > 64 * shape.nw))
+            !aligned16(P.aux2) || (stats ? !stats_shape_ok(P.Kp, shape.nw) : E == 0))
             return hipErrorInvalidValue;
         const dim3 grid((unsigned)a.total_rb, 1);
         const size_t lds = (size_t)shape.nw * kRowBlock * sizeof(int) + (size_t)P.Kp + sizeof(RowSmem);
         if (stats) launch_ksplit<1, 5, true>(grid, shape.nw, lds, s, a);
-        else launch_ksplit<1, 3, true>(grid, shape.nw, lds, s, a);
+        else if (E == 4) launch_ksplit<1, 3, true>(grid, shape.nw, lds, s, a);
+        else if (E == 8) launch_ksplit<1, 4, true>(grid, shape.nw, lds, s, a);
+        else launch_ksplit<1, 6, true>(grid, shape.nw, lds, s, a);
     } else if (a.has_pro) {  // single token, prologue-quantised input: KSPLIT shape only
         if (mt != 1 || a.M != 1 || !shape.ksplit) return hipErrorInvalidValue;
         const dim3 grid((unsigned)a.total_rb, 1);
@@ -574,10 +597,10 @@ hipError_t launch_gemv(const GemvArgs& args, int mt, GemvShape shape, hipStream_
         } else if (a.pro.mode == kAttnNorm) {
             lds += (size_t)(a.pro.K / a.pro.attn_hd) * (a.pro.attn_S + 1) * sizeof(float);
             launch_ksplit<1, 2>(grid, nw, lds, s, a);
-        } else if (vec && P.K / 4 <= (int)block.x) {
-            launch_ksplit<1, 3>(grid, nw, lds, s, a);
-        } else if (vec && P.K / 8 <= (int)block.x) {
-            launch_ksplit<1, 4>(grid, nw, lds, s, a);
+        } else if (const int E = vec ? vec_elements(P.K, (int)block.x) : 0) {
+            if (E == 4) launch_ksplit<1, 3>(grid, nw, lds, s, a);
+            else if (E == 8) launch_ksplit<1, 4>(grid, nw, lds, s, a);
+            else launch_ksplit<1, 6>(grid, nw, lds, s, a);
         } else {
             launch_ksplit<1, 1>(grid, nw, lds, s, a);
         }

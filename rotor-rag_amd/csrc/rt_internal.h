@@ -344,5 +344,9 @@ GemvShape gemv_shape_fused(int total_rb, int min_C);
 // The kRmsNormStats prologue fits a row of Kp bytes over nw waves (K / 32 <= 256 records,
 // at most 8 chunks per wave).
 bool stats_shape_ok(int Kp, int nw);
+// Elements per thread (4, 8 or 16) of the vectorised decode prologue for a row of K
+// (K % 64 == 0) on `threads` threads, 0 when none fits.
+constexpr int kVecLiveWaves = 16;  // measured: 4, 8 and 16 give the same decode time
+int vec_elements(int K, int threads);
 
 }  // namespace rt

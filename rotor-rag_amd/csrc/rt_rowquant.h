@@ -23,8 +23,17 @@ typedef __attribute__((address_space(3))) float lfloat;
 struct RowSmem {   // reduction scratch in LDS (one slot per wave)
     float f[16];
     double d[16];
+    int qs[16];    // the 4- / 8-element and attention prologues: each wave's sum of its quantised values
     lfloat* fac;   // kAttnNorm: [heads][S] combine factors (-1 = empty block), then [heads] denominators
 };
+
+// op over the n (<= 64) slots red[0 .. n): lane l reads slot l, one DPP reduction (no chain of
+// dependent LDS reads); the total is returned to every lane.  0 is the identity of op.
+template <typename T, typename Op>
+__device__ __forceinline__ T slots_reduce(const T* red, int n, Op op) {
+    const int lane = threadIdx.x & 63;
+    return lane63(wave_reduce63(lane < n ? red[lane] : T(0), T(0), op));
+}
 
 // Workgroup reduction through one slot per wave.  Each slot array serves one reduction
 // per row_quantize call (sums in RowSmem::d, maxima in RowSmem::f), so no barrier is
@@ -38,9 +47,7 @@ __device__ __forceinline__ T block_reduce(T v, T* red, Op op, bool wave_live = t
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
     if (lane == 63) red[wave] = v;
     __syncthreads();
-    T r = red[0];
-    for (int w = 1; w < nw; ++w) r = op(r, red[w]);
-    return r;
+    return slots_reduce(red, nw, op);
 }
 
 // byte p (0..15) of a permuted group holds element 4*(p%4) + p/4 of the group
@@ -294,17 +301,63 @@ __device__ __forceinline__ bool row_fits1(const QuantProb& P, int T) {
 typedef float v4f_a8 __attribute__((ext_vector_type(4), aligned(8)));
 typedef float v2f_a8 __attribute__((ext_vector_type(2), aligned(8)));
 
+// v[j] / d for fp32 elements and one fp32 divisor d > 0, computed as fl32(v fl64(1 / d)):
+// the f64 product is within 2^-52 (relative) of v / d, and a quotient in the normal range
+// lies at least 2^-49 (relative) from every rounding midpoint of fp32 (for a midpoint m in
+// [2^e, 2^(e+1)), v - m d is a non-zero multiple of 2^(e + e_d - 47)), so the rounded product
+// is the correctly rounded quotient, at a third of the IEEE division's instructions.  A
+// subnormal quotient can sit exactly on a midpoint: when a non-zero element's product lands
+// at or below 2^-126 the thread takes the IEEE division for all its elements.
 template <int E>
-__device__ __forceinline__ void scatter_q(const float (&v)[E], float sc, v4u* lq) {
-    unsigned char* lb = reinterpret_cast<unsigned char*>(lq);
-    const int k0 = E * (int)threadIdx.x;
+__device__ __forceinline__ void divide_all(float (&v)[E], float d) {
+    const double r = 1.0 / (double)d;
+    float c[E];
+    bool tiny = false;
 #pragma unroll
     for (int j = 0; j < E; ++j) {
-        const int k = k0 + j, e = k & 15;
-        float q = rintf(v[j] / sc);
-        q = fminf(fmaxf(q, -128.0f), 127.0f);
-        lb[(k & ~15) + 4 * (e & 3) + (e >> 2)] = (unsigned char)(int)q;
+        c[j] = (float)((double)v[j] * r);
+        tiny = tiny || (v[j] != 0.0f && fabsf(c[j]) <= 0x1p-126f);
     }
+    if (tiny) {
+#pragma unroll
+        for (int j = 0; j < E; ++j) c[j] = v[j] / d;
+    }
+#pragma unroll
+    for (int j = 0; j < E; ++j) v[j] = c[j];
+}
+
+// Writes rint(v[j] / sc), clamped to the int8 range, to the LDS row (one byte each) and
+// returns their sum.  v / sc as in divide_all; a quotient at or below 2^-126 in magnitude,
+// where the product may round differently, rounds to 0 either way.
+template <int E>
+__device__ __forceinline__ int scatter_q(const float (&v)[E], float sc, v4u* lq) {
+    const double r = 1.0 / (double)sc;
+    int q[E], s = 0;
+#pragma unroll
+    for (int j = 0; j < E; ++j) {
+        const float f = rintf((float)((double)v[j] * r));
+        q[j] = (int)fminf(fmaxf(f, -128.0f), 127.0f);
+        s += q[j];
+    }
+    if constexpr (E == 16) {  // the thread's elements are one whole group: one 16-byte write
+        lq[threadIdx.x] = pack_permuted(q);
+    } else {
+        unsigned char* lb = reinterpret_cast<unsigned char*>(lq);
+        const int k0 = E * (int)threadIdx.x;
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            const int k = k0 + j, e = k & 15;
+            lb[(k & ~15) + 4 * (e & 3) + (e >> 2)] = (unsigned char)q[j];
+        }
+    }
+    return s;
+}
+
+// The wave's sum of its quantised values into its slot RowSmem::qs (read after the caller's
+// barrier): a GEMV subtracts the row's total once instead of every wave summing its slice.
+__device__ __forceinline__ void qsum_to_slot(int s, RowSmem* sm, bool live) {
+    if (live) s = wave_reduce63(s, 0, [](int a, int b) { return a + b; });
+    if ((threadIdx.x & 63) == 63) sm->qs[threadIdx.x >> 6] = s;
 }
 
 template <int E>
@@ -337,7 +390,7 @@ __device__ __forceinline__ void row_loadE(const QuantProb& P, RowRegsE<E>& r) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) r.ssq[i] = 0.0;
-    if (P.mode == kRmsNormSsq) {  // K / 32 <= 256 partials (K <= 8192): up to four per lane
+    if (P.mode == kRmsNormSsq && r.live) {  // K / 32 <= 256 partials (K <= 8192): up to four per lane
         const double* pp = reinterpret_cast<const double*>(P.aux2);
         const int lane = threadIdx.x & 63, n = K >> 5;
 #pragma unroll
@@ -346,11 +399,27 @@ __device__ __forceinline__ void row_loadE(const QuantProb& P, RowRegsE<E>& r) {
     }
 }
 
+// Reduction over the waves that hold the row (the first nlive, `live`): they reduce their
+// values into slots, every wave passes the barrier, the live waves reduce the nlive slots.
+// Waves without elements spend nothing but the barrier.
+template <typename T, typename Op>
+__device__ __forceinline__ T live_reduce(T v, T* red, Op op, bool live, int nlive) {
+    if (live) {
+        v = wave_reduce63(v, T(0), op);
+        if ((threadIdx.x & 63) == 63) red[threadIdx.x >> 6] = v;
+    }
+    __syncthreads();
+    return live ? slots_reduce(red, nlive, op) : T(0);
+}
+
+// The row's RMSNorm / relu^2 and absmax quantisation into the LDS row.  Waves that own no
+// element (not live) take part in the barriers only; the returned scale and the RowSmem::qs
+// slots are those of the live waves (wave 0 always is one: K >= 64).
 template <int E>
 __device__ __forceinline__ float row_finishE(const QuantProb& P, RowRegsE<E>& r, v4u* lq, RowSmem* sm) {
     auto fmax_op = [](float x, float y) { return fmaxf(x, y); };
     auto dadd_op = [](double x, double y) { return x + y; };
-    const int t = threadIdx.x, K = P.K;
+    const int t = threadIdx.x, K = P.K, nlive = (K / E + 63) >> 6;
     const bool mine = t < K / E;
     float (&v)[E] = r.v;
     if (mine && has_relu2(P)) {
@@ -359,25 +428,31 @@ __device__ __forceinline__ float row_finishE(const QuantProb& P, RowRegsE<E>& r,
     }
     if (has_norm(P)) {
         double ss = 0.0;
-        if (P.mode == kRmsNormSsq) {  // every wave adds the given partials, in one order
-            ss = lane63(wave_reduce63((r.ssq[0] + r.ssq[1]) + (r.ssq[2] + r.ssq[3]), 0.0, dadd_op));
+        if (P.mode == kRmsNormSsq) {  // every live wave adds the given partials, in one order
+            if (r.live) ss = lane63(wave_reduce63((r.ssq[0] + r.ssq[1]) + (r.ssq[2] + r.ssq[3]), 0.0, dadd_op));
         } else {
 #pragma unroll
             for (int j = 0; j < E; ++j) ss += (double)v[j] * (double)v[j];
-            ss = block_reduce(ss, sm->d, dadd_op, r.live);
+            ss = live_reduce(ss, sm->d, dadd_op, r.live, nlive);
         }
-        const float norm = sqrtf((float)(ss / (double)K) + P.eps);
-        if (mine) {
+        if (r.live) {
+            const float norm = sqrtf((float)(ss / (double)K) + P.eps);
+            if (mine) {
+                divide_all<E>(v, norm);
 #pragma unroll
-            for (int j = 0; j < E; ++j) v[j] = (v[j] / norm) * r.w[j];
+                for (int j = 0; j < E; ++j) v[j] = v[j] * r.w[j];
+            }
         }
     }
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < E; ++j) amax = fmaxf(amax, fabsf(v[j]));
-    amax = block_reduce(amax, sm->f, fmax_op, r.live);
-    const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
-    if (mine) scatter_q<E>(v, sc, lq);
+    amax = live_reduce(amax, sm->f, fmax_op, r.live, nlive);
+    float sc = 1.0f;
+    if (r.live) {
+        sc = amax > 0.0f ? amax / 127.0f : 1.0f;
+        qsum_to_slot(mine ? scatter_q<E>(v, sc, lq) : 0, sm, true);
+    }
     return sc;
 }
 
@@ -444,8 +519,9 @@ __device__ __forceinline__ void attn_combine1(const QuantProb& P, const AttnRegs
             for (int j = 0; j < 4; ++j) num[j] += f * r.p[s][j];
             den += f * r.z[s];
         }
+        divide_all<4>(num, den);  // den >= 1: the block holding the maximum adds f = 1 times its sum >= 1
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = num[j] / den;
+        for (int j = 0; j < 4; ++j) v[j] = num[j];
     }
 }
 
@@ -462,15 +538,16 @@ __device__ __forceinline__ float attn_norm1(const QuantProb& P, float (&v)[4], c
     const float norm = sqrtf((float)(ss / (double)K) + P.eps);
     float amax = 0.0f;
     if (mine) {
+        divide_all<4>(v, norm);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            v[j] = (v[j] / norm) * w[j];
+            v[j] = v[j] * w[j];
             amax = fmaxf(amax, fabsf(v[j]));
         }
     }
     amax = block_reduce(amax, sm->f, fmax_op, live);
     const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
-    if (mine) scatter_q<4>(v, sc, lq);
+    qsum_to_slot(mine ? scatter_q<4>(v, sc, lq) : 0, sm, live);
     return sc;
 }
 

@@ -214,14 +214,15 @@ __device__ __forceinline__ void gemv_body(__amdgpu_buffer_rsrc_t rsrc, const int
     }
 }
 
-// The fp32 output of row r of row block rb for one token (M = 1, fp32 output): stored, and
-// returned for the statistics epilogue (0 for rows past N, which are not stored).
-__device__ __forceinline__ float emit1(const GemvProb& P, int rb, int r, int acc, float sx_pro) {
+// The fp32 output of row r of row block rb for one token (M = 1, fp32 output), from the
+// row's residual res_v and scale sw_v loaded beforehand: stored, and returned for the
+// statistics epilogue (0 for rows past N, which are not stored).
+__device__ __forceinline__ float emit1(const GemvProb& P, int rb, int r, int acc, float sx_pro, float res_v,
+                                       float sw_v) {
     const int n = rb * kRowBlock + r;
     if (n >= P.N) return 0.0f;
-    const float sw = P.rs ? P.rs[n] : P.s_w;
-    const float y = ((float)acc * sx_pro) * sw;
-    const float o = P.res ? P.res[n] + y : y;
+    const float y = ((float)acc * sx_pro) * sw_v;
+    const float o = P.res ? res_v + y : y;
     static_cast<float*>(P.out)[n] = o;
     return o;
 }
@@ -411,6 +412,16 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     // attention prologue holds its partials in registers first and issues it after their
     // combine.
     if (PRO != 5 && (PRO != 2 || !early)) gemv_preload<U>(rsrc, lane * 16, cb, A, B, PRO == 0);
+    // one token with a prologue: the residual and scale of wave 0's rows (the epilogue's),
+    // requested now so that the epilogue does not wait for them
+    float res_v = 0.0f, sw_v = P.s_w;
+    if constexpr (MT == 1 && PRO != 0 && !PAIR) {
+        const int n = rb * kRowBlock + lane;
+        if (wave == 0 && n < P.N) {
+            if (P.res) res_v = P.res[n];
+            if (P.rs) sw_v = P.rs[n];
+        }
+    }
     float sx_pro = -1.0f;
     if constexpr (PRO == 5) {
         // the wave's own activations: no barrier between the prologue and the dot products
@@ -477,14 +488,16 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
         }
         return;
     }
-    if (MT == 1 && PRO != 0 && a.stat_out) {  // one token, one problem: outputs and their statistics
+    if (MT == 1 && PRO != 0 && !a.out_i32) {  // one token, fp32 outputs (and their statistics)
         if (threadIdx.x < kRowBlock) {
             const int r = threadIdx.x, n = rb * kRowBlock + r;
             int s = 0;
             for (int w = 0; w < nw; ++w) s += red[w * kRowBlock + r];
-            const float o = emit1(P, rb, r, s, sx_pro);
-            const bool valid = n < P.N;
-            write_row_stats(o, valid ? a.stat_w[n] : 0.0f, valid, a.stat_out, 2 * rb, 2);
+            const float o = emit1(P, rb, r, s, sx_pro, res_v, sw_v);
+            if (a.stat_out) {
+                const bool valid = n < P.N;
+                write_row_stats(o, valid ? a.stat_w[n] : 0.0f, valid, a.stat_out, 2 * rb, 2);
+            }
         }
         return;
     }

@@ -147,6 +147,10 @@ struct rt_plan {
     GemmArgs* dev_gemms = nullptr;   // M > 8: the problems of one grouped launch [G]
     int* dev_tile2p = nullptr;       // M > 64: problem of every tile of that launch
     int gemm_cfg = 0, gemm_tiles = 0;  // M > 64: tile shape, tiles over all problems
+    int gemm_units = 0;              // 8 < M <= 64: workgroups of the split-K launch (parts x row blocks)
+    int* dev_unit2d = nullptr;       // 8 < M <= 64: descriptor of every unit
+    int* gemm_cnt = nullptr;         // split problems: arrivals per row block (zero between launches)
+    int* gemm_ws = nullptr;          // split problems: int32 partial tiles
     std::vector<const rt_act*> acts; // plans over caller-quantised activations
     bool fused = false;              // M = 1, input quantised in the GEMV prologue
     QuantProb pro{};
@@ -517,36 +521,88 @@ int rt_plan_free(rt_plan* plan) {
     if (plan->dev_rb2p) (void)hipFree(plan->dev_rb2p);
     if (plan->dev_gemms) (void)hipFree(plan->dev_gemms);
     if (plan->dev_tile2p) (void)hipFree(plan->dev_tile2p);
+    if (plan->dev_unit2d) (void)hipFree(plan->dev_unit2d);
+    if (plan->gemm_cnt) (void)hipFree(plan->gemm_cnt);
+    if (plan->gemm_ws) (void)hipFree(plan->gemm_ws);
     if (plan->dev_quant) (void)hipFree(plan->dev_quant);
     if (plan->act) (void)hipFree(plan->act);
     delete plan;
     return RT_OK;
 }
 
-// 8 < M <= 64: one split-K launch serves all problems (row blocks numbered as in probs)
 // M > 8: one launch serves all problems.  M <= 64: the split-K kernel, one unit per row
-// block (numbered as in probs).  M > 64: the tile kernel, the tiles of problem g after
-// those of problems 0..g-1, with a tile -> problem table.
+// block and part (upload_splitk_group).  M > 64: the tile kernel, the tiles of problem g
+// after those of problems 0..g-1, with a tile -> problem table.
+// Split-K parts of a problem with C chunks when the group's shortest problem has Cmin: a
+// problem several times longer than the shortest is cut into about C / Cmin parts (at most
+// 8), so that no workgroup walks far more chunks than the others.
+static int splitk_parts(int C, int Cmin) { return std::max(1, std::min(8, (C + Cmin / 2) / std::max(Cmin, 1))); }
+
+static hipError_t upload_splitk_group(rt_plan* p) {
+    const std::vector<GemmArgs>& g = p->gemms;
+    int Cmin = 1 << 30;
+    for (const GemmArgs& a : g) Cmin = std::min(Cmin, a.C);
+    std::vector<GemmArgs> d;  // descriptors: every part of every problem
+    std::vector<int> unit2d;
+    size_t cnt_n = 0, ws_n = 0;
+    std::vector<std::pair<size_t, size_t>> offs(g.size());  // counter, workspace offsets of split problems
+    for (size_t i = 0; i < g.size(); ++i) {
+        const int parts = splitk_parts(g[i].C, Cmin), nrb = g[i].Np / kRowBlock;
+        offs[i] = {cnt_n, ws_n};
+        if (parts > 1) {
+            cnt_n += (size_t)nrb;
+            ws_n += (size_t)parts * nrb * 4096;
+        }
+    }
+    hipError_t e = hipSuccess;
+    if (cnt_n) {
+        e = hipMalloc(&p->gemm_cnt, cnt_n * sizeof(int));
+        if (e == hipSuccess) e = hipMemset(p->gemm_cnt, 0, cnt_n * sizeof(int));
+        if (e == hipSuccess) e = hipMalloc(&p->gemm_ws, ws_n * sizeof(int));
+        if (e != hipSuccess) return e;
+    }
+    for (size_t i = 0; i < g.size(); ++i) {
+        const int parts = splitk_parts(g[i].C, Cmin), nrb = g[i].Np / kRowBlock;
+        for (int kp = 0; kp < parts; ++kp) {
+            GemmArgs a = g[i];
+            a.wg_begin = (int)unit2d.size();
+            a.kp = kp;
+            a.parts = parts;
+            a.c0 = (int)((long long)kp * a.C / parts);
+            a.c1 = (int)((long long)(kp + 1) * a.C / parts);
+            a.cnt = parts > 1 ? p->gemm_cnt + offs[i].first : nullptr;
+            a.part_ws = parts > 1 ? p->gemm_ws + offs[i].second : nullptr;
+            unit2d.insert(unit2d.end(), (size_t)nrb, (int)d.size());
+            d.push_back(a);
+        }
+    }
+    if (unit2d.empty() || unit2d.size() > (1u << 30)) return hipErrorInvalidValue;
+    p->gemm_units = (int)unit2d.size();
+    e = hipMalloc(&p->dev_gemms, sizeof(GemmArgs) * d.size());
+    if (e == hipSuccess) e = hipMemcpy(p->dev_gemms, d.data(), sizeof(GemmArgs) * d.size(), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMalloc(&p->dev_unit2d, sizeof(int) * unit2d.size());
+    if (e == hipSuccess)
+        e = hipMemcpy(p->dev_unit2d, unit2d.data(), sizeof(int) * unit2d.size(), hipMemcpyHostToDevice);
+    return e;
+}
+
 static hipError_t upload_gemm_group(rt_plan* p) {
     if (p->gemms.empty()) return hipSuccess;
+    if (gemm_bm(p->M) == 64) return upload_splitk_group(p);
     std::vector<GemmArgs> g = p->gemms;
     std::vector<int> tile2p;
-    if (gemm_bm(p->M) == 64) {
-        for (size_t i = 0; i < g.size(); ++i) g[i].wg_begin = p->probs[i].wg_begin;
-    } else {
-        std::vector<int> Ns(g.size());
-        for (size_t i = 0; i < g.size(); ++i) Ns[i] = g[i].N;
-        p->gemm_cfg = gemm_tile_cfg(p->M, Ns.data(), (int)g.size());
-        long long total = 0;
-        for (size_t i = 0; i < g.size(); ++i) {
-            g[i].wg_begin = (int)total;
-            const long long n = gemm_tile_count(p->gemm_cfg, p->M, g[i].N);
-            tile2p.insert(tile2p.end(), (size_t)n, (int)i);
-            total += n;
-        }
-        if (total <= 0 || total > (1 << 30)) return hipErrorInvalidValue;
-        p->gemm_tiles = (int)total;
+    std::vector<int> Ns(g.size());
+    for (size_t i = 0; i < g.size(); ++i) Ns[i] = g[i].N;
+    p->gemm_cfg = gemm_tile_cfg(p->M, Ns.data(), (int)g.size());
+    long long total = 0;
+    for (size_t i = 0; i < g.size(); ++i) {
+        g[i].wg_begin = (int)total;
+        const long long n = gemm_tile_count(p->gemm_cfg, p->M, g[i].N);
+        tile2p.insert(tile2p.end(), (size_t)n, (int)i);
+        total += n;
     }
+    if (total <= 0 || total > (1 << 30)) return hipErrorInvalidValue;
+    p->gemm_tiles = (int)total;
     hipError_t e = hipMalloc(&p->dev_gemms, sizeof(GemmArgs) * g.size());
     if (e == hipSuccess) e = hipMemcpy(p->dev_gemms, g.data(), sizeof(GemmArgs) * g.size(), hipMemcpyHostToDevice);
     if (e == hipSuccess && !tile2p.empty()) {
@@ -690,7 +746,7 @@ int rt_plan_describe(const rt_plan* plan, int* kind, int* tile_m, int* tile_n, i
         k = RT_LAUNCH_SPLITK;
         tm = 64;
         tn = kRowBlock;
-        u = plan->total_rb;
+        u = plan->gemm_units;
     } else if (plan->fused || plan->run_pro) {
         k = RT_LAUNCH_GEMV_FUSED;
         const GemvShape sh = plan->fused ? plan->shape : plan->run_shape;
@@ -783,7 +839,7 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
         return RT_OK;
     }
     if (plan->dev_gemms) {
-        RT_HIP(launch_gemm_group(plan->dev_gemms, plan->dev_rb2p, plan->total_rb, ctx->stream));
+        RT_HIP(launch_gemm_group(plan->dev_gemms, plan->dev_unit2d, plan->gemm_units, ctx->stream));
         return RT_OK;
     }
     RT_HIP(launch_gemv(a, plan->mt, plan->shape, ctx->stream));

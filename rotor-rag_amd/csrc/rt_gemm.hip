@@ -159,8 +159,9 @@ typedef __attribute__((address_space(4))) const int cidx_g;
 __device__ __forceinline__ GemmArgs find_gemm(const GemmGroupArgs& ga, int b) {
     if (!ga.dev) return ga.one;
     const cgemm* q = (cgemm*)ga.dev + ((cidx_g*)ga.rb2p)[b];
-    return GemmArgs{q->w, q->qx, q->sx, q->rs, q->out, q->s_w, q->M, q->N, q->Np, q->C, q->ldo, q->out_i32, q->res,
-                    q->wg_begin};
+    return GemmArgs{q->w,  q->qx,       q->sx, q->rs, q->out, q->s_w, q->M,     q->N,   q->Np,
+                    q->C,  q->ldo,      q->out_i32, q->res, q->wg_begin, q->c0, q->c1, q->kp, q->parts,
+                    q->cnt, q->part_ws};
 }
 
 template <int BM, int BN, int WAVES_M, int STAGES>
@@ -325,8 +326,9 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmGroupArgs ga) {
 }
 
 // ---- M <= 64: K split over the waves ------------------------------------------------
-// One workgroup per 64-column tile of the output and all (<= 64) rows; wave w of NW
-// covers chunks [w C / NW, (w + 1) C / NW).  Each wave fills a private LDS ring of S
+// One workgroup per 64-column tile of the output and all (<= 64) rows, over the unit's
+// chunks (a part of a long-K problem, GemmArgs::parts, or all C); wave w of NW covers an
+// NW-th of them.  Each wave fills a private LDS ring of S
 // stages by direct loads (4 A blocks + 1 weight chunk per step, S - 1 steps ahead) and
 // needs no barrier inside its loop: s_waitcnt on its own loads publishes a stage to
 // itself.  The NW int32 partial tiles are then summed in LDS (exact) and one pass
@@ -347,9 +349,11 @@ __global__ void __launch_bounds__(NW * 64) gemm_splitk_kernel(GemmGroupArgs ga) 
     const int t = threadIdx.x, lane = t & 63, g = lane >> 5, r32 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const GemmArgs a = find_gemm(ga, blockIdx.x);
-    const int C = a.C, n0 = ((int)blockIdx.x - a.wg_begin) * kRowBlock;
-    const int cb = __builtin_amdgcn_readfirstlane((wave * C) / NW);
-    const int ce = __builtin_amdgcn_readfirstlane(((wave + 1) * C) / NW);
+    const int C = a.C, rb = (int)blockIdx.x - a.wg_begin, n0 = rb * kRowBlock;
+    // this unit's chunks (one part of a split problem, or all), split over the waves
+    const int k0 = a.c1 > 0 ? a.c0 : 0, len = (a.c1 > 0 ? a.c1 : C) - k0;
+    const int cb = k0 + __builtin_amdgcn_readfirstlane((wave * len) / NW);
+    const int ce = k0 + __builtin_amdgcn_readfirstlane(((wave + 1) * len) / NW);
     char* const ring = lds_b + wave * S * STAGE;
     const int8_t* a_src = a.qx + (size_t)lane * 16;  // block f of chunk c at (f C + c) KiB
     const v4u* w_src = a.w + (size_t)(n0 / kRowBlock) * C * kRowBlock + lane;
@@ -418,6 +422,36 @@ __global__ void __launch_bounds__(NW * 64) gemm_splitk_kernel(GemmGroupArgs ga) 
         for (int w = 0; w < NW; ++w) acc_e += reinterpret_cast<const int*>(lds_b + w * S * STAGE)[e];
         v[j] = acc_e;
     }
+    if (a.parts > 1) {  // one part of a split problem: publish the tile; the last part adds them up
+        // The tiles and the count are device-scope (coherent across the XCDs) stores and loads
+        // rather than plain ones behind fences: a device-scope fence writes back and
+        // invalidates the whole L2 of the XCD (the launch took 33 instead of 19 us).  Each
+        // wave's tile stores have completed (s_waitcnt) before the barrier that precedes the
+        // count, so the part that sees the final count reads complete tiles.  The flag lives in
+        // the ring past wave 0's partial tile (a static LDS variable would push two
+        // workgroups past a CU's 160 KiB).
+        int& last = *reinterpret_cast<int*>(lds_b + S * STAGE - 4);
+        const size_t tile = (size_t)(a.Np / kRowBlock) * 4096;  // one part's tiles
+        int* mine = a.part_ws + a.kp * tile + (size_t)rb * 4096;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j)
+            __hip_atomic_store(mine + (mb + NW * j) * 64 + lane, v[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t == 0)
+            last = __hip_atomic_fetch_add(a.cnt + rb, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == a.parts - 1;
+        __syncthreads();
+        if (!last) return;
+        for (int p = 0; p < a.parts; ++p) {
+            if (p == a.kp) continue;
+            const int* other = a.part_ws + p * tile + (size_t)rb * 4096;
+#pragma unroll
+            for (int j = 0; j < EPT; ++j)
+                v[j] += __hip_atomic_load(other + (mb + NW * j) * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // every part of this row block has arrived: the count is ready for the next launch
+        if (t == 0) __hip_atomic_store(a.cnt + rb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     const unsigned range = (unsigned)a.M * (unsigned)a.ldo * 4u;
     const __amdgpu_buffer_rsrc_t out = __builtin_amdgcn_make_buffer_rsrc(a.out, 0, range, kBufDword3);
     const int coff = (int)((unsigned)n * 4u + ((unsigned)(n >= a.N) << 31));
@@ -449,7 +483,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_splitk_kernel(GemmGroupArgs ga) 
 template <int NW, int S>
 static hipError_t launch_splitk(const GemmGroupArgs& ga, int blocks, hipStream_t s) {
     constexpr int LDS = NW * S * (5 * 1024);
-    static_assert(S * 5 * 1024 >= 64 * 64 * 4, "a wave's ring must hold its partial tile");
+    static_assert(S * 5 * 1024 >= 64 * 64 * 4 + 4, "a wave's ring must hold its partial tile (and wave 0's the arrival flag)");
     if (LDS > 65536) {
         static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_splitk_kernel<NW, S>),
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, LDS);

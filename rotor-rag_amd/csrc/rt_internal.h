@@ -199,6 +199,14 @@ struct GemmArgs {
     int M, N, Np, C, ldo, out_i32;
     const float* res;    // optional fp32 [M][ldo] added to y (may alias out)
     int wg_begin;        // grouped launches: first global row block of this problem
+    // Split-K launches (M <= 64) may cut a long-K problem into `parts` descriptors, part kp
+    // covering chunks [c0, c1) (c1 == 0: all C, unsplit).  Each part's workgroup stores its
+    // int32 64 x 64 tile in part_ws [parts][row blocks][64][64] and counts its arrival in
+    // cnt [row blocks]; the last part of a row block sums the tiles, applies the epilogue
+    // and resets the count to 0 for the next launch.
+    int c0, c1, kp, parts;
+    int* cnt;
+    int* part_ws;
 };
 
 constexpr int kBufDword3 = 0x00020000;  // buffer resource word 3 for gfx9 raw buffers

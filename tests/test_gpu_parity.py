@@ -162,14 +162,16 @@ def test_ternary_matmul_duck_type(hip):
 
 # launch each plan of test_plan_matches_single_calls makes: (kind, tile_m, tile_n, workgroups)
 # (two distinct inputs at M = 1: the GEMV runs after a quantiser launch, 16-wave K split)
-PLAN_LAUNCH = {1: (0, 1, 64, 100), 16: (2, 64, 64, 100), 37: (2, 64, 64, 100), 64: (2, 64, 64, 100),
+PLAN_LAUNCH = {1: (0, 1, 64, 100), 16: (2, 64, 64, 180), 37: (2, 64, 64, 180), 64: (2, 64, 64, 180),
                130: (3, 64, 128, 150), 300: (3, 128, 128, 150), 600: (3, 192, 128, 200)}
 
 
 @pytest.mark.parametrize("M", [1, 16, 37, 64, 130, 300, 600])
 def test_plan_matches_single_calls(hip, M):
-    """A plan launches its problems together: one grid over all row blocks for M <= 64, one
-    grid over all tiles above (M = 130: 64 x 128 tiles, M = 300: 128 x 128, M = 600: 192 x 128,
+    """A plan launches its problems together: one grid over all row blocks for M <= 64 (the
+    K = 6912 problem cut into 3 parts of about the other problems' 40 chunks, combined by
+    the last part of each row block; replayed, which needs its counters reset), one grid
+    over all tiles above (M = 130: 64 x 128 tiles, M = 300: 128 x 128, M = 600: 192 x 128,
     as rt_plan_describe reports), while the single calls pick their own shapes."""
     import torch
 

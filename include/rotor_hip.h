@@ -75,7 +75,7 @@ const char* rt_last_error(void);
 
 /* ABI version (major*100 + minor): 101 = 100 + rt_plan_create_gate_up and RT_SRC_RMSNORM_SSQ;
  * 102 = 101 + rt_plan_describe; 103 = 102 + rt_linear_f32_noalloc; 104 = 103 + rt_plan_set_row_stats
- * and RT_SRC_RMSNORM_STATS. */
+ * and RT_SRC_RMSNORM_STATS; 105 = 104 + rt_plan_attach_attention and rt_plan_attention_timeouts. */
 int rt_version(void);
 
 /* Number of visible HIP devices (0 when none); RT_OK even when 0. */
@@ -259,6 +259,25 @@ int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, fl
  * detaches.  Fuses the norm statistics of the next RMSNorm (src/rotor/transformer.py:24-36)
  * into the linear that produces its input (:329-339, :396-411). */
 int rt_plan_set_row_stats(rt_plan* plan, const float* next_norm_w, void* stats);
+
+/* Run the decode step's RoPE + KV append + attention partials (rt_rope_attention_decode
+ * with out = NULL, same arguments, same results bit for bit) inside rt_plan_run's launch of
+ * a fused q/k/v plan: rt_plan_create_fused with G = 3 over the q, k and v projections
+ * (outputs q [H*hd], k and v [Hkv*hd] in that order), an RT_SRC_QUANT or RT_SRC_RMSNORM
+ * source with K % 64 == 0, hd = 128 and H / Hkv = 4 (the plan's workgroups hold one
+ * 256-thread tile per query head of a KV group).  The attention workgroups follow the
+ * GEMV's in the grid and start on a KV group as soon as its q, k and v rows are stored
+ * (a device-side arrival count; the wait is bounded).  k_cache = NULL detaches.  The
+ * pointers are kept: the caches, rope, pos and workspace must outlive the plan's runs.
+ * Replaces, for one token, src/rotor/transformer.py:250-281 after the projections
+ * :235-237. */
+int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, const float* rope, int H, int Hkv,
+                             int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes);
+/* Number of attention waits of the plan's launches that gave up (never expected; the
+ * results of such a launch are wrong).  Synchronises the device; a non-zero count also
+ * clears the plan's arrival counts.  No counterpart in the reference (its attention runs
+ * after the projections on the host). */
+int rt_plan_attention_timeouts(rt_plan* plan, int* count);
 
 /* ---- kernels around the linears for BitNet-2B-shape inference ----------------------
  * Positions are read from device memory (`pos`: position of the first of the M tokens)

@@ -167,6 +167,12 @@ struct rt_plan {
     RowStat* stat_out = nullptr;  // rt_plan_set_row_stats: the epilogue's statistics records
     const float* stat_w = nullptr;  // and the next RMSNorm's weight they are taken against
     int quant_maxK = 0;  // > 0: every quant problem takes the vectorised row kernel (largest K)
+    // rt_plan_attach_attention: the decode attention partials run in rt_plan_run's launch
+    bool att_on = false;
+    AttnTail att{};
+    int att_Hkv = 0, att_hd = 0;
+    void* att_mem = nullptr;  // tagged outputs, epoch, done, err
+    size_t att_bytes = 0;
 };
 
 struct rt_act {
@@ -186,7 +192,7 @@ extern "C" {
 
 const char* rt_last_error(void) { return g_err.c_str(); }
 
-int rt_version(void) { return 104; }
+int rt_version(void) { return 105; }
 
 int rt_device_count(int* n) {
     if (!n) return fail(RT_EINVAL, "rt_device_count: n is NULL");
@@ -526,6 +532,7 @@ int rt_plan_free(rt_plan* plan) {
     if (plan->gemm_ws) (void)hipFree(plan->gemm_ws);
     if (plan->dev_quant) (void)hipFree(plan->dev_quant);
     if (plan->act) (void)hipFree(plan->act);
+    if (plan->att_mem) (void)hipFree(plan->att_mem);
     delete plan;
     return RT_OK;
 }
@@ -842,7 +849,10 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
         RT_HIP(launch_gemm_group(plan->dev_gemms, plan->dev_unit2d, plan->gemm_units, ctx->stream));
         return RT_OK;
     }
-    RT_HIP(launch_gemv(a, plan->mt, plan->shape, ctx->stream));
+    if (plan->att_on)
+        RT_HIP(launch_gemv_attn(a, plan->att, plan->att_Hkv, plan->att_hd, plan->shape, ctx->stream));
+    else
+        RT_HIP(launch_gemv(a, plan->mt, plan->shape, ctx->stream));
     return RT_OK;
 }
 
@@ -1225,6 +1235,91 @@ int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, fl
     p->pair_g = g_out;
     p->pair_u = u_out;
     *out = p;
+    return RT_OK;
+}
+
+// The device state of the attention partials in a qkv launch: the tagged outputs (zero),
+// then the epoch (1), the done count and the error count (0).
+static hipError_t attention_state_reset(rt_plan* plan) {
+    hipError_t e = hipMemset(plan->att_mem, 0, plan->att_bytes);
+    const unsigned one = 1;
+    if (e == hipSuccess) e = hipMemcpy(plan->att.epoch, &one, sizeof(one), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    return e;
+}
+
+int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, const float* rope, int H, int Hkv,
+                             int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes) {
+    const char* who = "rt_plan_attach_attention";
+    if (!plan) return fail(RT_EINVAL, std::string(who) + ": plan is NULL");
+    if (!k_cache) {  // detach
+        plan->att_on = false;
+        return RT_OK;
+    }
+    if (!v_cache || !rope || !pos || !workspace) return fail(RT_EINVAL, std::string(who) + ": NULL argument");
+    int rc = check_heads(H, Hkv, hd, Lmax, who);
+    if (rc) return rc;
+    if (hd != 128) return fail(RT_EINVAL, std::string(who) + ": head_dim must be 128");
+    if (workspace_bytes < rt_attention_decode_workspace(H, hd, Lmax))
+        return fail(RT_EINVAL, std::string(who) + ": workspace too small");
+    if (!plan->fused || plan->G != 3 || plan->pair_a || plan->stat_out)
+        return fail(RT_EINVAL, std::string(who) + ": needs a fused decode plan of the q, k and v projections "
+                                                  "(rt_plan_create_fused, G = 3, RMSNorm or absmax source)");
+    const int Gq = H / Hkv;
+    if (plan->probs[0].N != H * hd || plan->probs[1].N != Hkv * hd || plan->probs[2].N != Hkv * hd)
+        return fail(RT_EINVAL, std::string(who) + ": the plan's outputs must be q [H * hd], k and v [Hkv * hd]");
+    if (64 * plan->shape.nw != 256 * Gq)
+        return fail(RT_EINVAL, std::string(who) + ": the plan's workgroups must hold one 256-thread attention tile "
+                                                  "per query head of a KV group (H / Hkv = 4 for this plan)");
+    const QuantProb& P = plan->pro;
+    if (P.mode == kRmsNormStats || P.mode == kAttnNorm || P.K % 64 ||
+        vec_elements(P.K, 64 * plan->shape.nw) == 0 || ((uintptr_t)P.x & 15u) || ((uintptr_t)P.aux & 15u))
+        return fail(RT_EINVAL, std::string(who) + ": the plan's source must be a 16-byte aligned row with K % 64 == 0");
+    DeviceGuard g(plan->device);
+    const size_t words = (size_t)(H + 2 * Hkv) * hd;
+    const size_t bytes = words * sizeof(unsigned long long) + 256;
+    if (plan->att_mem && plan->att_bytes != bytes) {
+        RT_HIP(hipDeviceSynchronize());
+        RT_HIP(hipFree(plan->att_mem));
+        plan->att_mem = nullptr;
+    }
+    if (!plan->att_mem) RT_HIP(hipMalloc(&plan->att_mem, bytes));
+    plan->att_bytes = bytes;
+    AttnTail& t = plan->att;
+    t.tagged = static_cast<unsigned long long*>(plan->att_mem);
+    int* tail = reinterpret_cast<int*>(t.tagged + words);
+    t.epoch = reinterpret_cast<unsigned*>(tail);
+    t.done = tail + 1;
+    t.err = tail + 2;
+    RT_HIP(attention_state_reset(plan));
+    t.Kc = k_cache;
+    t.Vc = v_cache;
+    t.rope = rope;
+    t.pos = pos;
+    t.work = static_cast<float*>(workspace);
+    t.Gq = Gq;
+    t.Lmax = Lmax;
+    t.S = attn_splits(Lmax);
+    t.qrows = H * hd;
+    t.nkv = Hkv * hd;
+    t.scale = 1.0f / sqrtf((float)hd);
+    plan->att_Hkv = Hkv;
+    plan->att_hd = hd;
+    plan->att_on = true;
+    return RT_OK;
+}
+
+int rt_plan_attention_timeouts(rt_plan* plan, int* count) {
+    const char* who = "rt_plan_attention_timeouts";
+    if (!plan || !count) return fail(RT_EINVAL, std::string(who) + ": NULL argument");
+    *count = 0;
+    if (!plan->att_mem) return RT_OK;
+    DeviceGuard g(plan->device);
+    RT_HIP(hipDeviceSynchronize());
+    int err = 0;
+    RT_HIP(hipMemcpy(&err, plan->att.err, sizeof(int), hipMemcpyDeviceToHost));
+    if (err) RT_HIP(attention_state_reset(plan));  // a wait gave up: start again from a clean state
+    *count = err;
     return RT_OK;
 }
 

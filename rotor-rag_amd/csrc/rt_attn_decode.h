@@ -1,0 +1,204 @@
+// Decode attention over one block of 64 keys for one query head: the work of a
+// 256-thread tile, shared by the split-L attention kernel (rt_model.hip) and by the qkv
+// GEMV launch that runs the attention partials in its trailing workgroups (rt_gemv.hip).
+//
+// Reference: MultiHeadAttention.forward (src/rotor/transformer.py:206-292: KV concat
+// :250-252, GQA repeat :260-263, scores/softmax/AV :267-281); this build adds RoPE and a
+// causal mask (the benchmark configuration).
+//
+// The tile (h, s) handles keys [64 s, 64 s + 64) of query head h for the single query at
+// position pos and writes a partial result wp[0..HD+2): the unnormalised output
+// sum_j e^(s_j - m) V_j (HD values), the block maximum m and the sum of exponentials z
+// (m = -inf, z = 0 for an empty block).  The partials are combined by attn_combine_kernel
+// or by the prologue of the o_proj GEMV (rt_rowquant.h, kAttnNorm); both use
+// attn_combine_element, so the two give identical values.
+#pragma once
+
+#include "rt_internal.h"
+
+namespace rt {
+
+constexpr int kAttnBlock = 64;  // keys per split
+
+template <int HD>
+struct AttnTileLds {
+    float qs[HD];
+    float ks[HD];
+    float vs[HD];
+    float part[4][kAttnBlock];
+    float pr[kAttnBlock];
+    float ored[256];
+};
+
+// The tile's LDS is reached through a local-address-space pointer: through a generic one,
+// a select between an LDS value and a register of the key block (the new key) becomes a
+// load through a selected generic pointer, which puts the key block in scratch memory.
+template <int HD>
+using AttnLdsPtr = __attribute__((address_space(3))) AttnTileLds<HD>*;
+
+// A thread's share of its key block, loaded before anything else (the keys and values do
+// not depend on the position): wave w of the tile holds dims [w HD/4, (w+1) HD/4) of key
+// j0 + lane; thread (d, g) = (t % HD, t / HD) value dim d of keys g, g + G, .. (G = 256 / HD).
+// Keys past Lmax re-read the last cached key; keys past the position are masked later.
+template <int HD>
+struct AttnKV {
+    static constexpr int G = 256 / HD, KD = HD / 4, VN = kAttnBlock / G;
+    float k[KD];
+    float v[VN];
+};
+
+template <int HD>
+__device__ __forceinline__ void attn_kv_load(const float* __restrict__ Kc, const float* __restrict__ Vc, int kh, int j0,
+                                             int Lmax, int t, AttnKV<HD>& kv) {
+    using KV = AttnKV<HD>;
+    const int lane = t & 63, wave = t >> 6, d = t % HD, g = t / HD;
+    const float* K = Kc + (size_t)kh * HD * Lmax + min(j0 + lane, Lmax - 1);
+#pragma unroll
+    for (int i = 0; i < KV::KD; ++i) kv.k[i] = K[(size_t)(wave * KV::KD + i) * Lmax];
+    const float* V = Vc + (size_t)kh * Lmax * HD + d;
+#pragma unroll
+    for (int i = 0; i < KV::VN; ++i) kv.v[i] = V[(size_t)min(j0 + g + i * KV::G, Lmax - 1) * HD];
+}
+
+// The RoPE factors (cos, sin) of rotation pair t (t < HD / 2) at position pos: loaded by
+// the caller as early as the position is known (the tile's first step waits for them).
+template <int HD>
+__device__ __forceinline__ void attn_rope_load(const float* __restrict__ rope, int pos, int t, float& c, float& sn) {
+    c = sn = 0.0f;
+    if (t < HD / 2) {
+        const float* cs = rope + (size_t)pos * HD + 2 * t;
+        c = cs[0];
+        sn = cs[1];
+    }
+}
+
+// The tile's work once the position is known and the block holds at least one key
+// (pos >= j0).  Every thread of the workgroup passes the tile's three barriers.
+// qh: the head's query (HD values); kn, vn: the head's KV group's new key and value (ROPE),
+// in global memory or in LDS (SRC, a pointer type); c, sn: attn_rope_load's factors (ROPE).
+// ROPE: qh, kn, vn are the raw projection outputs of the token at pos.  The tile rotates
+// its head's q (the arithmetic of rope_append_kernel); the tile whose block holds position
+// pos takes that key and value from LDS (rotated kn, vn) instead of the cache, in the same
+// summation order, and, when `writer` (the first query head of its KV group), writes them
+// into the caches of KV head kh for the later steps.  Without ROPE, qh is already rotated
+// and the caches hold the new key.
+template <int HD, bool ROPE, typename SRC>
+__device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float sn, float* __restrict__ Kc,
+                                          float* __restrict__ Vc, int kh, bool writer, int Lmax, int pos, int j0,
+                                          float scale, float* __restrict__ wp, int t, AttnLdsPtr<HD> sm,
+                                          const AttnKV<HD>& kv) {
+#pragma clang fp contract(off)  // every product and sum rounds on its own
+    static_assert(HD / 2 <= 256, "one rotation pair per thread");
+    using KV = AttnKV<HD>;
+    constexpr int BL = kAttnBlock, half = HD / 2, G = KV::G, KD = KV::KD, VN = KV::VN;
+    const int lane = t & 63, wave = t >> 6, d = t % HD, g = t / HD;
+    const int nk = min(BL, pos + 1 - j0);          // keys of this block (>= 1)
+    const bool holds_new = ROPE && pos < j0 + BL;  // this block ends with the new key
+    const int lp = pos - j0;                       // its lane / key index in the block
+    if (ROPE) {
+        if (t < half) {
+            const int i = t;
+            const float x1 = qh[i], x2 = qh[i + half];
+            sm->qs[i] = x1 * c - x2 * sn;
+            sm->qs[i + half] = x2 * c + x1 * sn;
+            if (holds_new) {
+                const float k1 = kn[i], k2 = kn[i + half];
+                sm->ks[i] = k1 * c - k2 * sn;
+                sm->ks[i + half] = k2 * c + k1 * sn;
+            }
+        }
+        if (holds_new)
+            for (int e = t; e < HD; e += 256) sm->vs[e] = vn[e];
+    } else {
+        for (int e = t; e < HD; e += 256) sm->qs[e] = qh[e];
+    }
+    __syncthreads();
+    if (holds_new && writer)  // one writer per KV head
+        for (int e = t; e < HD; e += 256) {
+            Kc[((size_t)kh * HD + e) * Lmax + pos] = sm->ks[e];
+            Vc[((size_t)kh * Lmax + pos) * HD + e] = sm->vs[e];
+        }
+    // scores: wave w sums its dims for key j0 + lane (the new key from LDS: the one lane
+    // that holds it takes its dims first, in a branch that every other wave skips).
+    // Branch-free otherwise: every lane computes (keys past the block's last are discarded
+    // by the softmax's mask), so the LDS reads go out together.
+    float kk[KD];
+#pragma unroll
+    for (int i = 0; i < KD; ++i) kk[i] = kv.k[i];
+    if (holds_new && lane == lp) {
+#pragma unroll
+        for (int i = 0; i < KD; ++i) kk[i] = sm->ks[wave * KD + i];
+    }
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int i = 0; i < KD; i += 4) {
+        const int dd = wave * KD + i;
+        a0 += sm->qs[dd + 0] * kk[i + 0];
+        a1 += sm->qs[dd + 1] * kk[i + 1];
+        a2 += sm->qs[dd + 2] * kk[i + 2];
+        a3 += sm->qs[dd + 3] * kk[i + 3];
+    }
+    sm->part[wave][lane] = (a0 + a1) + (a2 + a3);
+    __syncthreads();
+    if (wave == 0) {
+        float sc = lane < nk
+                       ? (((sm->part[0][lane] + sm->part[1][lane]) + (sm->part[2][lane] + sm->part[3][lane])) * scale)
+                       : -INFINITY;
+        const float mx = lane63(wave_reduce63(sc, -INFINITY, [](float x, float y) { return fmaxf(x, y); }));
+        const float p = lane < nk ? expf(sc - mx) : 0.0f;
+        const float z = wave_reduce63(p, 0.0f, [](float x, float y) { return x + y; });
+        sm->pr[lane] = p;
+        if (lane == 63) {
+            wp[HD] = mx;
+            wp[HD + 1] = z;
+        }
+    }
+    __syncthreads();
+    // unnormalised output: thread (d, g) sums keys g, g + G, ... of the block, two
+    // alternating partial sums.  The new key's value and the mask of keys past the
+    // block's last cost VALU work only in the block that needs them (both conditions are
+    // uniform over the workgroup): four tiles share a CU in the qkv launch, where this
+    // loop is VALU-bound.  No branches inside: the LDS reads go out together.
+    float vv[VN];
+#pragma unroll
+    for (int i = 0; i < VN; ++i) vv[i] = kv.v[i];
+    if (holds_new) {
+        const float vs_d = sm->vs[d];
+#pragma unroll
+        for (int i = 0; i < VN; ++i) vv[i] = g + i * G == lp ? vs_d : vv[i];
+    }
+    float o0 = 0.f, o1 = 0.f;
+    if (nk == BL) {
+#pragma unroll
+        for (int i = 0; i < VN; i += 2) {
+            o0 += sm->pr[g + i * G] * vv[i];
+            o1 += sm->pr[g + (i + 1) * G] * vv[i + 1];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < VN; i += 2) {
+            const int ja = g + i * G, jb = g + (i + 1) * G;
+            const float sa = o0 + sm->pr[ja] * vv[i], sb = o1 + sm->pr[jb] * vv[i + 1];
+            o0 = ja < nk ? sa : o0;
+            o1 = jb < nk ? sb : o1;
+        }
+    }
+    sm->ored[t] = o0 + o1;
+    __syncthreads();
+    if (g == 0) {
+        float o = sm->ored[d];
+        for (int gg = 1; gg < G; ++gg) o += sm->ored[gg * HD + d];
+        wp[d] = o;
+    }
+}
+
+// The partial of an empty block (no key at or before the position).
+template <int HD>
+__device__ __forceinline__ void attn_tile_empty(float* __restrict__ wp, int t) {
+    if (t == 0) {
+        wp[HD] = -INFINITY;
+        wp[HD + 1] = 0.0f;
+    }
+}
+
+}  // namespace rt

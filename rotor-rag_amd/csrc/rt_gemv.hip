@@ -31,6 +31,7 @@
 #include <type_traits>
 
 #include "rt_rowquant.h"
+#include "rt_attn_decode.h"
 
 // every fp32 operation rounds on its own, as the reference restatement computes them
 #pragma clang fp contract(off)
@@ -321,10 +322,27 @@ constexpr int kAttnMaxThreads = 640;
 // workgroup's row block holds both inputs of 32 outputs: it writes the FFN activation
 // a = relu(g)^2 * u of those 32 (g and u rounded as emit rounds y) and their f64 sum of
 // squares, the two inputs of the down projection's sub-norm.
-template <int MT, int PRO, bool PAIR = false>
+// Tail = AttnTail (M = 1, fp32 outputs): the attention partials of the token run in the
+// same launch (qkv_attn_block): the GEMV's outputs are stored device-coherent and, once
+// they are written, the workgroup adds one to the arrival count of its KV group.
+struct NoTail {};
+template <int HD>
+__device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb);
+template <int MT, int PRO, bool PAIR = false, typename Tail = NoTail>
 __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     gemv_ksplit_kernel(const float* pro_x, const float* pro_aux, const float* pro_aux2, int pro_K, int pro_mode,
-                       float pro_eps, unsigned shape, unsigned nw_m, const v4u* w1, GemvArgs a) {
+                       float pro_eps, unsigned shape, unsigned nw_m, const v4u* w1, GemvArgs a, Tail at) {
+    constexpr bool SIG = std::is_same<Tail, AttnTail>::value;
+    if constexpr (SIG) {
+        // the GEMV's workgroup count rides in the shape word (a launch of inline problems
+        // has no C1), so the GEMV workgroups start without a kernel-argument load
+        static_assert(MT == 1 && !PAIR, "attention partials follow the one-token qkv GEMV");
+        const int total_rb = (int)(shape >> 8);
+        if ((int)blockIdx.x >= total_rb) {
+            qkv_attn_block<128>(at, total_rb);
+            return;
+        }
+    }
     // The prologue source's fields, the launch shape word (waves per workgroup nw in bits
     // 0-4, inline problem count in bits 5-7, the chunks per row C1 of a one-problem launch
     // from bit 8), nw_m = ceil(2^31 / nw) and the weight tiles w1 of a one-problem launch
@@ -422,6 +440,16 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
             if (P.rs) sw_v = P.rs[n];
         }
     }
+    // the tagged copy of the outputs: its address and the launch's epoch are read now, while
+    // the prologue's row is in flight, and kept in SGPRs (read in the epilogue, the kernel
+    // argument and the epoch would cost two memory latencies there)
+    unsigned long long* tagged = nullptr;
+    unsigned long long tag = 0;
+    if constexpr (SIG) {
+        tagged = at.tagged + (size_t)blockIdx.x * kRowBlock;
+        tag = (unsigned long long)__hip_atomic_load(at.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) << 32;
+        asm volatile("" ::"s"(tagged), "s"(tag));
+    }
     float sx_pro = -1.0f;
     if constexpr (PRO == 5) {
         // the wave's own activations: no barrier between the prologue and the dot products
@@ -494,7 +522,10 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
             int s = 0;
             for (int w = 0; w < nw; ++w) s += red[w * kRowBlock + r];
             const float o = emit1(P, rb, r, s, sx_pro, res_v, sw_v);
-            if (a.stat_out) {
+            if constexpr (SIG) {
+                // rows past N are not read (every problem of a joint launch has N % 64 == 0)
+                __hip_atomic_store(tagged + r, tag | __float_as_uint(o), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else if (a.stat_out) {
                 const bool valid = n < P.N;
                 write_row_stats(o, valid ? a.stat_w[n] : 0.0f, valid, a.stat_out, 2 * rb, 2);
             }
@@ -506,6 +537,69 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
         int s = 0;
         for (int w = 0; w < nw; ++w) s += red[(w * MT + m) * kRowBlock + r];
         emit(a, P, rb, m0, m, r, s, sx_pro);
+    }
+}
+
+// Decode qkv GEMV (E-element RMSNorm prologue) with the attention partials of the token in
+// the same launch: workgroups [0, total_rb) are the GEMV's row blocks (q, k, v problems),
+// the following Hkv * S workgroups the attention of (KV head kh, key block s), kh slowest,
+// each of Gq 256-thread tiles (the Gq query heads of kh; blockDim = 256 Gq).  An attention
+// workgroup issues its key block's loads and reads the position and the epoch; when its
+// block holds a key, its first (Gq + 2) hd threads (one per q, k and v value of its KV
+// group) poll the GEMV's tagged outputs (bounded) until each carries the epoch and leave
+// the values in LDS, and the tiles of rt_attn_decode.h run on them.  Forward
+// progress: the attention workgroups wait only for GEMV workgroups, which come first in
+// the grid and never wait.
+template <int HD>
+__device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb) {
+    extern __shared__ __attribute__((aligned(16))) int red[];
+    const AttnLdsPtr<HD> sm = (AttnLdsPtr<HD>)red;
+    typedef __attribute__((address_space(3))) float lfl;
+    lfl* const qkv = (lfl*)(sm + at.Gq);  // the group's q (Gq HD), k (HD), v (HD)
+    const int i = (int)blockIdx.x - total_rb;
+    const int kh = i / at.S, s = i - kh * at.S;
+    const int sub = (int)(threadIdx.x >> 8), t = (int)(threadIdx.x & 255), h = kh * at.Gq + sub;
+    const int j0 = s * kAttnBlock;
+    const int nin = (at.Gq + 2) * HD;
+    AttnKV<HD> kv;
+    attn_kv_load<HD>(at.Kc, at.Vc, kh, j0, at.Lmax, t, kv);
+    const unsigned ep = __hip_atomic_load(at.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int pos = *at.pos;
+    float* wp = at.work + ((size_t)h * at.S + s) * (HD + 2);
+    const bool live = pos >= j0;
+    if (live) {
+        float c, sn;
+        attn_rope_load<HD>(at.rope, pos, t, c, sn);
+        const int e = (int)threadIdx.x;
+        if (e < nin) {  // waves whose lanes all hold a value of the group (nin % 64 == 0)
+            const int g = e < at.Gq * HD ? kh * at.Gq * HD + e
+                                         : at.qrows + (e < (at.Gq + 1) * HD ? 0 : at.nkv) + kh * HD +
+                                               (e - at.Gq * HD) % HD;
+            unsigned it = 0;
+            unsigned long long w;
+            while (true) {
+                w = __hip_atomic_load(at.tagged + g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (__all((unsigned)(w >> 32) == ep)) break;
+                if (++it > kAttnSpinLimit) {  // never expected: counted, and the launch goes on
+                    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(at.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            qkv[e] = __uint_as_float((unsigned)w);
+        }
+        __syncthreads();
+        attn_tile<HD, true>(qkv + sub * HD, qkv + at.Gq * HD, qkv + (at.Gq + 1) * HD, c, sn, at.Kc, at.Vc, kh,
+                            sub == 0, at.Lmax, pos, j0, at.scale, wp, t, sm + sub, kv);
+    } else {
+        attn_tile_empty<HD>(wp, t);
+    }
+    // the last attention workgroup of the launch (every other one is past its reads) resets
+    // the count and advances the epoch
+    if (threadIdx.x == 0 &&
+        __hip_atomic_fetch_add(at.done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - total_rb - 1) {
+        __hip_atomic_store(at.done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(at.epoch, ep + 1 == 0 ? 1u : ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -563,7 +657,7 @@ static void launch_ksplit(dim3 grid, int nw, size_t lds, hipStream_t s, const Ge
     const bool one = a.ninl == 1;
     const unsigned shape = (unsigned)nw | ((unsigned)a.ninl << 5) | (one ? (unsigned)a.inl[0].C << 8 : 0u);
     hipLaunchKernelGGL((gemv_ksplit_kernel<MT, PRO, PAIR>), grid, dim3((unsigned)(64 * nw)), lds, s, P.x, P.aux, P.aux2,
-                       P.K, P.mode, P.eps, shape, nw_reciprocal(nw), one ? a.inl[0].w : nullptr, a);
+                       P.K, P.mode, P.eps, shape, nw_reciprocal(nw), one ? a.inl[0].w : nullptr, a, NoTail{});
 }
 
 hipError_t launch_gemv(const GemvArgs& args, int mt, GemvShape shape, hipStream_t s) {
@@ -637,6 +731,42 @@ hipError_t launch_gemv(const GemvArgs& args, int mt, GemvShape shape, hipStream_
             default: return hipErrorInvalidValue;
         }
     }
+    return hipGetLastError();
+}
+
+template <int PRO>
+static void launch_qkv_attn(dim3 grid, int nw, size_t lds, hipStream_t s, const GemvArgs& a, const AttnTail& at) {
+    const QuantProb& P = a.pro;
+    const unsigned shape = (unsigned)nw | ((unsigned)a.ninl << 5) | ((unsigned)a.total_rb << 8);
+    hipLaunchKernelGGL((gemv_ksplit_kernel<1, PRO, false, AttnTail>), grid, dim3((unsigned)(64 * nw)), lds, s, P.x,
+                       P.aux, P.aux2, P.K, P.mode, P.eps, shape, nw_reciprocal(nw), static_cast<const v4u*>(nullptr),
+                       a, at);
+}
+
+hipError_t launch_gemv_attn(const GemvArgs& args, const AttnTail& at, int Hkv, int hd, GemvShape shape,
+                            hipStream_t s) {
+    GemvArgs a = args;
+    for (int j = 0; j < kInlineProbs; ++j)
+        a.inw[j] = j < a.ninl ? GemvWeights{a.inl[j].w, a.inl[j].C, a.inl[j].wg_begin} : GemvWeights{nullptr, 0, 0};
+    const QuantProb& P = a.pro;
+    const int nw = shape.nw;
+    // the shapes the kernel assumes: three inline problems over one RMSNorm-quantised row,
+    // one row block per workgroup, a 256-thread tile per query head of a KV group, groups of
+    // whole row blocks
+    const bool vec = P.K % 64 == 0 && aligned16(P.x) && aligned16(P.aux) && aligned16(P.aux2);
+    const int E = vec ? vec_elements(P.K, 64 * nw) : 0;
+    if (a.has_pro != 1 || a.M != 1 || a.out_i32 || a.pair_a || a.stat_out || a.ninl != 3 || !shape.ksplit ||
+        E == 0 || P.mode == kRmsNormStats || P.mode == kAttnNorm || hd != 128 || 64 * nw != 256 * at.Gq ||
+        at.qrows != at.Gq * Hkv * hd || at.nkv != Hkv * hd || a.inl[0].N != at.qrows || a.inl[1].N != at.nkv ||
+        a.inl[2].N != at.nkv || a.inl[1].wg_begin * kRowBlock != at.qrows ||
+        a.inl[2].wg_begin * kRowBlock != at.qrows + at.nkv || at.S <= 0 || at.S != attn_splits(at.Lmax))
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(a.total_rb + Hkv * at.S), 1);
+    const size_t lds = std::max((size_t)nw * kRowBlock * sizeof(int) + (size_t)P.Kp + sizeof(RowSmem),
+                                (size_t)at.Gq * sizeof(AttnTileLds<128>) + (size_t)(at.Gq + 2) * hd * sizeof(float));
+    if (E == 4) launch_qkv_attn<3>(grid, nw, lds, s, a, at);
+    else if (E == 8) launch_qkv_attn<4>(grid, nw, lds, s, a, at);
+    else launch_qkv_attn<6>(grid, nw, lds, s, a, at);
     return hipGetLastError();
 }
 

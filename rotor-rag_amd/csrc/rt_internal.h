@@ -177,6 +177,29 @@ struct GemvArgs {
     const float* stat_w;
 };
 
+// Attention partials in the qkv GEMV's launch (gemv_ksplit_kernel with an AttnTail): the
+// GEMV workgroups also store every output y of the q, k and v problems (concatenated, row
+// n of the launch at index n) as tagged[n] = epoch << 32 | bits(y), a 64-bit
+// device-coherent store; the Hkv * S attention workgroups read the epoch at their start and
+// poll their group's q, k and v words until every one carries it (bounded; err counts the
+// waits that gave up, never expected).  Each attention workgroup counts itself in *done;
+// the last one resets *done and advances *epoch, so the next launch's tags differ.
+constexpr unsigned kAttnSpinLimit = 1u << 18;
+struct AttnTail {
+    unsigned long long* tagged;  // [H hd + 2 Hkv hd]
+    unsigned* epoch;             // [1], >= 1
+    int* done;                   // [1]
+    int* err;                    // [1]
+    float* Kc;                   // [Hkv][hd][Lmax]
+    float* Vc;                   // [Hkv][Lmax][hd]
+    const float* rope;
+    const int* pos;
+    float* work;                 // partials [H][S][hd + 2]
+    int Gq, Lmax, S, nkv;        // nkv = Hkv hd: where k starts after q (H hd), v after k
+    int qrows;                   // H hd
+    float scale;
+};
+
 struct GemvShape {
     bool ksplit;  // true: one row block per workgroup, waves split K
     int nw;       // waves per workgroup
@@ -322,6 +345,10 @@ long long gemm_tile_count(int cfg, int M, int N);
 hipError_t launch_gemm_tiles(const GemmArgs* dev, const int* tile2p, int total_tiles, int cfg, hipStream_t s);
 // M <= 64 (gemm_bm(M) == 64): G problems in one launch over all their row blocks;
 // dev [G] (wg_begin set), rb2p [total_rb] problem of every global row block.
+// The M = 1 qkv plan (three inline problems, E-element RMSNorm prologue, 256 Gq threads per
+// workgroup) with the attention partials of its token in the same launch.
+hipError_t launch_gemv_attn(const GemvArgs& args, const AttnTail& at, int Hkv, int hd, GemvShape shape,
+                            hipStream_t s);
 hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, int total_rb, hipStream_t s);
 
 // model kernels (rt_model.hip)

@@ -14,6 +14,7 @@
 #include <algorithm>
 
 #include "rt_rowquant.h"
+#include "rt_attn_decode.h"
 
 #pragma clang fp contract(off)
 
@@ -299,134 +300,35 @@ __global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(const float* __r
     }
 }
 
-// Decode attention, split over the keys: workgroup (h, s) handles keys
-// [64 s, 64 s + 64) of query head h for the single query at *pos_p and writes a partial
-// result to work[h][s][0..HD+2): the unnormalised output sum_j e^(s_j - m) V_j (HD
-// values), the block maximum m and the sum of exponentials z (m = -inf, z = 0 for an
-// empty block).  The partials are combined by attn_combine_kernel or, in the decode
-// layer, by the prologue of the o_proj GEMV (rt_rowquant.h, kAttnNorm); both use
-// attn_combine_element, so the two give identical values.
-// ROPE: q, knew, vnew are the raw projection outputs of the token at *pos_p.  Every
-// workgroup rotates its head's q (the arithmetic of rope_append_kernel); the workgroup
-// whose block holds position *pos_p takes that key and value from LDS (rotated knew,
-// vnew) instead of the cache, in the same summation order, and the first query head of
-// each KV group writes them into the caches for the later steps.  Without ROPE, q is
-// already rotated and the caches hold the new key.
+// Decode attention, split over the keys: workgroup (h, s) is the tile of query head h and
+// key block s (rt_attn_decode.h), writing its partial to work[h][s][0..HD+2).
 template <int HD, bool ROPE>
 __global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restrict__ q, const float* __restrict__ knew,
                                                            const float* __restrict__ vnew, float* __restrict__ Kc,
                                                            float* __restrict__ Vc, const float* __restrict__ rope,
                                                            int H, int Hkv, int Lmax, const int* __restrict__ pos_p,
                                                            float scale, float* __restrict__ work) {
-    constexpr int BL = 64, half = HD / 2, G = 256 / HD, KD = HD / 4, VN = BL / G;
-    __shared__ float qs[HD];
-    __shared__ float ks[HD];
-    __shared__ float vs[HD];
-    __shared__ float part[4][BL];
-    __shared__ float pr[BL];
-    __shared__ float ored[256];
+    __shared__ AttnTileLds<HD> sm;
     // Workgroup (h, s) from an XCD-ordered index whose fastest part is the query head within
     // its KV group: the G heads that read one key block run on one XCD and share its L2
     // (decode 1.235 -> 1.218 ms/token against one workgroup per (blockIdx.x, blockIdx.y))
     const int S = gridDim.y, Gq = H / Hkv;
     const int w = xcd_order((int)(blockIdx.x + gridDim.x * blockIdx.y), (int)(gridDim.x * gridDim.y));
     const int kh = w / (Gq * S), s = (w / Gq) % S, h = kh * Gq + w % Gq, t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6;
-    const int j0 = s * BL;
-    // The block's keys and values do not depend on the position: their loads go out first
-    // (wave w: dims [w HD/4, (w+1) HD/4) of key j0 + lane; thread (d, g): value dim d of
-    // keys g, g + G, ..), together with the position's.  Keys past Lmax re-read the last
-    // cached key; keys past the position are masked below.
-    const int d = t % HD, g = t / HD;
-    float kreg[KD], vreg[VN];
-    {
-        const float* K = Kc + (size_t)kh * HD * Lmax + min(j0 + lane, Lmax - 1);
-#pragma unroll
-        for (int i = 0; i < KD; ++i) kreg[i] = K[(size_t)(wave * KD + i) * Lmax];
-        const float* V = Vc + (size_t)kh * Lmax * HD + d;
-#pragma unroll
-        for (int i = 0; i < VN; ++i) vreg[i] = V[(size_t)min(j0 + g + i * G, Lmax - 1) * HD];
-    }
-    const int pos = *pos_p, L = pos + 1;
-    const int nk = min(BL, L - j0);  // keys of this block (may be <= 0)
+    const int j0 = s * kAttnBlock;
+    AttnKV<HD> kv;
+    attn_kv_load<HD>(Kc, Vc, kh, j0, Lmax, t, kv);
+    const int pos = *pos_p;
     float* wp = work + ((size_t)h * S + s) * (HD + 2);
-    if (nk <= 0) {
-        if (t == 0) {
-            wp[HD] = -INFINITY;
-            wp[HD + 1] = 0.0f;
-        }
+    if (pos < j0) {
+        attn_tile_empty<HD>(wp, t);
         return;
     }
-    const bool holds_new = ROPE && pos < j0 + BL;  // this block ends with the new key
-    const int lp = pos - j0;                       // its lane / key index in the block
-    if (ROPE) {
-        const float* cs = rope + (size_t)pos * half * 2;
-        for (int i = t; i < half; i += 256) {
-            const float c = cs[2 * i], sn = cs[2 * i + 1];
-            const float x1 = q[(size_t)h * HD + i], x2 = q[(size_t)h * HD + i + half];
-            qs[i] = x1 * c - x2 * sn;
-            qs[i + half] = x2 * c + x1 * sn;
-            if (holds_new) {
-                const float k1 = knew[(size_t)kh * HD + i], k2 = knew[(size_t)kh * HD + i + half];
-                ks[i] = k1 * c - k2 * sn;
-                ks[i + half] = k2 * c + k1 * sn;
-            }
-        }
-        if (holds_new)
-            for (int e = t; e < HD; e += 256) vs[e] = vnew[(size_t)kh * HD + e];
-    } else {
-        for (int e = t; e < HD; e += 256) qs[e] = q[(size_t)h * HD + e];
-    }
-    __syncthreads();
-    if (holds_new && h % (H / Hkv) == 0)  // one writer per KV head
-        for (int e = t; e < HD; e += 256) {
-            Kc[((size_t)kh * HD + e) * Lmax + pos] = ks[e];
-            Vc[((size_t)kh * Lmax + pos) * HD + e] = vs[e];
-        }
-    // scores: wave w sums its dims for key j0 + lane (the new key from LDS)
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    if (lane < nk) {
-        const bool mine = holds_new && lane == lp;
-#pragma unroll
-        for (int i = 0; i < KD; i += 4) {
-            const int dd = wave * KD + i;
-            a0 += qs[dd + 0] * (mine ? ks[dd + 0] : kreg[i + 0]);
-            a1 += qs[dd + 1] * (mine ? ks[dd + 1] : kreg[i + 1]);
-            a2 += qs[dd + 2] * (mine ? ks[dd + 2] : kreg[i + 2]);
-            a3 += qs[dd + 3] * (mine ? ks[dd + 3] : kreg[i + 3]);
-        }
-    }
-    part[wave][lane] = (a0 + a1) + (a2 + a3);
-    __syncthreads();
-    if (wave == 0) {
-        float sc = lane < nk ? (((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane])) * scale)
-                             : -INFINITY;
-        const float mx = lane63(wave_reduce63(sc, -INFINITY, [](float x, float y) { return fmaxf(x, y); }));
-        const float p = lane < nk ? expf(sc - mx) : 0.0f;
-        const float z = wave_reduce63(p, 0.0f, [](float x, float y) { return x + y; });
-        pr[lane] = p;
-        if (lane == 63) {
-            wp[HD] = mx;
-            wp[HD + 1] = z;
-        }
-    }
-    __syncthreads();
-    // unnormalised output: thread (d, g) sums keys g, g + G, ... of the block, two
-    // alternating partial sums
-    auto vrow = [&](int i) { return holds_new && g + i * G == lp ? vs[d] : vreg[i]; };
-    float o0 = 0.f, o1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < VN; i += 2) {
-        if (g + i * G < nk) o0 += pr[g + i * G] * vrow(i);
-        if (g + (i + 1) * G < nk) o1 += pr[g + (i + 1) * G] * vrow(i + 1);
-    }
-    ored[t] = o0 + o1;
-    __syncthreads();
-    if (g == 0) {
-        float o = ored[d];
-        for (int gg = 1; gg < G; ++gg) o += ored[gg * HD + d];
-        wp[d] = o;
-    }
+    float c = 0.0f, sn = 0.0f;
+    if (ROPE) attn_rope_load<HD>(rope, pos, t, c, sn);
+    attn_tile<HD, ROPE>(q + (size_t)h * HD, ROPE ? knew + (size_t)kh * HD : nullptr,
+                        ROPE ? vnew + (size_t)kh * HD : nullptr, c, sn, Kc, Vc, kh, h % Gq == 0, Lmax, pos, j0, scale,
+                        wp, t, (AttnLdsPtr<HD>)&sm, kv);
 }
 
 // out[h*hd + d] from the S partials of head h (one thread per output element)

@@ -229,6 +229,11 @@ class _DeviceModel:
         # workgroup-wide reduction; False (default: measured 1.247 against 1.196 ms per
         # token on the 30-layer 2560 / 6912 model) lets each prologue reduce the row itself
         self.row_stats = False
+        # decode: True (default, where the plan's shape allows it: hd 128, 4 query heads per KV
+        # head, the q/k/v GEMV at 16 waves per workgroup) runs RoPE + KV append + the attention
+        # partials inside the q/k/v GEMV's launch (rt_plan_attach_attention), one launch per
+        # layer fewer; False launches rt_rope_attention_decode after the GEMV
+        self.attn_in_qkv = True
 
     def _state(self, M):
         st = self.state.get(M)
@@ -242,12 +247,14 @@ class _DeviceModel:
               "g": e(M, F), "u": e(M, F), "a": e(F),
               "ssq": torch.empty(F // 32, dtype=torch.float64, device=dev)}
         st["qkv"], st["gu"], st["o_plan"], st["d_plan"] = [], [], [], []
+        st["attn_fused"] = []  # per layer: the q/k/v plan runs the attention partials
         hip, eps = self.hip, self.m.eps
         stats = M == 1 and self.row_stats and all(
             L["attn_sub_norm"] is not None and L["ffn_sub_norm"] is not None for L in self.layers)
         if stats:  # statistics of h after o_proj, of a after gate/up, of h after down
             st["s_h1"], st["s_a"], st["s_h2"] = hip.row_stats_buffer(D), hip.row_stats_buffer(F), hip.row_stats_buffer(D)
         for li, L in enumerate(self.layers):
+            st["attn_fused"].append(False)
             if M == 1 and stats:
                 self._decode_plans_stats(st, li, L)
                 continue
@@ -255,6 +262,8 @@ class _DeviceModel:
                 h, o, g, u = st["h"][0], st["o"][0], st["g"][0], st["u"][0]
                 st["qkv"].append(hip.plan_fused([L["q_proj"], L["k_proj"], L["v_proj"]], _hip.SRC_RMSNORM, h,
                                                 L["input_norm"], eps=eps, ys=[st["q"][0], st["k"][0], st["v"][0]]))
+                if self.attn_in_qkv and L["attn_sub_norm"] is not None and self.attn_in_prologue:
+                    st["attn_fused"][li] = self._attach_attention(st["qkv"][li], L)
                 if L["attn_sub_norm"] is not None and self.attn_in_prologue:
                     st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_ATTN_NORM, self.attn_ws,
                                                        L["attn_sub_norm"], eps=eps, ys=[h], residuals=[h],
@@ -287,6 +296,29 @@ class _DeviceModel:
                 st["gu"].append(hip.plan_act([L["gate_proj"], L["up_proj"]], [self.act_d] * 2, M, [st["g"], st["u"]]))
         self.state[M] = st
         return st
+
+    def _attach_attention(self, plan, L):
+        """Attach the decode attention to layer L's q/k/v plan; False where the library does
+        not run it in that plan's launch (head size, query heads per KV head, workgroup size),
+        which leaves the separate rt_rope_attention_decode launch."""
+        try:
+            plan.attach_attention(L["kc"], L["vc"], self.rope, self.H, self.Hkv, self.hd, self.Lmax, self.pos,
+                                  self.attn_ws)
+        except RuntimeError as e:
+            if "rt_plan_attach_attention" not in str(e):
+                raise
+            return False
+        return True
+
+    def attention_timeouts(self):
+        """Attention waits that gave up in the q/k/v launches since the last call (never
+        expected; synchronises the device).  Raises if there were any: results are wrong."""
+        st = self.state.get(1)
+        n = 0
+        if st is not None:
+            n = sum(p.attention_timeouts() for p, on in zip(st["qkv"], st["attn_fused"]) if on)
+        if n:
+            raise RuntimeError(f"{n} attention waits in the q/k/v launches gave up: the decode results are invalid")
 
     def _decode_plans_stats(self, st, li, L):
         """One decode layer's four plans with the row statistics handed along: o_proj writes
@@ -335,7 +367,9 @@ class _DeviceModel:
             else:
                 hip.act_rmsnorm_quantize(h, L["input_norm"], self.act_d, eps)
                 st["qkv"][li].gemv()
-            if M == 1:  # RoPE + KV append + split attention in one launch; o_proj's prologue may combine
+            if M == 1 and st["attn_fused"][li]:
+                pass  # RoPE, KV append and the attention partials ran in the q/k/v launch
+            elif M == 1:  # RoPE + KV append + split attention in one launch; o_proj's prologue may combine
                 combine_here = L["attn_sub_norm"] is None or not self.attn_in_prologue
                 chk(lib.rt_rope_attention_decode(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
                                                  L["vc"].data_ptr(), self.rope.data_ptr(), self.H, self.Hkv, self.hd,
@@ -391,6 +425,8 @@ class _DeviceModel:
         self.ids[:M].copy_(torch.from_numpy(ids))
         self.pos.fill_(start)
         st = self._enqueue(M, pos_base=1 << 30, out_cap=0)
+        if M == 1:
+            self.attention_timeouts()
         h = st["h"]
         if M == 1:
             out = self.logits[None] if return_logits else self._final_norm(h)
@@ -446,6 +482,7 @@ class _DeviceModel:
                 self._enqueue(1, pos_base=P - 1, out_cap=n)
         ev[2].record()
         torch.cuda.synchronize()
+        self.attention_timeouts()
         if timings is not None:
             timings["prefill_ms"] = ev[0].elapsed_time(ev[1])
             timings["decode_ms"] = ev[1].elapsed_time(ev[2])

@@ -103,6 +103,27 @@ class LinearPlan:
                    "rt_plan_set_row_stats")
         self._keep = (self._keep, next_norm_w, stats)
 
+    def attach_attention(self, k_cache, v_cache, rope, H: int, Hkv: int, hd: int, Lmax: int, pos, workspace) -> None:
+        """Run the decode RoPE + KV append + attention partials of the token inside run()'s
+        launch of this q/k/v plan (rt_plan_attach_attention; the arguments of
+        rt_rope_attention_decode).  k_cache=None detaches."""
+        if k_cache is None:
+            _hip.check(_hip.load().rt_plan_attach_attention(self.handle, None, None, None, 0, 0, 0, 0, None, None, 0),
+                       "rt_plan_attach_attention")
+            return
+        _hip.check(_hip.load().rt_plan_attach_attention(self.handle, k_cache.data_ptr(), v_cache.data_ptr(),
+                                                        rope.data_ptr(), H, Hkv, hd, Lmax, pos.data_ptr(),
+                                                        workspace.data_ptr(), workspace.numel() * workspace.element_size()),
+                   "rt_plan_attach_attention")
+        self._keep = (self._keep, k_cache, v_cache, rope, pos, workspace)
+
+    def attention_timeouts(self) -> int:
+        """Attention waits of this plan's launches that gave up (rt_plan_attention_timeouts;
+        synchronises the device).  Never expected: a non-zero count means wrong results."""
+        n = ctypes.c_int()
+        _hip.check(_hip.load().rt_plan_attention_timeouts(self.handle, ctypes.byref(n)), "rt_plan_attention_timeouts")
+        return n.value
+
     def describe(self):
         """(kind, tile_m, tile_n, workgroups) of the launch the plan makes (rt_plan_describe);
         kind is one of _hip.LAUNCH_*."""

@@ -181,6 +181,112 @@ def test_rope_attention_decode_equals_separate_launches(hip, pos0, H, Hkv, hd, L
     assert torch.equal(ws, ws_ref)
 
 
+@pytest.mark.parametrize("pos0,Lmax", [(0, 640), (63, 640), (64, 640), (639, 640), (1000, 2048)])
+def test_qkv_plan_with_attention_equals_separate_launches(hip, pos0, Lmax):
+    """The q/k/v decode plan with the attention attached (RoPE + KV append + split-L partials
+    in the GEMV's launch, their workgroups waiting on per-KV-group arrival counts) gives the
+    q, k, v outputs, the partials and the caches of the plan followed by
+    rt_rope_attention_decode, bit for bit: on two runs in a row and on every replay of a
+    captured graph (the counts start from zero on every launch); no wait gives up."""
+    import torch
+
+    from oracle.rotor_oracle import rope_table
+    from rotor import _hip as H_
+
+    lib, chk = _lib()
+    H, Hkv, hd = 20, 5, 128
+    D = H * hd
+    rng = np.random.default_rng(pos0 + Lmax)
+    f = lambda *shape: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).cuda()
+    ws_ = [hip.upload(O.pack_rotor(W), D, s) for W, s in (O.make_ternary(rng, n, D) for n in (D, Hkv * hd, Hkv * hd))]
+    x = f(D)
+    nw = torch.from_numpy(rng.uniform(0.5, 1.5, D).astype(np.float32)).cuda()
+    kc0, vc0 = f(Hkv, hd, Lmax), f(Hkv, Lmax, hd)
+    rope = torch.from_numpy(np.ascontiguousarray(rope_table(Lmax, hd, 500000.0), np.float32)).cuda()
+    pos = torch.tensor([pos0], dtype=torch.int32, device="cuda")
+    nbytes = lib.rt_attention_decode_workspace(H, hd, Lmax)
+    outs = lambda: [torch.empty(D, device="cuda"), torch.empty(Hkv * hd, device="cuda"),
+                    torch.empty(Hkv * hd, device="cuda")]
+    hip._bind_stream()
+    # the plan, then the attention launch
+    qr, kr, vr = outs()
+    kc, vc = kc0.clone(), vc0.clone()
+    ws_ref = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    plan_ref = hip.plan_fused(ws_, H_.SRC_RMSNORM, x, nw, eps=1e-6, ys=[qr, kr, vr])
+    plan_ref.run()
+    chk(lib.rt_rope_attention_decode(hip.ctx, qr.data_ptr(), kr.data_ptr(), vr.data_ptr(), kc.data_ptr(),
+                                     vc.data_ptr(), rope.data_ptr(), H, Hkv, hd, Lmax, pos.data_ptr(),
+                                     ws_ref.data_ptr(), nbytes, None))
+    # one launch
+    q, k, v = outs()
+    kcf, vcf = kc0.clone(), vc0.clone()
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    plan = hip.plan_fused(ws_, H_.SRC_RMSNORM, x, nw, eps=1e-6, ys=[q, k, v])
+    plan.attach_attention(kcf, vcf, rope, H, Hkv, hd, Lmax, pos, ws)
+
+    def check(what):
+        torch.cuda.synchronize()
+        assert torch.equal(q, qr) and torch.equal(k, kr) and torch.equal(v, vr), f"q/k/v differ ({what})"
+        assert torch.equal(ws, ws_ref), f"partials differ ({what})"
+        assert torch.equal(kcf, kc) and torch.equal(vcf, vc), f"caches differ ({what})"
+
+    def reset():
+        for t in (q, k, v):
+            t.fill_(float("nan"))
+        ws.zero_()
+        kcf.copy_(kc0)
+        vcf.copy_(vc0)
+
+    for rep in range(2):
+        reset()
+        plan.run()
+        check(f"run {rep}")
+    assert plan.attention_timeouts() == 0
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        plan.run()
+    for rep in range(3):
+        reset()
+        g.replay()
+        check(f"replay {rep}")
+    assert plan.attention_timeouts() == 0
+    # detached, the plan runs the GEMV only
+    plan.attach_attention(None, None, None, 0, 0, 0, 0, None, None)
+    reset()
+    plan.run()
+    torch.cuda.synchronize()
+    assert torch.equal(q, qr) and torch.equal(kcf, kc0) and not ws.any()
+
+
+def test_attach_attention_rejects_other_plans(hip):
+    """Plans the attention cannot join (one problem; 2 query heads per KV head) are refused
+    with the library's message, and stay usable."""
+    import torch
+
+    from rotor import _hip as H_
+
+    rng = np.random.default_rng(5)
+    D, hd, Lmax = 2560, 128, 128
+    w = [hip.upload(O.pack_rotor(W), D, s) for W, s in (O.make_ternary(rng, n, D) for n in (D, 640, 640))]
+    x = torch.from_numpy(rng.standard_normal(D).astype(np.float32)).cuda()
+    nw = torch.ones(D, device="cuda")
+    kc, vc = torch.zeros(5, hd, Lmax, device="cuda"), torch.zeros(5, Lmax, hd, device="cuda")
+    rope, pos = torch.zeros(Lmax, hd // 2, 2, device="cuda"), torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = torch.zeros(_lib()[0].rt_attention_decode_workspace(20, hd, Lmax), dtype=torch.uint8, device="cuda")
+    ys = [torch.empty(D, device="cuda"), torch.empty(640, device="cuda"), torch.empty(640, device="cuda")]
+    one = hip.plan_fused(w[:1], H_.SRC_RMSNORM, x, nw, eps=1e-6, ys=ys[:1])
+    with pytest.raises(RuntimeError, match="rt_plan_attach_attention"):
+        one.attach_attention(kc, vc, rope, 20, 5, hd, Lmax, pos, ws)
+    three = hip.plan_fused(w, H_.SRC_RMSNORM, x, nw, eps=1e-6, ys=ys)
+    with pytest.raises(RuntimeError, match="rt_plan_attach_attention"):  # q must be H * hd = 10 * 128
+        three.attach_attention(kc, vc, rope, 10, 5, hd, Lmax, pos, ws)
+    with pytest.raises(RuntimeError, match="rt_plan_attach_attention"):  # workspace too small
+        three.attach_attention(kc, vc, rope, 20, 5, hd, Lmax, pos, ws[:16])
+    three.run()
+    one.run()
+    torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("V,D", [(1000, 512), (5000, 2560), (777, 1024)])
 def test_lm_head_argmax(hip, V, D):
     import torch
@@ -429,6 +535,32 @@ def test_decode_row_stats_handoff_bit_exact(hip):
     assert list(runs[0][1]) == list(runs[1][1])
 
 
+WIDE16 = dict(vocab_size=1000, d_model=2048, n_layers=2, n_heads=16, n_kv_heads=4, d_ff=2048, rope_theta=500000.0)
+
+
+def test_decode_attention_in_qkv_launch_bit_exact(hip):
+    """Decode with the attention partials in the q/k/v launch gives the same logits, bit for
+    bit, and the same graph-replayed greedy tokens as decode with the separate attention
+    launch (hidden 2048, 16 / 4 heads of 128: the shapes the joint launch takes)."""
+    params = O.make_bitnet_params(22, WIDE16, 96)
+    prompt = np.array([3, 14, 15, 92, 65, 35, 89], np.int32)
+    runs = []
+    for fused in (False, True):
+        model = _device_model(hip, params, WIDE16, 96)
+        model._dev.attn_in_qkv = fused
+        _, cache = model.forward(prompt, return_logits=False, use_cache=True)
+        tok, lgs = 7, []
+        for _ in range(4):
+            lg, cache = model.forward(np.array([tok], np.int32), past_kv_cache=cache, use_cache=True)
+            lgs.append(lg[0].copy())
+            tok = int(np.argmax(lg[0]))
+        toks = model.generate_greedy(prompt, 8, graph=True)
+        runs.append((np.stack(lgs), toks, model._dev.state[1]["attn_fused"]))
+    assert runs[0][2] == [False, False] and runs[1][2] == [True, True]
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert list(runs[0][1]) == list(runs[1][1])
+
+
 def _greedy_vs_oracle(model, params, cfg, prompt, n):
     """generate_greedy (prefill, then graph-replayed decode steps) beside the oracle's greedy
     protocol (src/rotor/generation.py:244-279: argmax, one token per step), the oracle's
@@ -481,6 +613,7 @@ def test_cfg4_full_width_matches_oracle(hip):
     # greedy decode: prefill + (n - 1) graph replays, tokens equal wherever the oracle's top-2
     # gap exceeds four times the logit deviation just measured
     toks, ref, gaps = _greedy_vs_oracle(model, params, cfg, prompt, n)
+    assert all(model._dev.state[1]["attn_fused"]), "decode runs the attention in the q/k/v launch"
     assert ref[0] == t0
     tol = max(0.05, 4 * err)
     compared = 0

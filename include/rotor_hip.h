@@ -267,7 +267,8 @@ int rt_plan_set_row_stats(rt_plan* plan, const float* next_norm_w, void* stats);
  * source with K % 64 == 0, hd = 128 and H / Hkv = 4 (the plan's workgroups hold one
  * 256-thread tile per query head of a KV group).  The attention workgroups follow the
  * GEMV's in the grid and start on a KV group as soon as its q, k and v rows are stored
- * (a device-side arrival count; the wait is bounded).  k_cache = NULL detaches.  The
+ * (the GEMV also writes them as (epoch, value) words that the attention polls; the wait
+ * is bounded).  k_cache = NULL detaches.  The
  * pointers are kept: the caches, rope, pos and workspace must outlive the plan's runs.
  * Replaces, for one token, src/rotor/transformer.py:250-281 after the projections
  * :235-237. */
@@ -275,8 +276,8 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
                              int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes);
 /* Number of attention waits of the plan's launches that gave up (never expected; the
  * results of such a launch are wrong).  Synchronises the device; a non-zero count also
- * clears the plan's arrival counts.  No counterpart in the reference (its attention runs
- * after the projections on the host). */
+ * resets the plan's hand-off state (tagged outputs and epoch).  No counterpart in the
+ * reference (its attention runs after the projections on the host). */
 int rt_plan_attention_timeouts(rt_plan* plan, int* count);
 
 /* ---- kernels around the linears for BitNet-2B-shape inference ----------------------

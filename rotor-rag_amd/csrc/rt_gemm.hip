@@ -71,6 +71,14 @@ __device__ __forceinline__ void wait_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// Wait until at most N of this wave's vector-memory loads are outstanding (no barrier).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 template <int BM, int BN, int WAVES_M, int STAGES>
 struct GemmTile {
     static constexpr int WAVES_N = 4 / WAVES_M;
@@ -325,6 +333,278 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmGroupArgs ga) {
     else store_tile<FI, FJ, 1>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
 }
 
+// ---- long K, one round over the CUs: 128 x 160 regions -------------------------------
+// Writes a wave's FI x FJ blocks of 16 x 16 (v_mfma_i32_16x16x64_i8 layout: lane l holds
+// column l % 16, rows 4 (l / 16) + r of element r) with store_tile's conventions.
+// mrow: this lane's first row relative to m0 (includes 4 (lane / 16)); nb: its column.
+template <int FI, int FJ, int EPI>
+__device__ __forceinline__ void store_tile16(const v4i (&acc)[FI][FJ], const GemmArgs& a, int m0, int rows, int mrow,
+                                             int nb, const float* sx, const float (&swv)[FJ]) {
+    const unsigned range = (unsigned)rows * (unsigned)a.ldo * 4u;
+    const __amdgpu_buffer_rsrc_t out =
+        __builtin_amdgcn_make_buffer_rsrc(static_cast<char*>(a.out) + (size_t)m0 * a.ldo * 4, 0, range, kBufDword3);
+    const __amdgpu_buffer_rsrc_t res = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(a.res ? a.res + (size_t)m0 * a.ldo : nullptr), 0, EPI == 2 ? range : 0u, kBufDword3);
+    int coff[FJ];
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) {
+        const int n = nb + j * 16;
+        coff[j] = (int)((unsigned)n * 4u + ((unsigned)(n >= a.N) << 31));
+    }
+    const int row_bytes = a.ldo * 4;
+#pragma unroll
+    for (int i = 0; i < FI; ++i) {
+        v4f sxv = {};
+        if (EPI) sxv = *reinterpret_cast<const v4f*>(sx + mrow + i * 16);  // rows mrow + 16 i + 0..3
+        int off[FJ][4];
+        float rv[FJ][4];
+#pragma unroll
+        for (int j = 0; j < FJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                off[j][r] = (mrow + i * 16 + r) * row_bytes + coff[j];
+                if (EPI == 2) rv[j][r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(res, off[j][r], 0, 0));
+            }
+#pragma unroll
+        for (int j = 0; j < FJ; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                unsigned bits;
+                if (EPI == 0) {
+                    bits = (unsigned)acc[i][j][r];
+                } else {
+                    const float y = ((float)acc[i][j][r] * sxv[r]) * swv[j];
+                    bits = __builtin_bit_cast(unsigned, EPI == 2 ? rv[j][r] + y : y);
+                }
+                __builtin_amdgcn_raw_buffer_store_b32(bits, out, off[j][r], 0, 0);
+            }
+    }
+}
+
+// Region 128 x 160 per workgroup: the 2048 x 2560 outputs of a 6912-deep problem make 256
+// regions, one per CU (the tile kernel's 192 x 128 tiles make 220).  Eight waves, two per
+// SIMD: four compute waves and four load waves.  A wave that issues a vector-memory load
+// waits until the CU's load path accepts it (measured: ~64 B/clk per CU into registers,
+// ~40 B/clk straight into LDS), so loads dealt out between the MFMAs add their time to the
+// MFMA stream; here no compute wave issues one.
+//   * Compute wave w = 2 kh + nh covers K half kh (chunks [kh C / 2, (kh + 1) C / 2), C
+//     even) of the region's columns [80 nh, 80 nh + 80) and all 128 rows: 8 x 5 blocks of
+//     v_mfma_i32_16x16x64_i8 (160 accumulator registers; this shape runs at full rate with
+//     8 or more independent accumulators).  Its A operand is exactly a 1 KiB qx block as
+//     loaded (lane l: row l % 16, bytes 16 (l / 16) ..), its B operand one dword of device
+//     code per lane (column l % 16, dword l / 16 of the row's 16-byte unit) expanded by four
+//     v_perm_b32, the expansion's dependent steps in different gaps between MFMAs.
+//   * Each K half has an LDS ring of S stages (its chunk's 8 A blocks and both column
+//     halves' 80 weight rows); load wave 4 + 2 kh + q fills A blocks [4 q, 4 q + 4) and the
+//     weight rows of column half q, S - 1 chunks ahead, by buffer loads straight into LDS.
+//   * One barrier per chunk step: load waves arrive once chunk c + 1 is in LDS (s_waitcnt
+//     on their loads), compute waves once their reads of chunk c - 1's stage have returned,
+//     so after barrier c chunk c + 1 may be read and chunk c - 1's stage refilled.
+//   * A chunk runs as two row halves (fragments 0-3, then 4-7), each over the five column
+//     blocks, so that every fragment and expanded B block is refilled for the next chunk
+//     right after its last use and 12 or more MFMAs before its next one (the compute waves
+//     stall on no LDS read).
+// The K-half partners then sum their partial regions in LDS (exact int32) and each compute
+// wave stores 64 rows through store_tile16.
+constexpr int kRegM = 128, kRegN = 160, kRegS = 7;
+constexpr int kRegWBytes = (kRegN / 2) * 16;                     // one column half's weight rows
+constexpr int kRegStage = (kRegM / 16) * 1024 + 2 * kRegWBytes;  // A blocks + both halves' rows
+constexpr int kRegThreads = 8 * 64;
+
+template <int S>
+__global__ void __launch_bounds__(kRegThreads) gemm_region_kernel(GemmGroupArgs ga) {
+    constexpr int FI = kRegM / 16, FJ = kRegN / 32;  // per compute wave: 16 x 16 blocks
+    constexpr int A_BYTES = FI * 1024, STAGE = kRegStage;
+    constexpr int LOADS = FI / 2 + 2;                // loads per load wave and chunk
+    constexpr int kMfma = FI * FJ;
+    static_assert(FJ * 16 > 64 && FJ * 16 <= 128, "two weight loads per chunk");
+    static_assert((S - 2) * LOADS <= 63, "vmcnt range");
+    static_assert(2 * S * STAGE >= 4 * (FI / 2) * FJ * 1024, "the rings hold the partial halves");
+    extern __shared__ __attribute__((aligned(16))) v4u lds[];
+    char* const lds_b = reinterpret_cast<char*>(lds);
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const bool loader = wave >= 4;
+    const int kh = (wave >> 1) & 1, q = wave & 1;  // K half; column half (compute) or share (load)
+    const int reg = xcd_order((int)blockIdx.x, (int)gridDim.x);
+    const GemmArgs a = find_gemm(ga, reg);
+    const int C = a.C, nR = (a.N + kRegN - 1) / kRegN, lr = reg - a.wg_begin;
+    const int m0 = (lr / nR) * kRegM, n0 = (lr % nR) * kRegN + q * (kRegN / 2);
+    const int cb = __builtin_amdgcn_readfirstlane(kh ? C >> 1 : 0);
+    const int ce = __builtin_amdgcn_readfirstlane(kh ? C : C >> 1);
+    char* const ring = lds_b + kh * (S * STAGE);
+    auto stage = [&](int c) { return ring + ((c - cb) % S) * STAGE; };
+
+    v4i acc[FI][FJ];
+#pragma unroll
+    for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int j = 0; j < FJ; ++j) acc[i][j] = v4i{};
+
+    if (loader) {
+        // A: 16-row block f of chunk c at ((m0 / 16 + f) C + c) KiB + 16 l of the activations
+        // (256-row padding); W: rows n0 + l (and n0 + 64 + l, l < 16), clamped to the padded
+        // rows, chunk c at + c KiB
+        const unsigned a_bytes = (unsigned)((a.M + 255) & ~255) * (unsigned)C * 64u;
+        const __amdgpu_buffer_rsrc_t ar = __builtin_amdgcn_make_buffer_rsrc((void*)a.qx, 0, a_bytes, kBufDword3);
+        const __amdgpu_buffer_rsrc_t wr =
+            __builtin_amdgcn_make_buffer_rsrc((void*)a.w, 0, (unsigned)a.Np * (unsigned)C * 16u, kBufDword3);
+        const int a_soff = ((m0 >> 4) + (FI / 2) * q) * C * 1024;
+        auto w_row = [&](int n) {
+            n = min(n, a.Np - 1);
+            return ((n >> 6) * C * 64 + (n & 63)) * 16;
+        };
+        const int w_off0 = w_row(n0 + lane), w_off1 = w_row(n0 + 64 + (lane & 15));
+        const bool w_second = lane < FJ * 16 - 64;
+        typedef __attribute__((address_space(3))) void* lds_p;
+        auto load_chunk = [&](int c) {
+            char* st = stage(c);
+#pragma unroll
+            for (int k = 0; k < FI / 2; ++k)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ar, (lds_p)(st + ((FI / 2) * q + k) * 1024), 16, lane * 16,
+                                                         a_soff + (k * C + c) * 1024, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_p)(st + A_BYTES + q * kRegWBytes), 16, w_off0, c * 1024,
+                                                     0, 0);
+            if (w_second)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_p)(st + A_BYTES + q * kRegWBytes + 1024), 16, w_off1,
+                                                         c * 1024, 0, 0);
+        };
+        for (int k = 0; k < S - 1; ++k) load_chunk(cb + k);
+        wait_vm<(S - 2) * LOADS>();
+        __syncthreads();  // barrier cb - 1: chunk cb in LDS
+        for (int c = cb; c + 1 < ce; ++c) {
+            // barrier c - 1 passed: chunk c - 1's stage is free
+            if (c + S - 1 < ce) {
+                load_chunk(c + S - 1);
+                wait_vm<(S - 2) * LOADS>();
+            } else {
+                wait_vm<0>();
+            }
+            __builtin_amdgcn_s_barrier();  // barrier c: chunk c + 1 in LDS
+        }
+    } else {
+        const int a_rd = lane * 16, w_rd = A_BYTES + q * kRegWBytes + (lane & 15) * 16 + 4 * (lane >> 4);
+        constexpr int HF = FI / 2;  // A fragments per row half
+        unsigned wraw[FJ];          // raw weight dwords (refilled for the next chunk)
+        v4i fa[FI];                 // A fragments (refilled for the next chunk)
+        v4i fb[FJ];                 // expanded B blocks (re-expanded for the next chunk)
+        unsigned xt[2][3], xm[2][4];  // expansion temporaries of blocks j (set j % 2)
+        auto read_a = [&](const char* st, int i) { fa[i] = *reinterpret_cast<const v4i*>(st + a_rd + i * 1024); };
+        auto read_w = [&](const char* st, int j) { wraw[j] = *reinterpret_cast<const unsigned*>(st + w_rd + j * 256); };
+        // step s (0..6) of expanding raw dword wraw[j] into fb[j]: shifts, masks, permutes
+        auto expand_step = [&](int j, int s) {
+            constexpr unsigned M = 0x03030303u;
+            const int e = j & 1;
+            if (s == 0) {
+                xt[e][0] = wraw[j] >> 2;
+                xt[e][1] = wraw[j] >> 4;
+                xt[e][2] = wraw[j] >> 6;
+            } else if (s == 1) {
+                xm[e][0] = wraw[j] & M;
+                xm[e][1] = xt[e][0] & M;
+            } else if (s == 2) {
+                xm[e][2] = xt[e][1] & M;
+                xm[e][3] = xt[e][2] & M;
+            } else if (s < 7) {
+                fb[j][s - 3] = (int)__builtin_amdgcn_perm(0u, kLut, xm[e][s - 3]);
+            }
+        };
+        // Chunk c (LAST: no next chunk), MFMA m = 20 h + 4 j + r: row half h, column block j,
+        // A fragment i = 4 h + r.  Items after the MFMAs:
+        //   * MFMAs 0-3: this chunk's fragments 4-7 (first used at MFMA 20);
+        //   * MFMAs 0-6: the rest of the expansion of this chunk's blocks 3 and 4;
+        //   * barrier c before MFMA kBar (this wave's reads have returned), then the next
+        //     chunk's weight dwords (MFMAs kBar..kBar + 4) and fragments 0-3 (MFMAs 20-23,
+        //     after their last use in this chunk), each 12 or more MFMAs before first use;
+        //   * the next chunk's block j (j < 4) expanded at MFMAs 24 + 4 j .. (after its last
+        //     use in this chunk at 23 + 4 j), block 3's last steps and block 4 carried over.
+        constexpr int kBar = 12;
+        auto body = [&](auto LAST, int c) {
+            constexpr bool last = decltype(LAST)::value;
+            const char* st = stage(c);
+            const char* nst = stage(c + 1);
+#pragma unroll
+            for (int m = 0; m < kMfma; ++m) {
+                const int h = m / 20, j = (m % 20) / 4, i = HF * h + m % 4;
+                if (m == kBar && !last) {
+                    __builtin_amdgcn_sched_barrier(0);
+                    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (m < HF) read_a(st, HF + m);
+                if (!last) {
+                    if (m >= kBar && m < kBar + FJ) read_w(nst, m - kBar);
+                    if (m >= 20 && m < 20 + HF) read_a(nst, m - 20);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (m < 3) expand_step(3, 4 + m);
+                if (m < 7) expand_step(4, m);
+                if (!last) {
+#pragma unroll
+                    for (int jj = 0; jj < 4; ++jj) {
+                        const int k = m - (24 + 4 * jj);
+                        if (k >= 0 && k < (jj < 3 ? 7 : 4)) expand_step(jj, k);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        static_assert(FI == 8 && FJ == 5 && kMfma == 40, "chunk schedule");
+        __syncthreads();  // barrier cb - 1: chunk cb in LDS
+#pragma unroll
+        for (int i = 0; i < HF; ++i) read_a(stage(cb), i);
+#pragma unroll
+        for (int j = 0; j < FJ; ++j) read_w(stage(cb), j);
+        // blocks 0-2 expanded, block 3 up to step 3: what a previous chunk would have done
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int s7 = 0; s7 < (j < 3 ? 7 : 4); ++s7) expand_step(j, s7);
+        for (int c = cb; c + 1 < ce; ++c) body(std::false_type{}, c);
+        body(std::true_type{}, ce - 1);
+    }
+
+    // K halves: compute wave (kh, nh) keeps row blocks [4 kh, 4 kh + 4) and hands the other
+    // four to its partner (1 - kh, nh) through slot w of 20 KiB, lane-major (16 bytes per
+    // lane and block); the load waves only pass the barriers
+    constexpr int HB = FI / 2;
+    __syncthreads();  // every wave is done with the rings
+    if (!loader) {
+        char* mine = lds_b + wave * (HB * FJ * 1024) + lane * 16;
+#pragma unroll
+        for (int i = 0; i < FI; ++i)
+            if ((i >= HB) != (kh == 1))  // the partner's rows
+#pragma unroll
+                for (int j = 0; j < FJ; ++j) *reinterpret_cast<v4i*>(mine + ((i % HB) * FJ + j) * 1024) = acc[i][j];
+    }
+    __syncthreads();
+    if (loader) return;
+    {
+        const char* theirs = lds_b + (wave ^ 2) * (HB * FJ * 1024) + lane * 16;
+#pragma unroll
+        for (int i = 0; i < FI; ++i)
+            if ((i >= HB) == (kh == 1))  // this wave's rows
+#pragma unroll
+                for (int j = 0; j < FJ; ++j) acc[i][j] += *reinterpret_cast<const v4i*>(theirs + ((i % HB) * FJ + j) * 1024);
+    }
+    const int mrow = HB * 16 * kh + 4 * (lane >> 4), nb = n0 + (lane & 15);
+    float swv[FJ];
+#pragma unroll
+    for (int j = 0; j < FJ; ++j) swv[j] = a.out_i32 ? 0.f : a.rs ? a.rs[min(nb + j * 16, a.N - 1)] : a.s_w;
+    const int rows = min(kRegM, a.M - m0);
+    const float* const sxp = a.out_i32 ? nullptr : a.sx + m0;
+    // this wave's half of the accumulators (row blocks [4 kh, 4 kh + 4))
+    auto store = [&](const v4i(&half)[HB][FJ]) {
+        if (a.out_i32) store_tile16<HB, FJ, 0>(half, a, m0, rows, mrow, nb, sxp, swv);
+        else if (a.res) store_tile16<HB, FJ, 2>(half, a, m0, rows, mrow, nb, sxp, swv);
+        else store_tile16<HB, FJ, 1>(half, a, m0, rows, mrow, nb, sxp, swv);
+    };
+    if (kh) store(reinterpret_cast<const v4i(&)[HB][FJ]>(acc[HB]));
+    else store(reinterpret_cast<const v4i(&)[HB][FJ]>(acc[0]));
+}
+
 // ---- M <= 64: K split over the waves ------------------------------------------------
 // One workgroup per 64-column tile of the output and all (<= 64) rows, over the unit's
 // chunks (a part of a long-K problem, GemmArgs::parts, or all C); wave w of NW covers an
@@ -334,13 +614,6 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmGroupArgs ga) {
 // itself.  The NW int32 partial tiles are then summed in LDS (exact) and one pass
 // applies the fp32 epilogue.  Fragment reads, weight expansion and the result layout
 // are those of gemm_kernel (a wave tile of 64 x 64 = 2 x 2 blocks of 32 x 32).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-    __builtin_amdgcn_sched_barrier(0);
-}
-
 template <int NW, int S>
 __global__ void __launch_bounds__(NW * 64) gemm_splitk_kernel(GemmGroupArgs ga) {
     constexpr int STAGE = 4 * 1024 + 1024, LOADS = 5;  // A: 4 blocks of 16 rows; W: 1 chunk
@@ -517,8 +790,20 @@ static hipError_t launch_tile(const GemmGroupArgs& ga, int tiles, hipStream_t s)
     return hipGetLastError();
 }
 
+template <int S>
+static hipError_t launch_region(const GemmGroupArgs& ga, int regions, hipStream_t s) {
+    constexpr int LDS = 2 * S * kRegStage;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_region_kernel<S>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
+    if (attr != hipSuccess) return attr;
+    if (regions <= 0) return hipSuccess;
+    hipLaunchKernelGGL((gemm_region_kernel<S>), dim3((unsigned)regions), dim3(kRegThreads), LDS, s, ga);
+    return hipGetLastError();
+}
+
 static hipError_t launch_tile_cfg(int cfg, const GemmGroupArgs& ga, int tiles, hipStream_t s) {
     switch (cfg) {
+        case kRegion128x160: return launch_region<kRegS>(ga, tiles, s);
         case kTile128x128: return launch_tile<128, 128, 2, 4>(ga, tiles, s);
         case kTile256x128: return launch_tile<256, 128, 2, 4>(ga, tiles, s);
         case kTile256x256: return launch_tile<256, 256, 2, 4>(ga, tiles, s);
@@ -530,8 +815,13 @@ static hipError_t launch_tile_cfg(int cfg, const GemmGroupArgs& ga, int tiles, h
     }
 }
 
-int gemm_tile_cfg(int M, const int* N, int G) {
+int gemm_tile_cfg(int M, const int* N, int G, int C) {
     if (gemm_bm(M) == 128) return kTile128x128;
+    if (C >= kRegMinC && C % 2 == 0) {  // long K: 128 x 160 regions when they make one round over the CUs
+        long long regions = 0;
+        for (int g = 0; g < G; ++g) regions += (long long)((M + kRegM - 1) / kRegM) * ((N[g] + kRegN - 1) / kRegN);
+        if (regions >= kRegMinTiles && regions <= kRegMaxTiles) return kRegion128x160;
+    }
     const long long mt = (M + 255) / 256;
     const long long mt192 = (M + 191) / 192;
     long long t256 = 0, t128 = 0, t192 = 0;
@@ -566,7 +856,7 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
         one.wg_begin = 0;
         return launch_splitk<kSplitkWaves, 4>(GemmGroupArgs{nullptr, nullptr, one}, a.Np / kRowBlock, s);
     }
-    const int cfg = gemm_tile_cfg(a.M, &a.N, 1);
+    const int cfg = gemm_tile_cfg(a.M, &a.N, 1, a.C);
     GemmArgs one = a;
     one.wg_begin = 0;
     return launch_tile_cfg(cfg, GemmGroupArgs{nullptr, nullptr, one}, (int)gemm_tile_count(cfg, a.M, a.N), s);

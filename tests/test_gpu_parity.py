@@ -38,7 +38,8 @@ LINEAR_CASES = [
     (256, 6912, 2560),
     (512, 2560, 6912),
     (2048, 6912, 2560),  # cfg 3 (gate/up)
-    (2048, 2560, 6912),  # cfg 3 (down): 192-row tiles
+    (2048, 2560, 6912),  # cfg 3 (down): 128 x 160 regions, K split over the waves
+    (2000, 2500, 4160),  # regions with rows past M and a last region of 100 columns, odd chunks per half
     (2000, 2560, 640),   # 192-row tiles, the last one past the 256-row padding
     (200, 13824, 256),   # the same with two row tiles
 ]
@@ -97,6 +98,24 @@ def test_linear_f32_parity(hip, M, N, K):
     # the fp32 epilogue is exactly ((float)acc * s_x) * s_w
     y_exact = (acc.astype(np.float32) * s[:, None]) * np.float32(scale)
     assert np.array_equal(y, y_exact)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 2560, 6912), (300, 2560, 2560), (2000, 2500, 4160)])
+def test_gemm_residual_epilogue(hip, M, N, K):
+    """The GEMM epilogue with a residual (region and tile kernels): y = r + ((acc s_x) s_w),
+    each a separate fp32 operation."""
+    import torch
+
+    rng = np.random.default_rng(M + N + K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    W, scale = O.make_ternary(rng, N, K)
+    r = rng.standard_normal((M, N), dtype=np.float32)
+    w = hip.upload(O.pack_rotor(W), K, scale)
+    act = hip.activations(M, K)
+    hip.act_quantize(torch.from_numpy(x).cuda(), act)
+    y = hip.linear_act(w, act, residual=torch.from_numpy(r).cuda()).cpu().numpy()
+    _, q, s, acc = O.ternary_linear(x, W, scale)
+    assert np.array_equal(y, r + (acc.astype(np.float32) * s[:, None]) * np.float32(scale))
 
 
 def test_extreme_accumulators(hip):
@@ -204,9 +223,11 @@ TILE_PLANS = {
     # the 512-token prefill's q/k/v and down: 64 x 128 tiles
     "qkv_m512": (512, [(2560, 2560, 0), (640, 2560, 0), (640, 2560, 0)], (64, 128, 240)),
     "down_m512": (512, [(2560, 6912, 0)], (64, 128, 160)),
-    # cfg 3: 256 x 256 (gate/up) and 192 x 128 (down) tiles
+    # cfg 3: 256 x 256 tiles (gate/up) and 128 x 160 regions (down)
     "cfg3_gate_up": (2048, [(6912, 2560, 0)], (256, 256, 216)),
-    "cfg3_down": (2048, [(2560, 6912, 0)], (192, 128, 220)),
+    "cfg3_down": (2048, [(2560, 6912, 0)], (128, 160, 256)),
+    # two long-K problems sharing one region launch (regions of problem 1 follow problem 0's)
+    "regions_two": (1024, [(2560, 4096, 0), (2400, 4096, 1)], (128, 160, 248)),
     # M = 100 (128-row activation padding): 128 x 128
     "m100": (100, [(2560, 2560, 0), (640, 2560, 1)], (128, 128, 25)),
 }

@@ -471,7 +471,7 @@ __global__ void __launch_bounds__(kRegThreads) gemm_region_kernel(GemmGroupArgs 
         };
         for (int k = 0; k < S - 1; ++k) load_chunk(cb + k);
         wait_vm<(S - 2) * LOADS>();
-        __syncthreads();  // barrier cb - 1: chunk cb in LDS
+        __builtin_amdgcn_s_barrier();  // barrier cb - 1: chunk cb in LDS (no fence: the wait is explicit)
         for (int c = cb; c + 1 < ce; ++c) {
             // barrier c - 1 passed: chunk c - 1's stage is free
             if (c + S - 1 < ce) {
@@ -552,7 +552,7 @@ __global__ void __launch_bounds__(kRegThreads) gemm_region_kernel(GemmGroupArgs 
             }
         };
         static_assert(FI == 8 && FJ == 5 && kMfma == 40, "chunk schedule");
-        __syncthreads();  // barrier cb - 1: chunk cb in LDS
+        __builtin_amdgcn_s_barrier();  // barrier cb - 1: chunk cb in LDS
 #pragma unroll
         for (int i = 0; i < HF; ++i) read_a(stage(cb), i);
 #pragma unroll
@@ -607,89 +607,121 @@ __global__ void __launch_bounds__(kRegThreads) gemm_region_kernel(GemmGroupArgs 
 
 // ---- M <= 64: K split over the waves ------------------------------------------------
 // One workgroup per 64-column tile of the output and all (<= 64) rows, over the unit's
-// chunks (a part of a long-K problem, GemmArgs::parts, or all C); wave w of NW covers an
-// NW-th of them.  Each wave fills a private LDS ring of S
-// stages by direct loads (4 A blocks + 1 weight chunk per step, S - 1 steps ahead) and
-// needs no barrier inside its loop: s_waitcnt on its own loads publishes a stage to
-// itself.  The NW int32 partial tiles are then summed in LDS (exact) and one pass
-// applies the fp32 epilogue.  Fragment reads, weight expansion and the result layout
-// are those of gemm_kernel (a wave tile of 64 x 64 = 2 x 2 blocks of 32 x 32).
+// chunks (a part of a long-K problem, GemmArgs::parts, or all C); compute wave w of NW
+// covers an NW-th of them (a wave tile of 64 x 64 = 2 x 2 blocks of 32 x 32, fragment
+// reads, weight expansion and result layout those of gemm_kernel) from a private LDS ring
+// of S stages.  Load wave NW + w fills that ring by direct loads (4 A blocks + 1 weight
+// chunk per step, S - 1 steps ahead): a wave that issues a load waits until the CU's load
+// path accepts it, which in the compute waves' stream cost more than their MFMAs.  One
+// barrier per step: load waves arrive once the next step is in LDS, compute waves after
+// the step's MFMAs (their reads of it returned), so the stage just read may be refilled.
+// Every wave runs the same number of steps (the larger share), a compute wave with one
+// chunk fewer skipping its last.  The NW int32 partial tiles are then summed in LDS
+// (exact) and all 2 NW waves apply the fp32 epilogue.  Two workgroups share a CU (80 KiB
+// of LDS, at most 128 registers per wave).
 template <int NW, int S>
-__global__ void __launch_bounds__(NW * 64) gemm_splitk_kernel(GemmGroupArgs ga) {
+__global__ void __launch_bounds__(2 * NW * 64, 4) gemm_splitk_kernel(GemmGroupArgs ga) {
     constexpr int STAGE = 4 * 1024 + 1024, LOADS = 5;  // A: 4 blocks of 16 rows; W: 1 chunk
+    constexpr int NT = 2 * NW * 64;                    // threads
     extern __shared__ __attribute__((aligned(16))) v4u lds[];
     char* const lds_b = reinterpret_cast<char*>(lds);
     const int t = threadIdx.x, lane = t & 63, g = lane >> 5, r32 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const bool loader = wave >= NW;
+    const int cw = loader ? wave - NW : wave;  // the compute wave this wave is or feeds
     const GemmArgs a = find_gemm(ga, blockIdx.x);
     const int C = a.C, rb = (int)blockIdx.x - a.wg_begin, n0 = rb * kRowBlock;
-    // this unit's chunks (one part of a split problem, or all), split over the waves
+    // this unit's chunks (one part of a split problem, or all), split over the compute waves
     const int k0 = a.c1 > 0 ? a.c0 : 0, len = (a.c1 > 0 ? a.c1 : C) - k0;
-    const int cb = k0 + __builtin_amdgcn_readfirstlane((wave * len) / NW);
-    const int ce = k0 + __builtin_amdgcn_readfirstlane(((wave + 1) * len) / NW);
-    char* const ring = lds_b + wave * S * STAGE;
-    const int8_t* a_src = a.qx + (size_t)lane * 16;  // block f of chunk c at (f C + c) KiB
-    const v4u* w_src = a.w + (size_t)(n0 / kRowBlock) * C * kRowBlock + lane;
-    auto issue = [&](int c) {
-        char* st = ring + (c % S) * STAGE;
-#pragma unroll
-        for (int f = 0; f < 4; ++f) load_lds16(a_src + ((size_t)f * C + c) * 1024, st + f * 1024);
-        load_lds16(w_src + (size_t)c * kRowBlock, st + 4096);
-    };
-    // per-lane read offsets in a stage (as gemm_kernel with WM = WN = 64)
-    const int a_rd = (r32 >> 4) * 1024 + ((r32 & 15) + 16 * g) * 16;
-    const int w_rd = 4096 + r32 * 16 + g * 4;  // column block j adds 32 rows = 512 bytes
+    const int cb = k0 + __builtin_amdgcn_readfirstlane((cw * len) / NW);
+    const int cnt = k0 + __builtin_amdgcn_readfirstlane(((cw + 1) * len) / NW) - cb;
+    const int steps = (len + NW - 1) / NW;
+    char* const ring = lds_b + cw * S * STAGE;
+    auto stg = [&](int s) { return ring + (s % S) * STAGE; };  // step s: chunk cb + s
 
     v16i acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
-    for (int c = cb; c < ce && c < cb + S - 1; ++c) issue(c);
-    for (int c = cb; c < ce; ++c) {
-        if (c + S - 1 < ce) {
-            issue(c + S - 1);  // its stage was read in step c - 1 (values already consumed)
-            wait_vm<(S - 1) * LOADS>();
-        } else {
-            wait_vm<0>();
+    if (loader) {
+        const int8_t* a_src = a.qx + (size_t)lane * 16;  // block f of chunk c at (f C + c) KiB
+        const v4u* w_src = a.w + (size_t)(n0 / kRowBlock) * C * kRowBlock + lane;
+        auto issue = [&](int s) {
+            char* st = stg(s);
+            const int c = cb + s;
+#pragma unroll
+            for (int f = 0; f < 4; ++f) load_lds16(a_src + ((size_t)f * C + c) * 1024, st + f * 1024);
+            load_lds16(w_src + (size_t)c * kRowBlock, st + 4096);
+        };
+        for (int s = 0; s < S - 1 && s < cnt; ++s) issue(s);
+        if (cnt >= S - 1) wait_vm<(S - 2) * LOADS>();
+        else wait_vm<0>();
+        __builtin_amdgcn_s_barrier();  // barrier -1: step 0 in LDS (no fence: the wait is explicit)
+        for (int s = 0; s + 1 < steps; ++s) {
+            // barrier s - 1 passed: step s - 1's stage is free
+            if (s + S - 1 < cnt) {
+                issue(s + S - 1);
+                wait_vm<(S - 2) * LOADS>();
+            } else {
+                wait_vm<0>();
+            }
+            __builtin_amdgcn_s_barrier();  // barrier s: step s + 1 in LDS
         }
-        const char* st = ring + (c % S) * STAGE;
-        v4i fa[2][2], fb[2][2];
+    } else {
+        // per-lane read offsets in a stage (as gemm_kernel with WM = WN = 64)
+        const int a_rd = (r32 >> 4) * 1024 + ((r32 & 15) + 16 * g) * 16;
+        const int w_rd = 4096 + r32 * 16 + g * 4;  // column block j adds 32 rows = 512 bytes
+        __builtin_amdgcn_s_barrier();              // barrier -1: step 0 in LDS
+        for (int s = 0; s < steps; ++s) {
+            if (s < cnt) {
+                const char* st = stg(s);
+                v4i fa[2][2], fb[2][2];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+                for (int h = 0; h < 2; ++h) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) fa[h][i] = *reinterpret_cast<const v4i*>(st + a_rd + i * 2048 + h * 512);
+                    for (int i = 0; i < 2; ++i) fa[h][i] = *reinterpret_cast<const v4i*>(st + a_rd + i * 2048 + h * 512);
 #pragma unroll
-            for (int j = 0; j < 2; ++j) fb[h][j] = decode_dword(*reinterpret_cast<const unsigned*>(st + w_rd + j * 512 + h * 8));
+                    for (int j = 0; j < 2; ++j)
+                        fb[h][j] = decode_dword(*reinterpret_cast<const unsigned*>(st + w_rd + j * 512 + h * 8));
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[h][i], fb[h][j], acc[i][j], 0, 0, 0);
+            }
+            if (s + 1 < steps) {
+                __builtin_amdgcn_sched_barrier(0);
+                asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // barrier s
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[h][i], fb[h][j], acc[i][j], 0, 0, 0);
     }
 
-    // sum the NW partial tiles: wave w stores its 64 x 64 int32 tile over its own ring
-    __syncthreads();  // every wave is done with its ring
-    int* part = reinterpret_cast<int*>(ring);
+    // sum the NW partial tiles: compute wave w stores its 64 x 64 int32 tile over its ring
+    __syncthreads();  // every wave is done with the rings
+    if (!loader) {
+        int* part = reinterpret_cast<int*>(ring);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+            for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int k = 0; k < 16; ++k)
-                part[(i * 32 + 8 * (k >> 2) + 4 * g + (k & 3)) * 64 + j * 32 + r32] = acc[i][j][k];
+                for (int k = 0; k < 16; ++k)
+                    part[(i * 32 + 8 * (k >> 2) + 4 * g + (k & 3)) * 64 + j * 32 + r32] = acc[i][j][k];
+    }
     __syncthreads();
-    // thread t: column n0 + t % 64, rows t / 64 + (NW) j, j < EPT; output and residual as
+    // thread t: column n0 + t % 64, rows t / 64 + 2 NW j, j < EPT; output and residual as
     // raw buffers over M rows (rows past M fall outside; a column past N adds bit 31)
-    constexpr int EPT = 64 * 64 / (NW * 64);
+    constexpr int EPT = 64 * 64 / NT, RS = NT / 64;  // elements per thread; row stride
     const int n = n0 + lane, mb = t >> 6;
     int v[EPT];
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
-        const int e = t + j * NW * 64;
+        const int e = t + j * NT;
         int acc_e = 0;
 #pragma unroll
         for (int w = 0; w < NW; ++w) acc_e += reinterpret_cast<const int*>(lds_b + w * S * STAGE)[e];
@@ -708,7 +740,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_splitk_kernel(GemmGroupArgs ga) 
         int* mine = a.part_ws + a.kp * tile + (size_t)rb * 4096;
 #pragma unroll
         for (int j = 0; j < EPT; ++j)
-            __hip_atomic_store(mine + (mb + NW * j) * 64 + lane, v[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(mine + (mb + RS * j) * 64 + lane, v[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (t == 0)
@@ -720,7 +752,7 @@ __global__ void __launch_bounds__(NW * 64) gemm_splitk_kernel(GemmGroupArgs ga) 
             const int* other = a.part_ws + p * tile + (size_t)rb * 4096;
 #pragma unroll
             for (int j = 0; j < EPT; ++j)
-                v[j] += __hip_atomic_load(other + (mb + NW * j) * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                v[j] += __hip_atomic_load(other + (mb + RS * j) * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         // every part of this row block has arrived: the count is ready for the next launch
         if (t == 0) __hip_atomic_store(a.cnt + rb, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -731,25 +763,25 @@ __global__ void __launch_bounds__(NW * 64) gemm_splitk_kernel(GemmGroupArgs ga) 
     if (a.out_i32) {
 #pragma unroll
         for (int j = 0; j < EPT; ++j)
-            __builtin_amdgcn_raw_buffer_store_b32((unsigned)v[j], out, (mb + NW * j) * a.ldo * 4 + coff, 0, 0);
+            __builtin_amdgcn_raw_buffer_store_b32((unsigned)v[j], out, (mb + RS * j) * a.ldo * 4 + coff, 0, 0);
         return;
     }
     const float sw = a.rs ? a.rs[min(n, a.N - 1)] : a.s_w;
     float sxv[EPT], rv[EPT];
 #pragma unroll
-    for (int j = 0; j < EPT; ++j) sxv[j] = a.sx[mb + NW * j];  // sx holds the 64 padded rows
+    for (int j = 0; j < EPT; ++j) sxv[j] = a.sx[mb + RS * j];  // sx holds the 64 padded rows
     const __amdgpu_buffer_rsrc_t res =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.res, 0, a.res ? range : 0u, kBufDword3);
     if (a.res) {
 #pragma unroll
         for (int j = 0; j < EPT; ++j)
-            rv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(res, (mb + NW * j) * a.ldo * 4 + coff, 0, 0));
+            rv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(res, (mb + RS * j) * a.ldo * 4 + coff, 0, 0));
     }
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
         const float y = ((float)v[j] * sxv[j]) * sw;
         const float o = a.res ? rv[j] + y : y;
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, o), out, (mb + NW * j) * a.ldo * 4 + coff, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, o), out, (mb + RS * j) * a.ldo * 4 + coff, 0, 0);
     }
 }
 
@@ -762,7 +794,7 @@ static hipError_t launch_splitk(const GemmGroupArgs& ga, int blocks, hipStream_t
                                                            hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
         if (attr != hipSuccess) return attr;
     }
-    hipLaunchKernelGGL((gemm_splitk_kernel<NW, S>), dim3((unsigned)blocks), dim3(NW * 64), LDS, s, ga);
+    hipLaunchKernelGGL((gemm_splitk_kernel<NW, S>), dim3((unsigned)blocks), dim3(2 * NW * 64), LDS, s, ga);
     return hipGetLastError();
 }
 

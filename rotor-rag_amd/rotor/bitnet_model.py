@@ -46,12 +46,18 @@ def rope_table(max_len: int, head_dim: int, theta: float) -> np.ndarray:
 
 
 class KVCache:
-    """Handle to the device KV cache of a model: `length` tokens of one sequence are cached.
+    """The KV cache of one sequence, read as the reference's list of per-layer caches
+    (src/rotor/bitnet_model.py:223-228 builds it from src/rotor/transformer.py:250-257):
+    ``len(cache)`` is the number of layers and ``cache[i]`` is ``{'k': K, 'v': V}``, float32
+    arrays ``[1, n_kv_heads, length, head_dim]`` copied from the device on access (keys
+    after RoPE, as this model attends with them).  ``cache.length`` is the number of
+    cached tokens.
 
     The cache memory belongs to the model and holds one sequence at a time: a forward that
     starts a new sequence (no past cache) or a generate_greedy call overwrites it, which
-    makes every older handle stale; passing a stale handle raises ValueError.  A handle of
-    the current sequence may be reused to continue (or rewind) from its length."""
+    makes every older handle stale; passing a stale handle, or reading one, raises
+    ValueError.  A handle of the current sequence may be reused to continue (or rewind)
+    from its length."""
 
     def __init__(self, model: "BitNetModel", length: int, epoch: int):
         self.model = model
@@ -59,7 +65,22 @@ class KVCache:
         self.epoch = epoch
 
     def __len__(self):
-        return self.length
+        return self.model.n_layers
+
+    def __getitem__(self, i):
+        if isinstance(i, slice):
+            return [self[j] for j in range(*i.indices(len(self)))]
+        n = len(self)
+        i = int(i)
+        if i < 0:
+            i += n
+        if not 0 <= i < n:
+            raise IndexError(f"layer {i} of a {n}-layer cache")
+        return self.model._dev.layer_cache(i, self.length, self.epoch)
+
+    def __iter__(self):
+        for i in range(len(self)):
+            yield self[i]
 
 
 class BitNetModel:
@@ -131,14 +152,26 @@ class BitNetModel:
     # ------------------------------------------------------------------ inference
     def forward(self, input_ids, return_logits: bool = True, past_kv_cache: Optional[KVCache] = None,
                 use_cache: bool = False):
-        """Same contract as src/rotor/bitnet_model.py:190-244: ids [seq] or [1, seq] ->
-        (logits [seq, vocab] (or [1, seq, vocab]), cache or None).  The KV cache stays on the
-        device; pass back the returned handle to continue a sequence."""
+        """Same contract as src/rotor/bitnet_model.py:190-244: ids [seq] or [batch, seq] ->
+        (logits [seq, vocab] (or [batch, seq, vocab]), cache or None).  The KV cache stays
+        on the device (a KVCache handle, readable as the reference's per-layer list); pass
+        it back to continue a sequence.  A batch of several sequences runs them one after
+        the other and keeps no cache (use_cache and past_kv_cache need batch 1)."""
         ids = np.asarray(input_ids)
         squeeze = ids.ndim == 1
+        if ids.ndim not in (1, 2):
+            raise ValueError("input_ids must be [seq] or [batch, seq]")
+        if ids.ndim == 2 and ids.shape[0] != 1:
+            # several sequences: each runs as its own sequence through the device cache, so
+            # they can share a forward only when no cache is kept between calls
+            if past_kv_cache is not None or use_cache:
+                raise ValueError("batch > 1 with a KV cache: the device cache holds one sequence; "
+                                 "run the sequences one at a time")
+            for row in ids:
+                self._dev._check_ids(row, 0)
+            outs = [self.forward(row, return_logits)[0] for row in ids]
+            return np.stack(outs), None
         if ids.ndim == 2:
-            if ids.shape[0] != 1:
-                raise ValueError("batch size 1 only")
             ids = ids[0]
         if past_kv_cache is not None:
             if past_kv_cache.model is not self or past_kv_cache.epoch != self._dev.epoch:
@@ -406,6 +439,16 @@ class _DeviceModel:
                                   self.token.data_ptr(), self.pos.data_ptr(), M, self.ids.data_ptr(),
                                   self.out_tokens.data_ptr(), pos_base, out_cap), "rt_lm_head_argmax")
         return st
+
+    def layer_cache(self, li, length, epoch):
+        """Layer li's cached K and V of the current sequence's first `length` tokens, as
+        float32 [1, Hkv, length, hd] host arrays."""
+        if epoch != self.epoch:
+            raise ValueError("stale KV cache: the model's device cache now holds a newer sequence")
+        L = self.layers[li]
+        k = L["kc"][:, :, :length].transpose(1, 2)  # the device keeps keys [Hkv, hd, Lmax]
+        v = L["vc"][:, :length, :]
+        return {"k": k.cpu().numpy()[None], "v": v.cpu().numpy()[None]}
 
     def _check_ids(self, ids, start):
         if len(ids) == 0:

@@ -374,7 +374,53 @@ def test_model_forward_matches_oracle(small_model):
     logits, cache = model.forward(np.array([42], np.int32), past_kv_cache=cache, use_cache=True)
     _, logits_o = O.bitnet_forward(params, SMALL, [42], oc)
     np.testing.assert_allclose(logits[0], logits_o, atol=0.05 * np.abs(logits_o).max(), rtol=0)
-    assert len(cache) == 9
+    assert cache.length == 9
+
+
+def test_kv_cache_reads_as_per_layer_list(small_model):
+    """The handle reads as the reference's list of per-layer {'k', 'v'} arrays
+    (src/rotor/bitnet_model.py:223-228, src/rotor/transformer.py:250-257), shaped
+    [1, Hkv, length, hd], equal to the oracle's cached keys (after RoPE) and values."""
+    model, params = small_model
+    ids = np.array([9, 8, 500, 7, 6], np.int32)
+    _, cache = model.forward(ids, use_cache=True)
+    _, cache = model.forward(np.array([33], np.int32), past_kv_cache=cache, use_cache=True)
+    oc = {}
+    O.bitnet_forward(params, SMALL, ids, oc)
+    O.bitnet_forward(params, SMALL, [33], oc)
+    Hkv, hd = SMALL["n_kv_heads"], SMALL["d_model"] // SMALL["n_heads"]
+    assert len(cache) == SMALL["n_layers"] and cache.length == 6
+    layers = list(cache)
+    assert len(layers) == SMALL["n_layers"]
+    for li, lc in enumerate(layers):
+        assert set(lc) == {"k", "v"}
+        for key in ("k", "v"):
+            assert lc[key].shape == (1, Hkv, 6, hd) and lc[key].dtype == np.float32
+            ref = oc[li][key]
+            np.testing.assert_allclose(lc[key][0], ref, atol=2e-2 * max(1.0, np.abs(ref).max()), rtol=0)
+    assert np.array_equal(cache[-1]["v"], layers[-1]["v"])
+    with pytest.raises(IndexError):
+        cache[SMALL["n_layers"]]
+    model.forward(np.array([1], np.int32))  # a new sequence: the handle is stale
+    with pytest.raises(ValueError, match="stale"):
+        cache[0]
+
+
+def test_model_batch_forward(small_model):
+    """[batch, seq] ids: each row as its own sequence, stacked like the reference's
+    [batch, seq, vocab] logits; a kept cache needs batch 1."""
+    model, _ = small_model
+    ids = np.array([[5, 6, 7, 8], [900, 1, 2, 3], [5, 6, 7, 9]], np.int32)
+    logits, cache = model.forward(ids)
+    assert logits.shape == (3, 4, SMALL["vocab_size"]) and cache is None
+    for b in range(3):
+        row, _ = model.forward(ids[b])
+        assert np.array_equal(logits[b], row)
+    assert np.array_equal(logits[0, :3], logits[2, :3])  # same prefix, causal
+    with pytest.raises(ValueError):
+        model.forward(ids, use_cache=True)
+    with pytest.raises(ValueError):
+        model.forward(np.array([[1, 2], [3, SMALL["vocab_size"]]], np.int32))
 
 
 def test_model_all_position_logits_shape(small_model):
@@ -416,7 +462,7 @@ def test_stale_kv_cache_rejected(small_model):
     _, c1 = model.forward(np.array([1, 2, 3], np.int32), use_cache=True)
     _, c2 = model.forward(np.array([4], np.int32), past_kv_cache=c1, use_cache=True)
     _, c3 = model.forward(np.array([5], np.int32), past_kv_cache=c2, use_cache=True)
-    assert len(c3) == 5
+    assert c3.length == 5
     with pytest.raises(ValueError):  # rejected ids: the cache and its handles stay valid
         model.forward(np.array([SMALL["vocab_size"]], np.int32), use_cache=True)
     model.forward(np.array([6], np.int32), past_kv_cache=c3)
@@ -495,7 +541,7 @@ def test_long_prompt_forward_matches_oracle(long_models, name, P):
     logits, cache = model.forward(np.array([42], np.int32), past_kv_cache=cache, use_cache=True)
     _, logits_o = O.bitnet_forward(params, cfg, [42], oc)
     np.testing.assert_allclose(logits[0], logits_o, atol=0.05 * np.abs(logits_o).max(), rtol=0)
-    assert len(cache) == P + 1
+    assert cache.length == P + 1
 
 
 @pytest.mark.parametrize("name", list(LONG_CFGS))

@@ -598,13 +598,12 @@ static hipError_t upload_gemm_group(rt_plan* p) {
     if (gemm_bm(p->M) == 64) return upload_splitk_group(p);
     std::vector<GemmArgs> g = p->gemms;
     std::vector<int> tile2p;
-    std::vector<int> Ns(g.size());
-    int Cmin = g[0].C;
+    std::vector<int> Ns(g.size()), Cs(g.size());
     for (size_t i = 0; i < g.size(); ++i) {
         Ns[i] = g[i].N;
-        Cmin = std::min(Cmin, g[i].C);
+        Cs[i] = g[i].C;
     }
-    p->gemm_cfg = gemm_tile_cfg(p->M, Ns.data(), (int)g.size(), Cmin);
+    p->gemm_cfg = gemm_tile_cfg(p->M, Ns.data(), Cs.data(), (int)g.size());
     long long total = 0;
     for (size_t i = 0; i < g.size(); ++i) {
         g[i].wg_begin = (int)total;

@@ -847,13 +847,22 @@ static hipError_t launch_tile_cfg(int cfg, const GemmGroupArgs& ga, int tiles, h
     }
 }
 
-int gemm_tile_cfg(int M, const int* N, int G, int C) {
+int gemm_tile_cfg(int M, const int* N, const int* C, int G) {
     if (gemm_bm(M) == 128) return kTile128x128;
-    if (C >= kRegMinC && C % 2 == 0) {  // long K: 128 x 160 regions when they make one round over the CUs
-        long long regions = 0;
-        for (int g = 0; g < G; ++g) regions += (long long)((M + kRegM - 1) / kRegM) * ((N[g] + kRegN - 1) / kRegN);
-        if (regions >= kRegMinTiles && regions <= kRegMaxTiles) return kRegion128x160;
+    // long K: 128 x 160 regions when they make one round over the CUs.  Every problem must
+    // split into two equal K halves (the halves' waves meet at one barrier per chunk) and
+    // keep the kernel's 32-bit buffer offsets: activations Mpad x Kp and weights Np x Kp / 4
+    // bytes below 2^31.
+    bool region_ok = true;
+    long long regions = 0;
+    const long long mpad = ((long long)M + 255) & ~255ll;
+    for (int g = 0; g < G; ++g) {
+        const long long np = ((long long)N[g] + kRowBlock - 1) / kRowBlock * kRowBlock;
+        region_ok = region_ok && C[g] >= kRegMinC && C[g] % 2 == 0 && mpad * C[g] * 64 < (1ll << 31) &&
+                    np * C[g] * 16 < (1ll << 31);
+        regions += (long long)((M + kRegM - 1) / kRegM) * ((N[g] + kRegN - 1) / kRegN);
     }
+    if (region_ok && regions >= kRegMinTiles && regions <= kRegMaxTiles) return kRegion128x160;
     const long long mt = (M + 255) / 256;
     const long long mt192 = (M + 191) / 192;
     long long t256 = 0, t128 = 0, t192 = 0;
@@ -888,7 +897,7 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
         one.wg_begin = 0;
         return launch_splitk<kSplitkWaves, 4>(GemmGroupArgs{nullptr, nullptr, one}, a.Np / kRowBlock, s);
     }
-    const int cfg = gemm_tile_cfg(a.M, &a.N, 1, a.C);
+    const int cfg = gemm_tile_cfg(a.M, &a.N, &a.C, 1);
     GemmArgs one = a;
     one.wg_begin = 0;
     return launch_tile_cfg(cfg, GemmGroupArgs{nullptr, nullptr, one}, (int)gemm_tile_count(cfg, a.M, a.N), s);

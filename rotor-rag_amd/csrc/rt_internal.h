@@ -332,9 +332,9 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s);
 // prefill's projections: 4.95 ms against 5.30 ms with 128 x 128): a few large tiles leave
 // most CUs idle.  192-row tiles do not divide the activations' 256-row padding: their
 // loads of rows past it re-read the last padded block (see gemm_kernel).  Before all of
-// these, problems at least kRegMinC chunks deep (K >= 4096) whose 128 x 160 regions number
-// kRegMinTiles..kRegMaxTiles take gemm_region_kernel (K split over the region's waves; C
-// is the smallest chunk count of the launch's problems).
+// these, launches whose problems are all at least kRegMinC chunks deep (K >= 4096) with an
+// even chunk count (C[g], the two K halves of a region walk equal steps) and whose 128 x 160
+// regions number kRegMinTiles..kRegMaxTiles take gemm_region_kernel.
 enum GemmTileCfg {
     kTile128x128 = 0,
     kTile256x128 = 1,
@@ -349,7 +349,7 @@ inline int gemm_tile_bm(int cfg) {
     return cfg == kTile64x128 ? 64 : cfg == kTile128x128 || cfg == kRegion128x160 ? 128 : cfg == kTile192x128 ? 192 : 256;
 }
 inline int gemm_tile_bn(int cfg) { return cfg == kTile256x256 ? 256 : cfg == kRegion128x160 ? 160 : 128; }
-int gemm_tile_cfg(int M, const int* N, int G, int C);
+int gemm_tile_cfg(int M, const int* N, const int* C, int G);
 long long gemm_tile_count(int cfg, int M, int N);
 // G problems with M > 64 in one tile launch: dev [G] (wg_begin = first tile of the
 // problem), tile2p [total_tiles] problem of every tile, cfg from gemm_tile_cfg.

@@ -39,7 +39,8 @@ LINEAR_CASES = [
     (512, 2560, 6912),
     (2048, 6912, 2560),  # cfg 3 (gate/up)
     (2048, 2560, 6912),  # cfg 3 (down): 128 x 160 regions, K split over the waves
-    (2000, 2500, 4160),  # regions with rows past M and a last region of 100 columns, odd chunks per half
+    (2000, 2500, 4224),  # regions with rows past M and a last region of 100 columns, 33 chunks per K half
+    (2000, 2500, 4160),  # the same with an odd chunk count: no regions (192-row tiles)
     (2000, 2560, 640),   # 192-row tiles, the last one past the 256-row padding
     (200, 13824, 256),   # the same with two row tiles
 ]
@@ -100,7 +101,7 @@ def test_linear_f32_parity(hip, M, N, K):
     assert np.array_equal(y, y_exact)
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 2560, 6912), (300, 2560, 2560), (2000, 2500, 4160)])
+@pytest.mark.parametrize("M,N,K", [(2048, 2560, 6912), (300, 2560, 2560), (2000, 2500, 4224), (2000, 2500, 4160)])
 def test_gemm_residual_epilogue(hip, M, N, K):
     """The GEMM epilogue with a residual (region and tile kernels): y = r + ((acc s_x) s_w),
     each a separate fp32 operation."""
@@ -228,6 +229,10 @@ TILE_PLANS = {
     "cfg3_down": (2048, [(2560, 6912, 0)], (128, 160, 256)),
     # two long-K problems sharing one region launch (regions of problem 1 follow problem 0's)
     "regions_two": (1024, [(2560, 4096, 0), (2400, 4096, 1)], (128, 160, 248)),
+    # ragged regions: rows past M, a last region of 100 columns, 33 chunks per K half
+    "regions_ragged": (2000, [(2500, 4224, 0)], (128, 160, 256)),
+    # a problem with an odd chunk count keeps the whole launch off the regions
+    "regions_mixed_parity": (1024, [(2560, 4096, 0), (2400, 4160, 1)], (192, 128, 234)),
     # M = 100 (128-row activation padding): 128 x 128
     "m100": (100, [(2560, 2560, 0), (640, 2560, 1)], (128, 128, 25)),
 }

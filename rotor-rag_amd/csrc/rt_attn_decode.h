@@ -20,6 +20,16 @@ namespace rt {
 
 constexpr int kAttnBlock = 64;  // keys per split
 
+// Workgroup barrier for the tile's LDS hand-offs: waits for this wave's LDS accesses only.
+// __syncthreads() also waits for the wave's outstanding global stores (its fence), which
+// held every tile of a workgroup behind the new key's cache stores and the partials' stores
+// (their round trip to memory) at each later barrier; nothing in the launch reads those.
+__device__ __forceinline__ void attn_lds_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 template <int HD>
 struct AttnTileLds {
     float qs[HD];
@@ -73,7 +83,7 @@ __device__ __forceinline__ void attn_rope_load(const float* __restrict__ rope, i
 }
 
 // The tile's work once the position is known and the block holds at least one key
-// (pos >= j0).  Every thread of the workgroup passes the tile's three barriers.
+// (pos >= j0).  Every thread of the workgroup passes the tile's four barriers.
 // qh: the head's query (HD values); kn, vn: the head's KV group's new key and value (ROPE),
 // in global memory or in LDS (SRC, a pointer type); c, sn: attn_rope_load's factors (ROPE).
 // ROPE: qh, kn, vn are the raw projection outputs of the token at pos.  The tile rotates
@@ -112,7 +122,7 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
     } else {
         for (int e = t; e < HD; e += 256) sm->qs[e] = qh[e];
     }
-    __syncthreads();
+    attn_lds_barrier();
     if (holds_new && writer)  // one writer per KV head
         for (int e = t; e < HD; e += 256) {
             Kc[((size_t)kh * HD + e) * Lmax + pos] = sm->ks[e];
@@ -139,7 +149,7 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
         a3 += sm->qs[dd + 3] * kk[i + 3];
     }
     sm->part[wave][lane] = (a0 + a1) + (a2 + a3);
-    __syncthreads();
+    attn_lds_barrier();
     if (wave == 0) {
         float sc = lane < nk
                        ? (((sm->part[0][lane] + sm->part[1][lane]) + (sm->part[2][lane] + sm->part[3][lane])) * scale)
@@ -153,12 +163,15 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
             wp[HD + 1] = z;
         }
     }
-    __syncthreads();
+    attn_lds_barrier();
     // unnormalised output: thread (d, g) sums keys g, g + G, ... of the block, two
     // alternating partial sums.  The new key's value and the mask of keys past the
-    // block's last cost VALU work only in the block that needs them (both conditions are
-    // uniform over the workgroup): four tiles share a CU in the qkv launch, where this
-    // loop is VALU-bound.  No branches inside: the LDS reads go out together.
+    // position cost VALU work only where they apply: four tiles share a CU in the qkv
+    // launch, where this loop is VALU-bound.  The keys go in runs of CH; g is uniform
+    // over a wave and nk over the workgroup, so a run lies wholly before nk (plain sums),
+    // wholly past it (skipped) or across it (masked sums) by a uniform branch, and the
+    // LDS reads of a run go out together.  Skipping a masked key leaves the sums as the
+    // masked form does, so the order of the additions is the same in every block.
     float vv[VN];
 #pragma unroll
     for (int i = 0; i < VN; ++i) vv[i] = kv.v[i];
@@ -168,23 +181,29 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
         for (int i = 0; i < VN; ++i) vv[i] = g + i * G == lp ? vs_d : vv[i];
     }
     float o0 = 0.f, o1 = 0.f;
-    if (nk == BL) {
+    constexpr int CH = VN >= 8 ? 8 : VN;
+    static_assert(VN % CH == 0 && CH % 2 == 0, "runs of key pairs");
 #pragma unroll
-        for (int i = 0; i < VN; i += 2) {
-            o0 += sm->pr[g + i * G] * vv[i];
-            o1 += sm->pr[g + (i + 1) * G] * vv[i + 1];
-        }
-    } else {
+    for (int c0 = 0; c0 < VN; c0 += CH) {
+        const int first = g + c0 * G, last = g + (c0 + CH - 1) * G;
+        if (last < nk) {
 #pragma unroll
-        for (int i = 0; i < VN; i += 2) {
-            const int ja = g + i * G, jb = g + (i + 1) * G;
-            const float sa = o0 + sm->pr[ja] * vv[i], sb = o1 + sm->pr[jb] * vv[i + 1];
-            o0 = ja < nk ? sa : o0;
-            o1 = jb < nk ? sb : o1;
+            for (int i = c0; i < c0 + CH; i += 2) {
+                o0 += sm->pr[g + i * G] * vv[i];
+                o1 += sm->pr[g + (i + 1) * G] * vv[i + 1];
+            }
+        } else if (first < nk) {
+#pragma unroll
+            for (int i = c0; i < c0 + CH; i += 2) {
+                const int ja = g + i * G, jb = g + (i + 1) * G;
+                const float sa = o0 + sm->pr[ja] * vv[i], sb = o1 + sm->pr[jb] * vv[i + 1];
+                o0 = ja < nk ? sa : o0;
+                o1 = jb < nk ? sb : o1;
+            }
         }
     }
     sm->ored[t] = o0 + o1;
-    __syncthreads();
+    attn_lds_barrier();
     if (g == 0) {
         float o = sm->ored[d];
         for (int gg = 1; gg < G; ++gg) o += sm->ored[gg * HD + d];

@@ -87,8 +87,13 @@ def test_rope_append_and_attention(hip, M, pos0, H, Hkv, hd, Lmax):
     np.testing.assert_allclose(out.cpu().numpy(), ref, atol=2e-5, rtol=1e-4)
 
 
+# The last block's key count nk = pos0 % 64 + 1 walks the value sums' runs of 8 key pairs:
+# hd 128 (2 key groups): runs of 16 keys, so nk 16 ends a run, 17 opens one, 25 and 31 end
+# inside one; hd 64 (4 groups): runs of 32 keys.
 @pytest.mark.parametrize("pos0,H,Hkv,hd,Lmax", [(0, 20, 5, 128, 640), (63, 20, 5, 128, 640), (64, 8, 2, 64, 200),
                                                 (511, 20, 5, 128, 640), (639, 20, 5, 128, 640), (100, 4, 4, 64, 130),
+                                                (527, 20, 5, 128, 640), (528, 20, 5, 128, 640), (600, 20, 5, 128, 640),
+                                                (606, 20, 5, 128, 640), (95, 8, 2, 64, 200),
                                                 (700, 8, 2, 64, 1000)])  # 16 blocks: general prologue path
 def test_attention_decode_split(hip, pos0, H, Hkv, hd, Lmax):
     """Flash-decoding form equals the single-workgroup form; the workspace is reusable."""
@@ -135,7 +140,8 @@ def test_attention_decode_split(hip, pos0, H, Hkv, hd, Lmax):
 
 
 @pytest.mark.parametrize("pos0,H,Hkv,hd,Lmax", [(0, 20, 5, 128, 640), (63, 20, 5, 128, 640), (64, 8, 2, 64, 200),
-                                                (639, 20, 5, 128, 640), (130, 4, 4, 64, 131)])
+                                                (639, 20, 5, 128, 640), (130, 4, 4, 64, 131), (527, 20, 5, 128, 640),
+                                                (600, 20, 5, 128, 640)])
 def test_rope_attention_decode_equals_separate_launches(hip, pos0, H, Hkv, hd, Lmax):
     """One launch of RoPE + KV append + split attention gives the partials, the combined
     output and the caches of rt_rope_kv_append followed by rt_attention_decode, bit for

@@ -13,7 +13,10 @@ can silently lose:
   * no lane read (v_readfirstlane / v_readlane) is written as inline asm: the compiler
     inserts no wait states before an asm statement that reads a VGPR its previous VALU
     instruction wrote, and such a read can return the stale value (it did, for the GEMV's
-    chunk bounds, with wrong sums as the result).
+    chunk bounds, with wrong sums as the result);
+  * the cross-workgroup hand-offs that run without a fence (the split-K parts' int32
+    tiles, the decode q/k/v outputs polled by the attention workgroups) keep their
+    device-coherent stores and loads and the wait before the arrival count.
 """
 import re
 import shutil
@@ -146,3 +149,42 @@ def test_splitk_uses_no_static_lds(gemm):
     for n in [n for n in gemm if "gemm_splitk_kernel" in n]:
         m = re.search(r"\.amdhsa_group_segment_fixed_size\s+(\d+)", gemm["__meta__"][n])
         assert m and int(m.group(1)) == 0, n
+
+
+def test_splitk_exchange_is_coherent(gemm):
+    # The split-K parts hand their int32 tiles to the last arriver without a fence: the
+    # tiles are stored device-coherent (sc1), every store has completed (s_waitcnt
+    # vmcnt(0)) and the workgroup has passed a barrier before the arrival count is added
+    # to, and the last arriver reads the other parts' tiles device-coherent.  A compiler
+    # that dropped the coherence bits or moved the wait would break the exchange silently.
+    for n in [n for n in gemm if "gemm_splitk_kernel" in n]:
+        t = gemm[n]
+        i = t.index("global_atomic_add")
+        before, after = t[:i], t[i:]
+        stores = re.findall(r"global_store_dword\b[^\n]*", before)
+        assert stores and all(re.search(r"\bsc1\b", s) for s in stores), f"{n}: tile stores {stores}"
+        tail = before[before.rindex("global_store_dword"):]
+        assert re.search(r"s_waitcnt vmcnt\(0\)(.|\n)*s_barrier", tail), f"{n}: no wait + barrier before the count"
+        # the last arriver's reads of the other parts' tiles: from the count to its reset
+        # (a device-coherent store of zero); the epilogue's scale loads follow
+        reset = re.search(r"global_store_dword\b[^\n]*\bsc1\b", after)
+        assert reset, f"{n}: no device-coherent reset of the arrival count"
+        loads = re.findall(r"global_load_dword\b[^\n]*", after[:reset.start()])
+        assert loads and all(re.search(r"\bsc1\b", s) for s in loads), f"{n}: tile loads {loads}"
+
+
+def test_attention_handoff_is_coherent(gemv):
+    # The q/k/v GEMV of the decode step stores its outputs as 64-bit (epoch, value) words
+    # device-coherent (sc1) and the attention workgroups of the same launch poll them with
+    # device-coherent loads (between s_sleep); the epoch is read coherent too.
+    names = [n for n in gemv if "gemv_ksplit_kernel" in n and "AttnTail" in n]
+    assert len(names) >= 3, names
+    for n in names:
+        t = gemv[n]
+        lines = t.splitlines()
+        sleeps = [i for i, l in enumerate(lines) if "s_sleep" in l]
+        polls = [l for i in sleeps for l in lines[i + 1:i + 9] if "global_load_dwordx2" in l]
+        assert polls and all(re.search(r"\bsc1\b", l) for l in polls), f"{n}: polls {polls}"
+        tagged = [l for l in re.findall(r"global_store_dwordx2[^\n]*", t) if re.search(r"\bsc1\b", l)]
+        assert tagged, f"{n}: no device-coherent 64-bit store of the tagged outputs"
+        assert re.search(r"global_load_dword\b[^\n]*\bsc1\b", t), f"{n}: the epoch is not read coherent"

@@ -53,12 +53,6 @@ typedef struct rt_act rt_act;         /* reusable quantised activations        *
 #define RT_SRC_RMSNORM_SSQ 6    /* as RT_SRC_RMSNORM, with sum_k x^2 given as K/32 f64 partial
                                    sums: aux2 = (const float*) the `ssq` array written by an
                                    rt_plan_create_gate_up plan (K % 64 == 0, K <= 8192) */
-#define RT_SRC_RMSNORM_STATS 7  /* as RT_SRC_RMSNORM, with the row's statistics given: aux2 =
-                                   (const float*) the RT_ROWSTAT_BYTES * K / 32 bytes written by
-                                   the plan that produced x (rt_plan_set_row_stats); the decode
-                                   GEMV then needs no workgroup-wide reduction (K % 64 == 0,
-                                   K <= 8192, 16-byte aligned x, aux and records) */
-#define RT_ROWSTAT_BYTES 32     /* statistics of 32 consecutive row elements */
 typedef struct rt_src {
     int mode;           /* RT_SRC_*                                  */
     const float* x;     /* fp32 [K] (device); partials for ATTN_NORM */
@@ -75,7 +69,9 @@ const char* rt_last_error(void);
 
 /* ABI version (major*100 + minor): 101 = 100 + rt_plan_create_gate_up and RT_SRC_RMSNORM_SSQ;
  * 102 = 101 + rt_plan_describe; 103 = 102 + rt_linear_f32_noalloc; 104 = 103 + rt_plan_set_row_stats
- * and RT_SRC_RMSNORM_STATS; 105 = 104 + rt_plan_attach_attention and rt_plan_attention_timeouts. */
+ * and RT_SRC_RMSNORM_STATS; 105 = 104 + rt_plan_attach_attention and rt_plan_attention_timeouts;
+ * 106 = 105 without rt_plan_set_row_stats and RT_SRC_RMSNORM_STATS (measured slower than each
+ * decode prologue reducing its own row), + rt_attention_decode_combine. */
 int rt_version(void);
 
 /* Number of visible HIP devices (0 when none); RT_OK even when 0. */
@@ -249,17 +245,6 @@ int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const r
 int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, float s_up, const rt_src* src,
                            float* a, double* ssq, float* g_out, float* u_out, rt_plan** out);
 
-/* Let a one-problem fused decode plan (rt_plan_create_fused with G = 1, or a gate/up pair
- * plan) also write the statistics that the NEXT plan's RMSNorm + quantiser needs of its
- * output row y (the output after the residual; the pair plan's a): per 32 consecutive
- * outputs, RT_ROWSTAT_BYTES at `stats` (N / 32 records, device, 16-byte aligned), taken
- * against next_norm_w fp32 [N] (device), the weight of that RMSNorm.  A plan with source
- * RT_SRC_RMSNORM_STATS, x = y, aux = next_norm_w and aux2 = stats then quantises exactly as
- * RT_SRC_RMSNORM would, with no workgroup-wide reduction in its prologue.  NULL, NULL
- * detaches.  Fuses the norm statistics of the next RMSNorm (src/rotor/transformer.py:24-36)
- * into the linear that produces its input (:329-339, :396-411). */
-int rt_plan_set_row_stats(rt_plan* plan, const float* next_norm_w, void* stats);
-
 /* Run the decode step's RoPE + KV append + attention partials (rt_rope_attention_decode
  * with out = NULL, same arguments, same results bit for bit) inside rt_plan_run's launch of
  * a fused q/k/v plan: rt_plan_create_fused with G = 3 over the q, k and v projections
@@ -311,6 +296,14 @@ int rt_attention_decode(rt_ctx* ctx, const float* q, const float* k_cache, const
                         int Hkv, int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes);
 int rt_attention_decode_partials(rt_ctx* ctx, const float* q, const float* k_cache, const float* v_cache, int H,
                                  int Hkv, int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes);
+/* The second launch of rt_attention_decode on its own: the per-head combine of the
+ * partials in `workspace` (left by rt_attention_decode_partials, rt_rope_attention_decode
+ * or a q/k/v plan with the attention attached) into out [H*hd], in the operation order a
+ * RT_SRC_ATTN_NORM plan's prologue uses, so both see the same attention output.  Reads the
+ * workspace only.  Replaces, for one token, src/rotor/transformer.py:268-281 (softmax and
+ * the weighted sum of the values, per head). */
+int rt_attention_decode_combine(rt_ctx* ctx, const void* workspace, size_t workspace_bytes, int H, int hd, int Lmax,
+                                float* out);
 
 /* The decode step's RoPE + KV append + rt_attention_decode_partials in one launch, for the
  * single token at *pos: q [H*hd], k and v [Hkv*hd] are the raw projection outputs (not

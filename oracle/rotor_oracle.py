@@ -165,14 +165,19 @@ def linear_i64(q, W):
 
 
 def linear_i64_fast(q, W):
-    """Same result as :func:`linear_i64` computed with float64 BLAS.
+    """Same result as :func:`linear_i64` computed with floating-point BLAS.
 
-    Exact: every product and partial sum is an integer of magnitude < 2**53
-    (|q| <= 128, |W| <= 1, K < 2**40), so no rounding occurs.
+    Exact: every product and partial sum is an integer of magnitude at most 128 K
+    (|q| <= 128, |W| <= 1): below 2**24 in float32 (K < 131072), else below 2**53 in
+    float64 (K < 2**40), so no rounding occurs in any summation order.
     """
-    q = np.asarray(q, dtype=np.float64)
-    W = np.asarray(W, dtype=np.float64)
-    assert q.shape[-1] < (1 << 40)
+    K = np.asarray(q).shape[-1]
+    assert K < (1 << 40)
+    # with int8 q and ternary W, |partial sums| <= 128 K: below 2^24 they are exact in
+    # float32 too (half the memory traffic of the float64 product)
+    dt = np.float32 if 128 * K < (1 << 24) and np.abs(np.asarray(q)).max(initial=0) <= 128 else np.float64
+    q = np.asarray(q, dtype=dt)
+    W = np.asarray(W, dtype=dt)
     return (q @ W.T).astype(np.int64)
 
 
@@ -315,23 +320,27 @@ def apply_rope(x, table, pos0):
 def causal_gqa_attention(q, K, V, pos0):
     """q [M, H, hd] (queries at pos0..), K/V [Hkv, L, hd] (all cached keys) ->
     out [M, H, hd]; scale 1/sqrt(hd); query m sees keys 0..pos0+m.  Computed in f64
-    (src/rotor/transformer.py:260-281 plus the causal mask of the configuration)."""
+    (src/rotor/transformer.py:260-281 plus the causal mask of the configuration), all
+    queries of a head at once with the keys past each query masked out."""
     M, H, hd = q.shape
     Hkv = K.shape[0]
     rep = H // Hkv
-    out = np.zeros((M, H, hd), np.float64)
+    L = pos0 + M
     scale = np.float32(1.0) / np.sqrt(np.float32(hd))
-    for m in range(M):
-        L = pos0 + m + 1
-        for h in range(H):
-            kk = K[h // rep, :L].astype(np.float64)
-            sc = (kk @ q[m, h].astype(np.float64)) * np.float64(scale)
-            p = np.exp(sc - sc.max())
-            out[m, h] = (p / p.sum()) @ V[h // rep, :L].astype(np.float64)
+    visible = np.arange(L)[None, :] <= (pos0 + np.arange(M))[:, None]  # [M, L]
+    out = np.zeros((M, H, hd), np.float64)
+    for kv in range(Hkv):
+        kk = K[kv, :L].astype(np.float64)
+        vv = V[kv, :L].astype(np.float64)
+        for h in range(kv * rep, (kv + 1) * rep):
+            sc = (q[:, h].astype(np.float64) @ kk.T) * np.float64(scale)
+            sc = np.where(visible, sc, -np.inf)
+            p = np.exp(sc - sc.max(axis=1, keepdims=True))
+            out[:, h] = (p / p.sum(axis=1, keepdims=True)) @ vv
     return out.astype(np.float32)
 
 
-def bitnet_forward(params, cfg, ids, cache, attn_in=None, attn_ref=None):
+def bitnet_forward(params, cfg, ids, cache, attn_in=None, attn_ref=None, x_out=None):
     """One forward of the cfg-4 model on token ids [M] at position len(cache)
     (cache: dict with per-layer K/V lists, updated in place).  Returns the final-normed
     hidden states [M, D] and the logits of the last token [V] (f64 accumulation).
@@ -342,7 +351,8 @@ def bitnet_forward(params, cfg, ids, cache, attn_in=None, attn_ref=None):
     attn_in (optional, per layer [M, H*hd] fp32): attention outputs to continue each layer
     with in place of the ones computed here (teacher forcing: every other operation is
     reproducible bit for bit, attention only to fp32 summation order); attn_ref (optional
-    list) receives the attention outputs computed here, layer by layer.
+    list) receives the attention outputs computed here, layer by layer; x_out (optional
+    list) receives the hidden states [M, D] before the final norm.
     """
     H, Hkv, eps = cfg["n_heads"], cfg["n_kv_heads"], cfg.get("rms_norm_eps", 1e-6)
     D = cfg["d_model"]
@@ -380,6 +390,8 @@ def bitnet_forward(params, cfg, ids, cache, attn_in=None, attn_ref=None):
         qd, sd = quant_rows(act)
         x = x + w2a8_linear_from_q(qd, sd, L["down_proj"][0], L["down_proj"][1])[0]
     cache["len"] = pos0 + M
+    if x_out is not None:
+        x_out.append(x)
     hn = rms_norm_f64acc(x, params["final_norm"], eps)
     # the tied head in f64 (products of two f32 values are exact); the f64 copy of the
     # embedding is made once per parameter set (2.6 GB at V = 128256, D = 2560)
@@ -406,10 +418,13 @@ def bitnet_greedy(params, cfg, prompt, n):
     return np.array(toks), np.array(gaps)
 
 
-def make_bitnet_params(seed, cfg, max_len, sub_norms=True):
+def make_bitnet_params(seed, cfg, max_len, sub_norms=True, fast=False):
     """Seeded random-init cfg-4 weights: ternary matrices and scales as in cfg 0,
-    norm weights ~U(0.5, 1.5), bf16 embedding ~N(0, 1)."""
+    norm weights ~U(0.5, 1.5), bf16 embedding ~N(0, 1).  fast=True draws the ternary values
+    with make_ternary_fast (the same distribution, another stream of numbers; for the
+    30-layer model, where make_ternary takes minutes)."""
     rng = np.random.default_rng(seed)
+    ternary = make_ternary_fast if fast else make_ternary
     D, F, H, Hkv, V = cfg["d_model"], cfg["d_ff"], cfg["n_heads"], cfg["n_kv_heads"], cfg["vocab_size"]
     hd = D // H
     shapes = {"q_proj": (H * hd, D), "k_proj": (Hkv * hd, D), "v_proj": (Hkv * hd, D), "o_proj": (D, H * hd),
@@ -419,11 +434,11 @@ def make_bitnet_params(seed, cfg, max_len, sub_norms=True):
         L = {"input_norm": rng.uniform(0.5, 1.5, D).astype(np.float32),
              "post_norm": rng.uniform(0.5, 1.5, D).astype(np.float32)}
         for name, (n, k) in shapes.items():
-            L[name] = make_ternary(rng, n, k)
+            L[name] = ternary(rng, n, k)
         L["attn_sub_norm"] = rng.uniform(0.5, 1.5, D).astype(np.float32) if sub_norms else None
         L["ffn_sub_norm"] = rng.uniform(0.5, 1.5, F).astype(np.float32) if sub_norms else None
         layers.append(L)
-    embed = f32_to_bf16(rng.standard_normal((V, D), dtype=np.float32))
+    embed = (f32_to_bf16_fast if fast else f32_to_bf16)(rng.standard_normal((V, D), dtype=np.float32))
     final_norm = rng.uniform(0.5, 1.5, D).astype(np.float32)
     return {"layers": layers, "embed": embed, "final_norm": final_norm,
             "rope": rope_table(max_len, hd, cfg.get("rope_theta", 500000.0))}
@@ -439,6 +454,21 @@ def make_ternary(rng, N, K):
     W = rng.choice(np.array([-1, 0, 1], dtype=np.int8), size=(N, K), p=[0.3, 0.4, 0.3]).astype(np.int8)
     scale = np.float32(rng.uniform(0.01, 0.05))
     return W, scale
+
+
+def make_ternary_fast(rng, N, K):
+    """As make_ternary, from uniform bytes in [0, 10): 0-2 -> -1, 3-6 -> 0, 7-9 -> +1
+    (P = 0.3 / 0.4 / 0.3 exactly), then the scale."""
+    u = rng.integers(0, 10, size=(N, K), dtype=np.uint8)
+    W = (u >= 7).astype(np.int8) - (u <= 2).astype(np.int8)
+    scale = np.float32(rng.uniform(0.01, 0.05))
+    return W, scale
+
+
+def f32_to_bf16_fast(x):
+    """f32_to_bf16 in 32-bit integer arithmetic (no overflow for finite inputs)."""
+    u = np.asarray(x, np.float32).view(np.uint32)
+    return ((u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
 
 
 def make_linear_case(seed, M, N, K):
@@ -462,7 +492,9 @@ PINNED = {
     "rms_norm/relu2_gate/ffn_block": "closed forms: constant rows, unit weight, sign cases",
     "rms_norm_f64acc": "closed forms (constant rows -> +-w); agrees with rms_norm within 1 ulp",
     "ffn_block_w2a8": "composition of pinned functions; equals ffn_block when intermediates agree",
-    "bf16/rope/attention/bitnet_forward": "bf16 round trip; RoPE norm preservation and pos-0 identity; attention "
-                                          "closed forms (one key -> V, equal keys -> mean of V, causal prefix); "
-                                          "incremental decode == full-sequence forward",
+    "bf16/rope/attention/bitnet_forward": "bf16 round trip; RoPE norm preservation, pos-0 identity and frequency "
+                                          "KAT; attention closed forms (one key -> V, equal keys -> mean of V, "
+                                          "causal prefix, two keys -> logistic mix sig(a/sqrt(hd)) at the score "
+                                          "scale 1/sqrt(hd), which 1/hd or no scale fails); incremental decode == "
+                                          "full-sequence forward",
 }

@@ -91,8 +91,6 @@ struct Scratch {
 // symbol, not a device address: the address is resolved per device with
 // hipGetSymbolAddress (device current) and only that pointer is used.
 static_assert(RT_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size");
-static_assert(sizeof(RowStat) == RT_ROWSTAT_BYTES && kStatRows == 32 && RT_SRC_RMSNORM_STATS == kRmsNormStats,
-              "statistics records of the C ABI");
 static __device__ __align__(256) unsigned char scratch[RT_NOALLOC_SCRATCH_BYTES];
 
 namespace {
@@ -114,6 +112,20 @@ hipError_t noalloc_scratch(int dev, void** out) {
     }
     *out = addr[dev];
     return hipSuccess;
+}
+
+// Once per device `dev` (current): the kernels' function attributes, so that no launch
+// (e.g. the first one of a shape inside a stream capture) makes a function-attribute call.
+hipError_t prepare_device(int dev) {
+    static std::mutex mu;
+    static bool done[kMaxDevices] = {};
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (done[dev]) return hipSuccess;
+    hipError_t e = gemm_prepare_device();
+    if (e == hipSuccess) e = model_prepare_device();
+    if (e == hipSuccess) done[dev] = true;
+    return e;
 }
 
 }  // namespace
@@ -164,8 +176,6 @@ struct rt_plan {
     float* pair_g = nullptr;      // optional g, u [N / 2]
     float* pair_u = nullptr;
     float pair_sg = 1.0f, pair_su = 1.0f;  // gate and up scales
-    RowStat* stat_out = nullptr;  // rt_plan_set_row_stats: the epilogue's statistics records
-    const float* stat_w = nullptr;  // and the next RMSNorm's weight they are taken against
     int quant_maxK = 0;  // > 0: every quant problem takes the vectorised row kernel (largest K)
     // rt_plan_attach_attention: the decode attention partials run in rt_plan_run's launch
     bool att_on = false;
@@ -192,7 +202,7 @@ extern "C" {
 
 const char* rt_last_error(void) { return g_err.c_str(); }
 
-int rt_version(void) { return 105; }
+int rt_version(void) { return 106; }
 
 int rt_device_count(int* n) {
     if (!n) return fail(RT_EINVAL, "rt_device_count: n is NULL");
@@ -216,6 +226,7 @@ int rt_ctx_create(int device, rt_ctx** out) {
     RT_HIP(hipSetDevice(device));
     void* sp = nullptr;
     RT_HIP(noalloc_scratch(device, &sp));
+    RT_HIP(prepare_device(device));
     rt_ctx* c = new rt_ctx();
     c->device = device;
     c->noalloc = static_cast<int8_t*>(sp);
@@ -834,8 +845,6 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
         a.pair_u = plan->pair_u;
         a.pair_sg = plan->pair_sg;
         a.pair_su = plan->pair_su;
-        a.stat_out = plan->stat_out;
-        a.stat_w = plan->stat_w;
     }
     a.dev = plan->dev_probs;
     a.rb2p = plan->dev_rb2p;
@@ -1100,6 +1109,18 @@ int rt_attention_decode(rt_ctx* ctx, const float* q, const float* k_cache, const
     return RT_OK;
 }
 
+int rt_attention_decode_combine(rt_ctx* ctx, const void* workspace, size_t workspace_bytes, int H, int hd, int Lmax,
+                                float* out) {
+    const char* who = "rt_attention_decode_combine";
+    if (!ctx || !workspace || !out) return fail(RT_EINVAL, std::string(who) + ": NULL argument");
+    if (H <= 0 || hd <= 0 || Lmax <= 0) return fail(RT_EINVAL, std::string(who) + ": H, hd and Lmax must be positive");
+    if (workspace_bytes < rt_attention_decode_workspace(H, hd, Lmax))
+        return fail(RT_EINVAL, std::string(who) + ": workspace too small");
+    DeviceGuard g(ctx->device);
+    RT_HIP(launch_attn_combine(static_cast<const float*>(workspace), H, hd, attn_splits(Lmax), out, ctx->stream));
+    return RT_OK;
+}
+
 int rt_lm_head_argmax(rt_ctx* ctx, const uint16_t* emb, const float* x, const float* norm_w, float eps, int V, int D,
                       float* logits, unsigned long long* best, int* token, int* pos, int advance, int* next_ids,
                       int* out_tokens, int pos_base, int out_cap) {
@@ -1122,21 +1143,18 @@ int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const r
     if (G <= 0 || G > (1 << 16)) return fail(RT_EINVAL, "rt_plan_create_fused: G out of range");
     if (!src->x) return fail(RT_EINVAL, "rt_plan_create_fused: source x is NULL");
     if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRelu2Mul && src->mode != kRelu2MulNorm &&
-        src->mode != kAttnNorm && src->mode != kRmsNormSsq && src->mode != kRmsNormStats)
+        src->mode != kAttnNorm && src->mode != kRmsNormSsq)
         return fail(RT_EINVAL, "rt_plan_create_fused: unknown source mode");
     if (src->mode == kAttnNorm && (src->attn_head_dim <= 0 || src->attn_head_dim % 16 || src->attn_max_len <= 0 ||
                                    !w[0] || w[0]->K % src->attn_head_dim))
         return fail(RT_EINVAL, "rt_plan_create_fused: attention source needs head_dim (multiple of 16) dividing K "
                                "and max_len");
     if ((src->mode != kQuant && !src->aux) ||
-        ((src->mode == kRelu2MulNorm || src->mode == kRmsNormSsq || src->mode == kRmsNormStats) && !src->aux2))
+        ((src->mode == kRelu2MulNorm || src->mode == kRmsNormSsq) && !src->aux2))
         return fail(RT_EINVAL, "rt_plan_create_fused: the source mode needs aux/aux2");
     const int K = w[0] ? w[0]->K : 0;
-    if ((src->mode == kRmsNormSsq || src->mode == kRmsNormStats) && (K % 64 || K > 8192))
-        return fail(RT_EINVAL, "rt_plan_create_fused: RMSNORM_SSQ / RMSNORM_STATS need K % 64 == 0 and K <= 8192");
-    auto a16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
-    if (src->mode == kRmsNormStats && !(a16(src->x) && a16(src->aux) && a16(src->aux2)))
-        return fail(RT_EINVAL, "rt_plan_create_fused: RMSNORM_STATS needs 16-byte aligned x, aux and statistics");
+    if (src->mode == kRmsNormSsq && (K % 64 || K > 8192))
+        return fail(RT_EINVAL, "rt_plan_create_fused: RMSNORM_SSQ needs K % 64 == 0 and K <= 8192");
     for (int g = 0; g < G; ++g) {
         if (!w[g] || !y[g]) return fail(RT_EINVAL, "rt_plan_create_fused: NULL entry in a pointer array");
         if (w[g]->K != K) return fail(RT_EINVAL, "rt_plan_create_fused: all weights must share K (one input)");
@@ -1174,11 +1192,6 @@ int rt_plan_create_fused(rt_ctx* ctx, int G, const rt_weights* const* w, const r
     }
     p->total_rb = wg;
     p->shape = gemv_shape_fused(wg, minC);
-    if (src->mode == kRmsNormStats && !stats_shape_ok(Kp, p->shape.nw)) {
-        rt_plan_free(p);
-        return fail(RT_EINVAL, "rt_plan_create_fused: too few row blocks for the RMSNORM_STATS prologue "
-                               "(at most 8 chunks of 64 inputs per wave)");
-    }
     std::vector<int> rb2p(wg);
     for (int g = 0; g < G; ++g)
         for (int r = 0; r < w[g]->Np / kRowBlock; ++r) rb2p[p->probs[g].wg_begin + r] = g;
@@ -1200,9 +1213,9 @@ int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, fl
     if (!ctx || !w_gu || !src || !src->x || !a || !ssq || !out)
         return fail(RT_EINVAL, std::string(who) + ": NULL argument");
     *out = nullptr;
-    if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRmsNormSsq && src->mode != kRmsNormStats)
-        return fail(RT_EINVAL, std::string(who) + ": the source must be QUANT, RMSNORM, RMSNORM_SSQ or RMSNORM_STATS");
-    if ((src->mode != kQuant && !src->aux) || ((src->mode == kRmsNormSsq || src->mode == kRmsNormStats) && !src->aux2))
+    if (src->mode != kQuant && src->mode != kRmsNorm && src->mode != kRmsNormSsq)
+        return fail(RT_EINVAL, std::string(who) + ": the source must be QUANT, RMSNORM or RMSNORM_SSQ");
+    if ((src->mode != kQuant && !src->aux) || (src->mode == kRmsNormSsq && !src->aux2))
         return fail(RT_EINVAL, std::string(who) + ": the source mode needs aux/aux2");
     if (w_gu->N % kRowBlock) return fail(RT_EINVAL, std::string(who) + ": the interleaved matrix needs N % 64 == 0");
     if (w_gu->device != ctx->device) return fail(RT_EINVAL, std::string(who) + ": weights live on another device");
@@ -1210,11 +1223,8 @@ int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, fl
     const GemvShape shape = gemv_shape_fused(Nb, w_gu->C);
     // an E-element prologue (K / 16 <= threads at least), 16-byte aligned rows
     auto a16 = [](const void* q) { return ((uintptr_t)q & 15u) == 0; };
-    const bool fits =
-        src->mode == kRmsNormStats ? stats_shape_ok(Kp, shape.nw) : vec_elements(K, 64 * shape.nw) != 0;
-    if (K % 64 || !fits || !a16(src->x) || !a16(src->aux) || !a16(src->aux2))
-        return fail(RT_EINVAL, std::string(who) + ": needs K % 64 == 0, K / 16 <= the workgroup's threads (at most "
-                                                  "8 chunks of 64 inputs per wave with RMSNORM_STATS) and "
+    if (K % 64 || vec_elements(K, 64 * shape.nw) == 0 || !a16(src->x) || !a16(src->aux) || !a16(src->aux2))
+        return fail(RT_EINVAL, std::string(who) + ": needs K % 64 == 0, K / 16 <= the workgroup's threads and "
                                                   "16-byte aligned sources");
     DeviceGuard guard(ctx->device);
     rt_plan* p = new rt_plan();
@@ -1265,7 +1275,7 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
     if (hd != 128) return fail(RT_EINVAL, std::string(who) + ": head_dim must be 128");
     if (workspace_bytes < rt_attention_decode_workspace(H, hd, Lmax))
         return fail(RT_EINVAL, std::string(who) + ": workspace too small");
-    if (!plan->fused || plan->G != 3 || plan->pair_a || plan->stat_out)
+    if (!plan->fused || plan->G != 3 || plan->pair_a)
         return fail(RT_EINVAL, std::string(who) + ": needs a fused decode plan of the q, k and v projections "
                                                   "(rt_plan_create_fused, G = 3, RMSNorm or absmax source)");
     const int Gq = H / Hkv;
@@ -1275,14 +1285,16 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
         return fail(RT_EINVAL, std::string(who) + ": the plan's workgroups must hold one 256-thread attention tile "
                                                   "per query head of a KV group (H / Hkv = 4 for this plan)");
     const QuantProb& P = plan->pro;
-    if (P.mode == kRmsNormStats || P.mode == kAttnNorm || P.K % 64 ||
+    if (P.mode == kAttnNorm || P.K % 64 ||
         vec_elements(P.K, 64 * plan->shape.nw) == 0 || ((uintptr_t)P.x & 15u) || ((uintptr_t)P.aux & 15u))
         return fail(RT_EINVAL, std::string(who) + ": the plan's source must be a 16-byte aligned row with K % 64 == 0");
     DeviceGuard g(plan->device);
     const size_t words = (size_t)(H + 2 * Hkv) * hd;
     const size_t bytes = words * sizeof(unsigned long long) + 256;
+    // a launch of this plan may still be in flight on the caller's stream: wait for it
+    // before the hand-off state is freed or reset
+    if (plan->att_mem) RT_HIP(hipDeviceSynchronize());
     if (plan->att_mem && plan->att_bytes != bytes) {
-        RT_HIP(hipDeviceSynchronize());
         RT_HIP(hipFree(plan->att_mem));
         plan->att_mem = nullptr;
     }
@@ -1323,24 +1335,6 @@ int rt_plan_attention_timeouts(rt_plan* plan, int* count) {
     RT_HIP(hipMemcpy(&err, plan->att.err, sizeof(int), hipMemcpyDeviceToHost));
     if (err) RT_HIP(attention_state_reset(plan));  // a wait gave up: start again from a clean state
     *count = err;
-    return RT_OK;
-}
-
-int rt_plan_set_row_stats(rt_plan* plan, const float* next_norm_w, void* stats) {
-    const char* who = "rt_plan_set_row_stats";
-    if (!plan) return fail(RT_EINVAL, std::string(who) + ": plan is NULL");
-    if (!next_norm_w != !stats) return fail(RT_EINVAL, std::string(who) + ": give both the weight and the records, "
-                                                                          "or neither");
-    if (stats) {
-        if (!plan->fused || plan->G != 1)
-            return fail(RT_EINVAL, std::string(who) + ": only one-problem fused decode plans "
-                                                      "(rt_plan_create_fused with G = 1, rt_plan_create_gate_up)");
-        const int rows = plan->pair_a ? plan->probs[0].N / 2 : plan->probs[0].N;
-        if (rows % kStatRows) return fail(RT_EINVAL, std::string(who) + ": the plan's outputs must be a multiple of 32");
-        if (((uintptr_t)stats & 15u) != 0) return fail(RT_EINVAL, std::string(who) + ": records must be 16-byte aligned");
-    }
-    plan->stat_out = static_cast<RowStat*>(stats);
-    plan->stat_w = next_norm_w;
     return RT_OK;
 }
 

@@ -785,15 +785,23 @@ __global__ void __launch_bounds__(2 * NW * 64, 4) gemm_splitk_kernel(GemmGroupAr
     }
 }
 
+// The kernels' dynamic LDS sizes above 64 KiB are allowed once per device, at context
+// creation (gemm_prepare_device), so that no launch, e.g. the first one under a stream
+// capture, makes a function-attribute call.
+template <typename Kern>
+static hipError_t allow_lds(Kern* k, int bytes) {
+    return bytes > 65536 ? hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, bytes)
+                         : hipSuccess;
+}
+
+template <int NW, int S>
+constexpr int splitk_lds() { return NW * S * (5 * 1024); }
+
 template <int NW, int S>
 static hipError_t launch_splitk(const GemmGroupArgs& ga, int blocks, hipStream_t s) {
-    constexpr int LDS = NW * S * (5 * 1024);
+    constexpr int LDS = splitk_lds<NW, S>();
     static_assert(S * 5 * 1024 >= 64 * 64 * 4 + 4, "a wave's ring must hold its partial tile (and wave 0's the arrival flag)");
-    if (LDS > 65536) {
-        static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_splitk_kernel<NW, S>),
-                                                           hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
-        if (attr != hipSuccess) return attr;
-    }
     hipLaunchKernelGGL((gemm_splitk_kernel<NW, S>), dim3((unsigned)blocks), dim3(2 * NW * 64), LDS, s, ga);
     return hipGetLastError();
 }
@@ -811,12 +819,6 @@ hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, int total_rb,
 template <int BM, int BN, int WAVES_M, int STAGES>
 static hipError_t launch_tile(const GemmGroupArgs& ga, int tiles, hipStream_t s) {
     using T = GemmTile<BM, BN, WAVES_M, STAGES>;
-    if (T::LDS_BYTES > 65536) {
-        static const hipError_t attr =
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN, WAVES_M, STAGES>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, T::LDS_BYTES);
-        if (attr != hipSuccess) return attr;
-    }
     if (tiles <= 0) return hipSuccess;
     hipLaunchKernelGGL((gemm_kernel<BM, BN, WAVES_M, STAGES>), dim3((unsigned)tiles), dim3(256), T::LDS_BYTES, s, ga);
     return hipGetLastError();
@@ -825,12 +827,25 @@ static hipError_t launch_tile(const GemmGroupArgs& ga, int tiles, hipStream_t s)
 template <int S>
 static hipError_t launch_region(const GemmGroupArgs& ga, int regions, hipStream_t s) {
     constexpr int LDS = 2 * S * kRegStage;
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_region_kernel<S>),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS);
-    if (attr != hipSuccess) return attr;
     if (regions <= 0) return hipSuccess;
     hipLaunchKernelGGL((gemm_region_kernel<S>), dim3((unsigned)regions), dim3(kRegThreads), LDS, s, ga);
     return hipGetLastError();
+}
+
+template <int BM, int BN, int WAVES_M, int STAGES>
+static hipError_t allow_tile_lds() {
+    return allow_lds(&gemm_kernel<BM, BN, WAVES_M, STAGES>, GemmTile<BM, BN, WAVES_M, STAGES>::LDS_BYTES);
+}
+
+hipError_t gemm_prepare_device() {
+    hipError_t e = allow_lds(&gemm_splitk_kernel<kSplitkWaves, 4>, splitk_lds<kSplitkWaves, 4>());
+    if (e == hipSuccess) e = allow_lds(&gemm_region_kernel<kRegS>, 2 * kRegS * kRegStage);
+    if (e == hipSuccess) e = allow_tile_lds<128, 128, 2, 4>();
+    if (e == hipSuccess) e = allow_tile_lds<256, 128, 2, 4>();
+    if (e == hipSuccess) e = allow_tile_lds<256, 256, 2, 4>();
+    if (e == hipSuccess) e = allow_tile_lds<192, 128, 2, 4>();
+    if (e == hipSuccess) e = allow_tile_lds<64, 128, 1, 8>();
+    return e;
 }
 
 static hipError_t launch_tile_cfg(int cfg, const GemmGroupArgs& ga, int tiles, hipStream_t s) {

@@ -320,11 +320,7 @@ constexpr int kAttnMaxThreads = 640;
 // PRO: 0 no prologue; 1 prologue quantising a row source (plain, RMSNorm, relu²·up,
 // relu²·up + sub-norm), 16 elements per thread; 3 / 4 the same with 4 / 8 consecutive
 // elements per thread (K % 64 == 0, K / 4 or K / 8 <= threads, 16-byte aligned sources);
-// 2 prologue combining decode-attention partials (kAttnNorm); 5 RMSNorm from the row's
-// statistics (kRmsNormStats): every wave quantises only its own chunks, with no
-// workgroup barrier before the dot products.
-// With a.stat_out (M = 1, one problem) the epilogue also writes the RowStat records of
-// the outputs for the next plan's kRmsNormStats prologue.
+// 2 prologue combining decode-attention partials (kAttnNorm).
 // PAIR (PRO 3, gate/up of the decode FFN): the matrix interleaves gate and up in 32-row
 // groups (row 64 j + r: gate row 32 j + r for r < 32, up row 32 j + r - 32 otherwise), so a
 // workgroup's row block holds both inputs of 32 outputs: it writes the FFN activation
@@ -376,18 +372,11 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     // first weight batches, which stream in during the prologue's arithmetic.
     constexpr bool VEC = PRO == 3 || PRO == 4 || PRO == 6;  // the E-element prologues
     constexpr int E = PRO == 4 ? 8 : PRO == 6 ? 16 : 4;      // elements per thread of PRO 3 / 4 / 6
-    using Regs = typename std::conditional<
-        PRO == 5, StatRegs,
-        typename std::conditional<PRO == 2, AttnRegs,
-                                  typename std::conditional<VEC, RowRegsE<E>, RowRegs>::type>::type>::type;
+    using Regs = typename std::conditional<PRO == 2, AttnRegs,
+                                           typename std::conditional<VEC, RowRegsE<E>, RowRegs>::type>::type;
     Regs rr;
     bool early = false;
-    if constexpr (PRO == 5) {
-        // the wave's chunks (every problem of a fused plan has the prologue row's K), so the
-        // records and the wave's elements are requested before anything else
-        const int C5 = (pro.K + 63) >> 6;  // from the preloaded K (Kp would be another load)
-        stat_load(pro, div_nw(wave * C5, nw_m), div_nw((wave + 1) * C5, nw_m), rr);
-    } else if constexpr (PRO == 1) {
+    if constexpr (PRO == 1) {
         early = row_fits1(pro, blockDim.x);
         if (early) row_load1(pro, 0, rr);
     } else if constexpr (VEC) {
@@ -397,8 +386,7 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
         early = attn_fits1(pro, blockDim.x);
         if (early) attn_load1(pro, rr);
     }
-    static_assert(!PAIR || ((VEC || PRO == 5) && MT == 1),
-                  "the pair epilogue follows an E-element or the statistics prologue");
+    static_assert(!PAIR || (VEC && MT == 1), "the pair epilogue follows an E-element prologue");
     const WStream ws = w1 ? WStream{w1, C1, 0, 0} : find_stream(a, ninl, blockIdx.x);
     const int rb = blockIdx.x - ws.wg_begin;
     const int C = ws.C, ldx = C * 16;
@@ -412,12 +400,6 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     int accP[MT], accQ[MT], sx[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) accP[m] = accQ[m] = 0;
-    // the statistics prologue's weight batches go out before anything that waits for a
-    // load (the scheduler would otherwise hoist the record reductions above them)
-    if constexpr (PRO == 5) {
-        gemv_preload<U>(rsrc, lane * 16, cb, A, B, cb + U < ce);
-        __builtin_amdgcn_sched_barrier(0);
-    }
     // The rest of the descriptor (epilogue): for inline problems the one at the index the
     // stream lookup chose; otherwise the table lookup.
     const int pj = __builtin_amdgcn_readfirstlane(ws.j);
@@ -437,7 +419,7 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     // With a prologue only the first batch is in flight during it (register budget); the
     // attention prologue holds its partials in registers first and issues it after their
     // combine.
-    if (PRO != 5 && (PRO != 2 || !early)) gemv_preload<U>(rsrc, lane * 16, cb, A, B, PRO == 0 && cb + U < ce);
+    if (PRO != 2 || !early) gemv_preload<U>(rsrc, lane * 16, cb, A, B, PRO == 0 && cb + U < ce);
     // one token with a prologue: the residual and scale of wave 0's rows (the epilogue's),
     // requested now so that the epilogue does not wait for them
     float res_v = 0.0f, sw_v = P.s_w;
@@ -459,14 +441,7 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
         asm volatile("" ::"s"(tagged), "s"(tag));
     }
     float sx_pro = -1.0f;
-    if constexpr (PRO == 5) {
-        // the wave's own activations: no barrier between the prologue and the dot products
-        v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
-        int qsum = 0;
-        sx_pro = stat_finish(pro, cb, ce, rr, lq, qsum);
-        sx[0] = qsum;
-        gemv_body<MT, U, lint, true>(rsrc, lane * 16, (lint*)lq, ldx, cb, ce, accP, accQ, A, B);
-    } else if constexpr (PRO != 0) {
+    if constexpr (PRO != 0) {
         v4u* lq = reinterpret_cast<v4u*>(red + nw * MT * kRowBlock);
         RowSmem* sm = reinterpret_cast<RowSmem*>(lq + (pro.Kp >> 4));
         sm->fac = (lfloat*)(sm + 1);  // kAttnNorm factors follow
@@ -522,22 +497,18 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
             }
             const double ss = wave_reduce63((double)av * (double)av, 0.0, [](double x, double y) { return x + y; });
             if (threadIdx.x == kRowBlock - 1) a.pair_ssq[rb] = ss;
-            if (a.stat_out) write_row_stats(av, valid ? a.stat_w[i] : 0.0f, valid, a.stat_out, rb, 1);
         }
         return;
     }
-    if (MT == 1 && PRO != 0 && !a.out_i32) {  // one token, fp32 outputs (and their statistics)
+    if (MT == 1 && PRO != 0 && !a.out_i32) {  // one token, fp32 outputs
         if (threadIdx.x < kRowBlock) {
-            const int r = threadIdx.x, n = rb * kRowBlock + r;
+            const int r = threadIdx.x;
             int s = 0;
             for (int w = 0; w < nw; ++w) s += red[w * kRowBlock + r];
             const float o = emit1(P, rb, r, s, sx_pro, res_v, sw_v);
             if constexpr (SIG) {
                 // rows past N are not read (every problem of a joint launch has N % 64 == 0)
                 __hip_atomic_store(tagged + r, tag | __float_as_uint(o), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            } else if (a.stat_out) {
-                const bool valid = n < P.N;
-                write_row_stats(o, valid ? a.stat_w[n] : 0.0f, valid, a.stat_out, 2 * rb, 2);
             }
         }
         return;
@@ -651,11 +622,6 @@ int vec_elements(int K, int threads) {
     return K / 16 <= threads ? 16 : 0;
 }
 
-bool stats_shape_ok(int Kp, int nw) {
-    const int C = Kp / kChunk;
-    return nw >= 1 && Kp <= 8192 && (C + nw - 1) / nw <= 4 * kStatSteps;
-}
-
 // One KSPLIT launch of nw waves per workgroup; the leading scalar arguments are the
 // prologue source's fields (zeros without a prologue), the shape word (nw <= 16, the inline
 // problem count and the chunks per row of a one-problem launch, C <= 2^16), nw's reciprocal
@@ -688,17 +654,15 @@ hipError_t launch_gemv(const GemvArgs& args, int mt, GemvShape shape, hipStream_
         const dim3 grid((unsigned)(a.total_rb / shape.nw), 1);
         const size_t lds = (size_t)a.pro.Kp + sizeof(RowSmem);  // pro.Kp: the largest Kp of the problems
         hipLaunchKernelGGL((gemv_rows_kernel<1, 1>), grid, block, lds, s, a);
-    } else if (a.has_pro && a.pair_a) {  // gate/up pair: an E-element or the statistics prologue
+    } else if (a.has_pro && a.pair_a) {  // gate/up pair: an E-element prologue
         const QuantProb& P = a.pro;
-        const bool stats = P.mode == kRmsNormStats;
-        const int E = stats ? 0 : vec_elements(P.K, 64 * shape.nw);
+        const int E = vec_elements(P.K, 64 * shape.nw);
         if (mt != 1 || a.M != 1 || !shape.ksplit || P.K % 64 || !aligned16(P.x) || !aligned16(P.aux) ||
-            !aligned16(P.aux2) || (stats ? !stats_shape_ok(P.Kp, shape.nw) : E == 0))
+            !aligned16(P.aux2) || E == 0)
             return hipErrorInvalidValue;
         const dim3 grid((unsigned)a.total_rb, 1);
         const size_t lds = (size_t)shape.nw * kRowBlock * sizeof(int) + (size_t)P.Kp + sizeof(RowSmem);
-        if (stats) launch_ksplit<1, 5, true>(grid, shape.nw, lds, s, a);
-        else if (E == 4) launch_ksplit<1, 3, true>(grid, shape.nw, lds, s, a);
+        if (E == 4) launch_ksplit<1, 3, true>(grid, shape.nw, lds, s, a);
         else if (E == 8) launch_ksplit<1, 4, true>(grid, shape.nw, lds, s, a);
         else launch_ksplit<1, 6, true>(grid, shape.nw, lds, s, a);
     } else if (a.has_pro) {  // single token, prologue-quantised input: KSPLIT shape only
@@ -708,10 +672,7 @@ hipError_t launch_gemv(const GemvArgs& args, int mt, GemvShape shape, hipStream_
         const int nw = a.pro.mode == kAttnNorm ? std::min(shape.nw, kAttnMaxThreads / 64) : shape.nw;
         size_t lds = (size_t)nw * kRowBlock * sizeof(int) + (size_t)a.pro.Kp + sizeof(RowSmem);
         const bool vec = P.K % 64 == 0 && aligned16(P.x) && aligned16(P.aux) && aligned16(P.aux2);
-        if (a.pro.mode == kRmsNormStats) {
-            if (!vec || !stats_shape_ok(P.Kp, nw)) return hipErrorInvalidValue;
-            launch_ksplit<1, 5>(grid, nw, lds, s, a);
-        } else if (a.pro.mode == kAttnNorm) {
+        if (a.pro.mode == kAttnNorm) {
             lds += (size_t)(a.pro.K / a.pro.attn_hd) * (a.pro.attn_S + 1) * sizeof(float);
             launch_ksplit<1, 2>(grid, nw, lds, s, a);
         } else if (const int E = vec ? vec_elements(P.K, (int)block.x) : 0) {
@@ -765,8 +726,8 @@ hipError_t launch_gemv_attn(const GemvArgs& args, const AttnTail& at, int Hkv, i
     // whole row blocks
     const bool vec = P.K % 64 == 0 && aligned16(P.x) && aligned16(P.aux) && aligned16(P.aux2);
     const int E = vec ? vec_elements(P.K, 64 * nw) : 0;
-    if (a.has_pro != 1 || a.M != 1 || a.out_i32 || a.pair_a || a.stat_out || a.ninl != 3 || !shape.ksplit ||
-        E == 0 || P.mode == kRmsNormStats || P.mode == kAttnNorm || hd != 128 || 64 * nw != 256 * at.Gq ||
+    if (a.has_pro != 1 || a.M != 1 || a.out_i32 || a.pair_a || a.ninl != 3 || !shape.ksplit ||
+        E == 0 || P.mode == kAttnNorm || hd != 128 || 64 * nw != 256 * at.Gq ||
         at.qrows != at.Gq * Hkv * hd || at.nkv != Hkv * hd || a.inl[0].N != at.qrows || a.inl[1].N != at.nkv ||
         a.inl[2].N != at.nkv || a.inl[1].wg_begin * kRowBlock != at.qrows ||
         a.inl[2].wg_begin * kRowBlock != at.qrows + at.nkv || at.S <= 0 || at.S != attn_splits(at.Lmax))

@@ -79,30 +79,8 @@ __host__ __device__ inline unsigned rotor_code(unsigned g) {
 //             (cast; the `ssq` output of a gate/up pair plan): the 4- and 8-element
 //             prologues add those up instead of reducing x over the workgroup; every
 //             other path ignores them and reduces x itself
-//   kRmsNormStats  as kRmsNorm, with the row's statistics given in aux2 (cast; RowStat[K/32],
-//             written by the producer of x): the decode GEMV prologue then needs no
-//             workgroup reduction (kernels other than that prologue reduce x themselves)
 enum QuantMode { kQuant = 0, kPermute = 1, kRmsNorm = 2, kRelu2Mul = 3, kRelu2MulNorm = 4, kAttnNorm = 5,
-                 kRmsNormSsq = 6, kRmsNormStats = 7 };
-
-// Statistics of a row y that the next RMSNorm + absmax quantiser needs, per group of 32
-// consecutive elements, with w the next RMSNorm's weight:
-//   ssq    sum of (double) y_k^2;
-//   tmax   max of t_k = |y_k| |w_k|, in f64 (exact: a product of two floats);
-//   ncand  the number of k with t_k >= tmax (1 - kStatDelta), cx / cw = y_k, w_k of the
-//          first of them.
-// The quantiser's absmax is max_k fl(fl(|y_k| / n) |w_k|) (n the RMSNorm divisor); each of
-// the two roundings moves a value by at most a factor 1 +- 2^-24, so only the k with
-// t_k >= max_j t_j (1 - 2^-22) can hold that maximum: with kStatDelta = 2^-20 they are all
-// among the recorded candidates of the groups whose tmax reaches the threshold, and a
-// group with one candidate needs no other element.
-struct RowStat {
-    double ssq, tmax;
-    float cx, cw;
-    int ncand, pad;
-};
-constexpr int kStatRows = 32;
-constexpr double kStatDelta = 0x1p-20;
+                 kRmsNormSsq = 6 };
 
 struct QuantProb {
     const float* x;      // fp32 [M][K] (gate in kRelu2Mul)
@@ -170,11 +148,6 @@ struct GemvArgs {
     float* pair_g;
     float* pair_u;
     float pair_sg, pair_su;  // the gate and up scales
-    // M = 1 KSPLIT launches over one problem: when stat_out is set, the epilogue also writes
-    // the RowStat of every 32 outputs (y after the residual, or the pair's a) against the
-    // next RMSNorm's weight stat_w [N] (stat_out [N / 32])
-    RowStat* stat_out;
-    const float* stat_w;
 };
 
 // Attention partials in the qkv GEMV's launch (gemv_ksplit_kernel with an AttnTail): the
@@ -361,6 +334,10 @@ hipError_t launch_gemm_tiles(const GemmArgs* dev, const int* tile2p, int total_t
 hipError_t launch_gemv_attn(const GemvArgs& args, const AttnTail& at, int Hkv, int hd, GemvShape shape,
                             hipStream_t s);
 hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, int total_rb, hipStream_t s);
+// Once per device (current) before any launch: the function attributes the GEMM kernels
+// and the prefill attention need (dynamic LDS above 64 KiB).
+hipError_t gemm_prepare_device();
+hipError_t model_prepare_device();
 
 // model kernels (rt_model.hip)
 hipError_t launch_embed(const uint16_t* E, const int* ids, int M, int V, int D, float* h, hipStream_t s);
@@ -387,9 +364,6 @@ inline int gemv_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 GemvShape gemv_shape(int total_rb, int m_blocks, int min_C);
 // Launch shape of a plan whose GEMV quantises its input in the prologue (M = 1).
 GemvShape gemv_shape_fused(int total_rb, int min_C);
-// The kRmsNormStats prologue fits a row of Kp bytes over nw waves (K / 32 <= 256 records,
-// at most 8 chunks per wave).
-bool stats_shape_ok(int Kp, int nw);
 // Elements per thread (4, 8 or 16) of the vectorised decode prologue for a row of K
 // (K % 64 == 0) on `threads` threads, 0 when none fits.
 constexpr int kVecLiveWaves = 16;  // measured: 4, 8 and 16 give the same decode time

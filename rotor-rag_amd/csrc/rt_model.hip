@@ -465,15 +465,20 @@ hipError_t launch_rope_append(float* q, float* k, const float* v, float* Kc, flo
     return hipGetLastError();
 }
 
+// the matrix-core prefill attention's LDS (above 64 KiB: allowed once per device, at
+// context creation, so that no launch makes a function-attribute call)
+constexpr size_t kAttnPrefillLds = (size_t)(4 * 128 * 32 * 2 + 4 * 32 * 2) * sizeof(float);
+
+hipError_t model_prepare_device() {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_prefill_mfma_kernel<128>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAttnPrefillLds);
+}
+
 hipError_t launch_attention(const float* q, const float* Kc, const float* Vc, float* out, int M, int H, int Hkv,
                             int hd, int Lmax, const int* pos, float scale, hipStream_t s) {
     const int G = H / Hkv;
     if (hd == 128 && G <= 32 && 32 % G == 0 && Lmax % 4 == 0) {  // matrix-core kernel
-        constexpr size_t lds = (size_t)(4 * 128 * 32 * 2 + 4 * 32 * 2) * sizeof(float);
-        static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void*>(&attn_prefill_mfma_kernel<128>), hipFuncAttributeMaxDynamicSharedMemorySize,
-            (int)lds);
-        if (attr != hipSuccess) return attr;
+        constexpr size_t lds = kAttnPrefillLds;
         const int BQ = 32 / G;
         hipLaunchKernelGGL((attn_prefill_mfma_kernel<128>), dim3((unsigned)Hkv, (unsigned)((M + BQ - 1) / BQ)),
                            dim3(256), lds, s, q, Kc, Vc, out, M, H, Hkv, Lmax, pos, scale);

@@ -551,147 +551,6 @@ __device__ __forceinline__ float attn_norm1(const QuantProb& P, float (&v)[4], c
     return sc;
 }
 
-// ---- row statistics (RowStat) between decode plans ----------------------------------
-// Producer side: one wave holds outputs y of 64 consecutive rows (lane r: row r; lanes
-// whose row is past the output hold valid = false) with the next RMSNorm's weights w and
-// writes the RowStat of each half (records rec0 and rec0 + 1; `halves` = 1 writes only
-// the first, for 32 rows in lanes 0..31).
-__device__ __forceinline__ void write_row_stats(float y, float w, bool valid, RowStat* dst, int rec0, int halves) {
-    const int lane = threadIdx.x & 63;
-    auto dadd = [](double a, double b) { return a + b; };
-    auto dmax = [](double a, double b) { return fmax(a, b); };
-    const double t = valid ? (double)fabsf(y) * (double)fabsf(w) : 0.0;  // exact
-    const double sq = valid ? (double)y * (double)y : 0.0;
-    const double ss = half_reduce31(sq, 0.0, dadd);
-    const double tm = half_reduce31(t, 0.0, dmax);
-    const double tm0 = read_lane(tm, 31), tm1 = read_lane(tm, 63);
-    const double thr = (lane < 32 ? tm0 : tm1) * (1.0 - kStatDelta);
-    const unsigned long long c = __ballot(valid && t >= thr);
-    const unsigned c0 = (unsigned)c, c1 = (unsigned)(c >> 32);
-    const int f0 = c0 ? __builtin_ctz(c0) : 0, f1 = c1 ? 32 + __builtin_ctz(c1) : 32;
-    const float x0 = read_lane(y, f0), w0 = read_lane(w, f0), x1 = read_lane(y, f1), w1 = read_lane(w, f1);
-    if (lane == 31 || (lane == 63 && halves > 1)) {
-        const bool hi = lane == 63;
-        RowStat s;
-        s.ssq = ss;
-        s.tmax = hi ? tm1 : tm0;
-        s.cx = hi ? x1 : x0;
-        s.cw = hi ? w1 : w0;
-        s.ncand = __builtin_popcount(hi ? c1 : c0);
-        s.pad = 0;
-        dst[rec0 + (hi ? 1 : 0)] = s;
-    }
-}
-
-// Consumer side: the kRmsNormStats prologue of the decode GEMV, per wave and without any
-// workgroup reduction.  The wave owns chunks [cb, ce) of the row (64 elements each, at most
-// 4 kStatSteps chunks): stat_load issues the loads of the row's K / 32 <= 256 records (four
-// per lane) and of the wave's own elements of x and of the norm weight; stat_finish derives
-// the RMSNorm divisor and the absmax the whole-row prologue would compute (see RowStat:
-// every wave and workgroup adds the records in the same order), quantises the wave's
-// elements into the LDS row (bytes of chunks [cb, ce) only) and returns the scale, with
-// the sum of the wave's int8 values in qsum.
-constexpr int kStatSteps = 2;  // 256 elements per step
-struct StatRegs {
-    float x[kStatSteps][4], w[kStatSteps][4];
-    double ssq[4], tm[4];
-    float cx[4], cw[4];
-    int nc[4];
-};
-
-// Straight-line loads (no branch around them, so none waits for another): lanes past
-// the records or past the wave's chunks re-read a valid element and zero what they got.
-__device__ __forceinline__ void stat_load(const QuantProb& P, int cb, int ce, StatRegs& r) {
-    const int lane = threadIdx.x & 63, n = P.K / kStatRows;
-    const RowStat* st = reinterpret_cast<const RowStat*>(P.aux2);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int g = lane + 64 * i;
-        const bool ok = g < n;
-        const RowStat s = st[ok ? g : n - 1];
-        r.ssq[i] = ok ? s.ssq : 0.0;
-        r.tm[i] = ok ? s.tmax : 0.0;
-        r.cx[i] = ok ? s.cx : 0.0f;
-        r.cw[i] = ok ? s.cw : 0.0f;
-        r.nc[i] = ok ? s.ncand : 0;
-    }
-    const int klast = max(64 * ce - 4, 0);
-#pragma unroll
-    for (int s = 0; s < kStatSteps; ++s) {
-        const int k = 64 * cb + 256 * s + 4 * lane;
-        const bool ok = k < 64 * ce;
-        float x[4], w[4];
-        loadE<4>(P.x + (ok ? k : klast), x);
-        loadE<4>(P.aux + (ok ? k : klast), w);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            r.x[s][j] = ok ? x[j] : 0.0f;
-            r.w[s][j] = ok ? w[j] : 0.0f;
-        }
-    }
-}
-
-__device__ __forceinline__ float stat_finish(const QuantProb& P, int cb, int ce, const StatRegs& r, v4u* lq, int& qsum) {
-    const int lane = threadIdx.x & 63, K = P.K;
-    auto dadd = [](double a, double b) { return a + b; };
-    auto dmax = [](double a, double b) { return fmax(a, b); };
-    auto fmx = [](float a, float b) { return fmaxf(a, b); };
-    const double ss = lane63(wave_reduce63((r.ssq[0] + r.ssq[1]) + (r.ssq[2] + r.ssq[3]), 0.0, dadd));
-    const float norm = sqrtf((float)(ss / (double)K) + P.eps);
-    const double T = lane63(wave_reduce63(fmax(fmax(r.tm[0], r.tm[1]), fmax(r.tm[2], r.tm[3])), 0.0, dmax));
-    float amax = 0.0f;
-    if (T > 0.0) {  // else every product |y| |w| is zero, and so is every quantised value
-        // candidate groups; rows so small that the values could be subnormal take every
-        // group with a non-zero product through the slow path
-        const bool tiny = T < 0x1p-100;
-        const double thr = T * (1.0 - kStatDelta);
-        bool slow[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const bool cand = r.tm[i] > 0.0 && (tiny || r.tm[i] >= thr);
-            slow[i] = cand && (tiny || r.nc[i] != 1);
-            if (cand && !slow[i]) amax = fmaxf(amax, (fabsf(r.cx[i]) / norm) * fabsf(r.cw[i]));
-        }
-        // groups with several candidates: every element of the group (lanes 0..31)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            unsigned long long b = __ballot(slow[i]);
-            while (b) {
-                const int g = __builtin_ctzll(b) + 64 * i;
-                b &= b - 1;
-                if (lane < kStatRows) {
-                    const int k = g * kStatRows + lane;
-                    amax = fmaxf(amax, (fabsf(P.x[k]) / norm) * fabsf(P.aux[k]));
-                }
-            }
-        }
-        amax = lane63(wave_reduce63(amax, 0.0f, fmx));
-    }
-    const float sc = amax > 0.0f ? amax / 127.0f : 1.0f;
-    unsigned char* lb = reinterpret_cast<unsigned char*>(lq);
-    int qs = 0;
-#pragma unroll
-    for (int s = 0; s < kStatSteps; ++s) {
-        const int k0 = 64 * cb + 256 * s + 4 * lane;
-        if (k0 < 64 * ce) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int k = k0 + j, e = k & 15;
-                float q = rintf(((r.x[s][j] / norm) * r.w[s][j]) / sc);
-                q = fminf(fmaxf(q, -128.0f), 127.0f);
-                lb[(k & ~15) + 4 * (e & 3) + (e >> 2)] = (unsigned char)(int)q;
-                qs += (int)q;
-            }
-        }
-    }
-    qsum = wave_sum(qs);
-    // the wave reads back the bytes its lanes wrote
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    return sc;
-}
-
 // Quantise token row m of P (all modes but kPermute) into qrow (Kp/16 permuted groups)
 // and return its scale.  Rows of up to REG groups of 16 per thread stay in registers,
 // longer rows are read again on every pass.  Every thread of the workgroup must call it

@@ -15,7 +15,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "librotor_hip.so"
-ABI_VERSION = 105  # rt_version() of the library this table binds
+ABI_VERSION = 106  # rt_version() of the library this table binds
 
 class RtSrc(ctypes.Structure):
     """rt_src of include/rotor_hip.h"""
@@ -24,8 +24,6 @@ class RtSrc(ctypes.Structure):
 
 
 SRC_QUANT, SRC_RMSNORM, SRC_RELU2MUL, SRC_RELU2MUL_NORM, SRC_ATTN_NORM, SRC_RMSNORM_SSQ = 0, 2, 3, 4, 5, 6
-SRC_RMSNORM_STATS = 7
-ROWSTAT_BYTES = 32  # statistics of 32 consecutive row elements (RT_ROWSTAT_BYTES)
 LAUNCH_GEMV, LAUNCH_GEMV_FUSED, LAUNCH_SPLITK, LAUNCH_TILES = 0, 1, 2, 3
 
 # name -> (restype, argtypes); every entry point of include/rotor_hip.h
@@ -70,7 +68,6 @@ SIGNATURES = {
     "rt_plan_create_fused": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(RtSrc), ctypes.POINTER(_P),
                                   ctypes.POINTER(_P), ctypes.POINTER(_P)]),
     "rt_plan_create_gate_up": (_I, [_P, _P, _F, _F, ctypes.POINTER(RtSrc), _P, _P, _P, _P, ctypes.POINTER(_P)]),
-    "rt_plan_set_row_stats": (_I, [_P, _P, _P]),
     "rt_plan_attach_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t]),
     "rt_plan_attention_timeouts": (_I, [_P, _P]),
     "rt_embed": (_I, [_P, _P, _I, _I, _P, _I, _P]),
@@ -79,6 +76,7 @@ SIGNATURES = {
     "rt_attention_decode_workspace": (ctypes.c_size_t, [_I, _I, _I]),
     "rt_attention_decode": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t]),
     "rt_attention_decode_partials": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t]),
+    "rt_attention_decode_combine": (_I, [_P, _P, ctypes.c_size_t, _I, _I, _I, _P]),
     "rt_rope_attention_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t, _P]),
     "rt_lm_head_argmax": (_I, [_P, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I]),
 }

@@ -204,9 +204,15 @@ class _DeviceModel:
 
         self.m = model
         self.epoch = 0  # sequence counter of the device KV cache (see KVCache)
-        # when a dict: multi-token forwards append a device copy of every layer's attention
-        # output to trace["attn"] (for checking a forward layer by layer; off by default)
+        # when a dict (off by default; for checking a run layer by layer against a CPU
+        # restatement): a multi-token forward appends a device copy of every layer's attention
+        # output to trace["attn"] and stores {"h": last row's hidden state before the final
+        # norm [D], "logits": the fused LM head's logits of that row [V]} as trace["prefill"];
+        # every one-token step (forward, or generate's decode steps, graph-replayed or not)
+        # appends {"attn": [layers, H * hd] attention outputs (the split partials combined as
+        # the o_proj prologue combines them), "h": [D], "logits": [V]} to trace["steps"]
         self.trace = None
+        self._tbuf = None  # the trace's device buffers (allocated before any graph capture)
         hip = self.hip = model.gpu
         dev = self.device = hip.device
         D, F, H, Hkv, hd = model.d_model, model.d_ff, model.n_heads, model.n_kv_heads, model.head_dim
@@ -256,12 +262,6 @@ class _DeviceModel:
         # prologue only normalises and quantises; False runs the gate/up plan and lets the
         # down prologue form relu(g)^2 * u and reduce it
         self.ffn_pair = D % 64 == 0 and F % 64 == 0 and F <= 8192
-        # decode: True (with the pair and both sub-norms) hands the statistics of every
-        # RMSNorm input row (sums of squares, absmax candidates) from the plan that writes
-        # the row to the plan that normalises it, whose prologue then quantises with no
-        # workgroup-wide reduction; False (default: measured 1.247 against 1.196 ms per
-        # token on the 30-layer 2560 / 6912 model) lets each prologue reduce the row itself
-        self.row_stats = False
         # decode: True (default, where the plan's shape allows it: hd 128, 4 query heads per KV
         # head, the q/k/v GEMV at 16 waves per workgroup) runs RoPE + KV append + the attention
         # partials inside the q/k/v GEMV's launch (rt_plan_attach_attention), one launch per
@@ -282,15 +282,8 @@ class _DeviceModel:
         st["qkv"], st["gu"], st["o_plan"], st["d_plan"] = [], [], [], []
         st["attn_fused"] = []  # per layer: the q/k/v plan runs the attention partials
         hip, eps = self.hip, self.m.eps
-        stats = M == 1 and self.row_stats and all(
-            L["attn_sub_norm"] is not None and L["ffn_sub_norm"] is not None for L in self.layers)
-        if stats:  # statistics of h after o_proj, of a after gate/up, of h after down
-            st["s_h1"], st["s_a"], st["s_h2"] = hip.row_stats_buffer(D), hip.row_stats_buffer(F), hip.row_stats_buffer(D)
         for li, L in enumerate(self.layers):
             st["attn_fused"].append(False)
-            if M == 1 and stats:
-                self._decode_plans_stats(st, li, L)
-                continue
             if M == 1:  # decode: one launch per plan, the input row is quantised in the GEMV prologue
                 h, o, g, u = st["h"][0], st["o"][0], st["g"][0], st["u"][0]
                 st["qkv"].append(hip.plan_fused([L["q_proj"], L["k_proj"], L["v_proj"]], _hip.SRC_RMSNORM, h,
@@ -353,40 +346,29 @@ class _DeviceModel:
         if n:
             raise RuntimeError(f"{n} attention waits in the q/k/v launches gave up: the decode results are invalid")
 
-    def _decode_plans_stats(self, st, li, L):
-        """One decode layer's four plans with the row statistics handed along: o_proj writes
-        those of h for the FFN norm, the gate/up pair those of a for the sub-norm, down those
-        of h for the next layer's input norm (layer 0 normalises the embedding itself)."""
-        hip, eps = self.hip, self.m.eps
-        h, a = st["h"][0], st["a"]
-        if li == 0:
-            qkv = hip.plan_fused([L["q_proj"], L["k_proj"], L["v_proj"]], _hip.SRC_RMSNORM, h, L["input_norm"],
-                                 eps=eps, ys=[st["q"][0], st["k"][0], st["v"][0]])
+    def _trace_bufs(self):
+        if self._tbuf is None:
+            import torch
+
+            e = lambda *s: torch.empty(s, dtype=torch.float32, device=self.device)
+            self._tbuf = {"attn": e(len(self.layers), self.H * self.hd), "h": e(self.D)}
+        return self._tbuf
+
+    def _trace_record(self, key):
+        """Copies of the trace buffers and the logits after a forward (see self.trace)."""
+        tb = self._tbuf
+        rec = {"h": tb["h"].clone(), "logits": self.logits.clone()}
+        if key == "steps":
+            rec["attn"] = tb["attn"].clone()
+            self.trace.setdefault("steps", []).append(rec)
         else:
-            qkv = hip.plan_fused([L["q_proj"], L["k_proj"], L["v_proj"]], _hip.SRC_RMSNORM_STATS, h, L["input_norm"],
-                                 st["s_h2"], eps=eps, ys=[st["q"][0], st["k"][0], st["v"][0]])
-        o_plan = hip.plan_fused([L["o_proj"]], _hip.SRC_ATTN_NORM, self.attn_ws, L["attn_sub_norm"], eps=eps, ys=[h],
-                                residuals=[h], attn_head_dim=self.hd, attn_max_len=self.Lmax)
-        o_plan.set_row_stats(L["post_norm"], st["s_h1"])
-        if "gate_up" not in L:  # the interleaved copy the pair plan runs (decode only)
-            L["gate_up"] = hip.interleave_gate_up(L["gate_proj"], L["up_proj"])
-        w_gu, scales = L["gate_up"]
-        gu = hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM_STATS, h, L["post_norm"], st["s_h1"], eps=eps, a=a,
-                              ssq=st["ssq"])
-        gu.set_row_stats(L["ffn_sub_norm"], st["s_a"])
-        d_plan = hip.plan_fused([L["down_proj"]], _hip.SRC_RMSNORM_STATS, a, L["ffn_sub_norm"], st["s_a"], eps=eps,
-                                ys=[h], residuals=[h])
-        if li + 1 < len(self.layers):
-            d_plan.set_row_stats(self.layers[li + 1]["input_norm"], st["s_h2"])
-        st["qkv"].append(qkv)
-        st["o_plan"].append(o_plan)
-        st["gu"].append(gu)
-        st["d_plan"].append(d_plan)
+            self.trace[key] = rec
 
     def _enqueue(self, M, pos_base, out_cap):
         """Forward of the M tokens in ids[0:M] at position *pos; LM head + argmax of the last."""
         hip, lib, ctx = self.hip, _hip.load(), self.hip.ctx
         st = self._state(M)
+        tb = self._trace_bufs() if self.trace is not None else None
         h, q, k, v, o, g, u = st["h"], st["q"], st["k"], st["v"], st["o"], st["g"], st["u"]
         hip._bind_stream()
         chk = _hip.check
@@ -400,15 +382,23 @@ class _DeviceModel:
             else:
                 hip.act_rmsnorm_quantize(h, L["input_norm"], self.act_d, eps)
                 st["qkv"][li].gemv()
-            if M == 1 and st["attn_fused"][li]:
-                pass  # RoPE, KV append and the attention partials ran in the q/k/v launch
-            elif M == 1:  # RoPE + KV append + split attention in one launch; o_proj's prologue may combine
-                combine_here = L["attn_sub_norm"] is None or not self.attn_in_prologue
-                chk(lib.rt_rope_attention_decode(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
-                                                 L["vc"].data_ptr(), self.rope.data_ptr(), self.H, self.Hkv, self.hd,
-                                                 self.Lmax, self.pos.data_ptr(), self.attn_ws.data_ptr(),
-                                                 self.attn_ws_bytes, o.data_ptr() if combine_here else None),
-                    "rt_rope_attention_decode")
+            if M == 1:
+                combine_here = False
+                if not st["attn_fused"][li]:
+                    # RoPE + KV append + split attention in one launch (else they ran in the
+                    # q/k/v launch); o_proj's prologue combines the partials, or this launch does
+                    combine_here = L["attn_sub_norm"] is None or not self.attn_in_prologue
+                    chk(lib.rt_rope_attention_decode(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
+                                                     L["vc"].data_ptr(), self.rope.data_ptr(), self.H, self.Hkv,
+                                                     self.hd, self.Lmax, self.pos.data_ptr(), self.attn_ws.data_ptr(),
+                                                     self.attn_ws_bytes, o.data_ptr() if combine_here else None),
+                        "rt_rope_attention_decode")
+                if tb is not None and combine_here:
+                    tb["attn"][li].copy_(o[0])
+                elif tb is not None:  # the attention output the o_proj prologue forms from the partials
+                    chk(lib.rt_attention_decode_combine(ctx, self.attn_ws.data_ptr(), self.attn_ws_bytes, self.H,
+                                                        self.hd, self.Lmax, tb["attn"][li].data_ptr()),
+                        "rt_attention_decode_combine")
             else:
                 chk(lib.rt_rope_kv_append(ctx, q.data_ptr(), k.data_ptr(), v.data_ptr(), L["kc"].data_ptr(),
                                           L["vc"].data_ptr(), self.rope.data_ptr(), M, self.H, self.Hkv, self.hd,
@@ -434,6 +424,8 @@ class _DeviceModel:
             else:
                 hip.act_relu2_mul_quantize(g, u, self.act_f)
             hip.linear_act(L["down_proj"], self.act_f, out=h, residual=h)
+        if tb is not None:
+            tb["h"].copy_(h[M - 1])
         chk(lib.rt_lm_head_argmax(ctx, self.emb.data_ptr(), h[M - 1].data_ptr(), self.final_norm.data_ptr(), eps,
                                   self.m.vocab_size, self.D, self.logits.data_ptr(), self.best.data_ptr(),
                                   self.token.data_ptr(), self.pos.data_ptr(), M, self.ids.data_ptr(),
@@ -470,6 +462,8 @@ class _DeviceModel:
         st = self._enqueue(M, pos_base=1 << 30, out_cap=0)
         if M == 1:
             self.attention_timeouts()
+        if self.trace is not None:
+            self._trace_record("steps" if M == 1 else "prefill")
         h = st["h"]
         if M == 1:
             out = self.logits[None] if return_logits else self._final_norm(h)
@@ -504,6 +498,8 @@ class _DeviceModel:
         if P + n > self.Lmax:
             raise ValueError("prompt + new tokens exceed max_seq_len")
         self._state(P)
+        if self.trace is not None:
+            self._trace_bufs()  # before the capture (not in the graph's memory pool)
         g = None
         if n > 1 and graph:  # capture the decode step first (capture does not execute it)
             self._state(1)
@@ -515,14 +511,17 @@ class _DeviceModel:
         self.pos.fill_(0)
         self.best.zero_()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        rec = self._trace_record if self.trace is not None else (lambda key: None)
         ev[0].record()
         self._enqueue(P, pos_base=P - 1, out_cap=n)            # prefill; out_tokens[0]
+        rec("steps" if P == 1 else "prefill")
         ev[1].record()
         for _ in range(n - 1):
             if g is not None:
                 g.replay()
             else:
                 self._enqueue(1, pos_base=P - 1, out_cap=n)
+            rec("steps")
         ev[2].record()
         torch.cuda.synchronize()
         self.attention_timeouts()

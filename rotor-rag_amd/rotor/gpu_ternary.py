@@ -91,18 +91,6 @@ class LinearPlan:
         b._bind_stream()
         _hip.check(_hip.load().rt_plan_gemv(b.ctx, self.handle), "rt_plan_gemv")
 
-    def set_row_stats(self, next_norm_w, stats) -> None:
-        """Let this one-problem decode plan also write the statistics of its output row that
-        the next plan's RMSNorm needs (rt_plan_set_row_stats): stats = a device buffer of
-        out_features / 32 * ROWSTAT_BYTES bytes (HIPTernaryOps.row_stats_buffer), taken against
-        next_norm_w; a plan with source SRC_RMSNORM_STATS reads them.  (None, None) detaches."""
-        if (next_norm_w is None) != (stats is None):
-            raise ValueError("set_row_stats: give both the norm weight and the buffer, or neither")
-        ptr = lambda t: t.data_ptr() if t is not None else None
-        _hip.check(_hip.load().rt_plan_set_row_stats(self.handle, ptr(next_norm_w), ptr(stats)),
-                   "rt_plan_set_row_stats")
-        self._keep = (self._keep, next_norm_w, stats)
-
     def attach_attention(self, k_cache, v_cache, rope, H: int, Hkv: int, hd: int, Lmax: int, pos, workspace) -> None:
         """Run the decode RoPE + KV append + attention partials of the token inside run()'s
         launch of this q/k/v plan (rt_plan_attach_attention; the arguments of
@@ -448,22 +436,11 @@ class HIPTernaryOps:
                    "rt_plan_create_fused")
         return LinearPlan(self, h, (list(weights), [x, aux, aux2], list(ys), list(residuals or [])))
 
-    def row_stats_buffer(self, n: int):
-        """Device buffer for the row statistics of an n-element row (rt_plan_set_row_stats)."""
-        torch = _torch()
-        if n % 32:
-            raise ValueError("row statistics cover groups of 32 elements: n % 32 must be 0")
-        return torch.zeros(n // 32 * _hip.ROWSTAT_BYTES, dtype=torch.uint8, device=self.device)
-
     def _check_src(self, mode, K, x, aux, aux2, who):
-        stats = mode == _hip.SRC_RMSNORM_STATS
         for t in ((x if mode != _hip.SRC_ATTN_NORM else None), aux,
-                  (aux2 if mode not in (_hip.SRC_RMSNORM_SSQ, _hip.SRC_RMSNORM_STATS) else None)):
+                  (aux2 if mode != _hip.SRC_RMSNORM_SSQ else None)):
             if t is not None and (t.numel() < K or not t.is_contiguous() or t.device != self.device):
                 raise ValueError(f"{who}: source tensors must be contiguous device tensors of >= K elements")
-        if stats and (aux2 is None or aux2.numel() * aux2.element_size() < K // 32 * _hip.ROWSTAT_BYTES
-                      or not aux2.is_contiguous() or aux2.device != self.device):
-            raise ValueError(f"{who}: RMSNORM_STATS needs aux2 = the statistics buffer of the source row")
         if mode == _hip.SRC_RMSNORM_SSQ:
             t = aux2
             if (t is None or t.dtype != _torch().float64 or t.numel() < K // 32 or not t.is_contiguous()

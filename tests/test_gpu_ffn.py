@@ -257,131 +257,3 @@ def test_gate_up_pair_plan_rejects_shapes(hip):
     a, ssq = torch.empty(64, device="cuda"), torch.empty(2, dtype=torch.float64, device="cuda")
     with pytest.raises(RuntimeError, match="K % 64"):
         hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM, h, nw, a=a, ssq=ssq)
-
-
-# ---- row statistics handed from a producer plan's epilogue to the next plan's prologue ----
-# A producer fused plan with zero weights outputs exactly its residual, so any row r can be
-# injected as the producer's output; its statistics epilogue (rt_plan_set_row_stats) then
-# feeds a consumer with source RMSNORM_STATS, whose result must equal the same consumer
-# reducing the row itself (RMSNORM) bit for bit, for every kind of row: random, all values
-# tied (every 32-group has many absmax candidates: the slow path), all zero, values so
-# small that the normalised products are subnormal, two maxima in one group or in two,
-# and norm weights with zeros.
-ROW_KINDS = ["random", "ties", "zero", "tiny", "dup_max_same_group", "dup_max_two_groups", "zero_weights"]
-
-
-def _stat_row(kind, K, rng):
-    r = rng.standard_normal(K).astype(np.float32) * 3
-    w = rng.uniform(0.5, 1.5, K).astype(np.float32)
-    if kind == "ties":
-        r[:] = 1.5
-        w[:] = 0.75
-    elif kind == "zero":
-        r[:] = 0.0
-    elif kind == "tiny":
-        r *= np.float32(1e-41)  # subnormal inputs
-    elif kind == "dup_max_same_group":
-        w[:] = 1.0
-        r[70], r[75] = 50.0, -50.0
-    elif kind == "dup_max_two_groups":
-        w[:] = 1.0
-        r[3], r[K - 5] = 40.0, 40.0
-    elif kind == "zero_weights":
-        w[::3] = 0.0
-        r[::3] *= 100  # the largest |r| meet zero weights
-    return r, w
-
-
-@pytest.mark.parametrize("kind", ROW_KINDS)
-@pytest.mark.parametrize("K,N", [(2560, 6912), (6912, 2560)])
-def test_row_stats_handoff(hip, kind, K, N):
-    import torch
-
-    from rotor import _hip
-
-    rng = np.random.default_rng(K + len(kind))
-    d = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
-    r, w = _stat_row(kind, K, rng)
-    # producer: K outputs = the injected row (zero weights over a random 2560-input row)
-    wz = hip.upload(O.pack_rotor(np.zeros((K, 2560), np.int8)), 2560, 0.02)
-    xin, h, res = d(rng.standard_normal(2560)), torch.empty(K, device="cuda"), d(r)
-    wn = d(w)
-    stats = hip.row_stats_buffer(K)
-    prod = hip.plan_fused([wz], _hip.SRC_RMSNORM, xin, d(np.ones(2560)), eps=1e-6, ys=[h], residuals=[res])
-    prod.set_row_stats(wn, stats)
-    prod.run()
-    torch.cuda.synchronize()
-    assert torch.equal(h, res)
-    W, sw = O.make_ternary(rng, N, K)
-    wt = hip.upload(O.pack_rotor(W), K, sw)
-    y_stats, y_ref = torch.empty(N, device="cuda"), torch.empty(N, device="cuda")
-    hip.plan_fused([wt], _hip.SRC_RMSNORM_STATS, h, wn, stats, eps=1e-6, ys=[y_stats]).run()
-    hip.plan_fused([wt], _hip.SRC_RMSNORM, h, wn, eps=1e-6, ys=[y_ref]).run()
-    torch.cuda.synchronize()
-    assert torch.equal(y_stats, y_ref), f"max |diff| {(y_stats - y_ref).abs().max().item()}"
-    # the records: f64 sums of squares and maxima of |y| |w| per 32 elements
-    rec = stats.cpu().numpy().view(np.float64).reshape(-1, 4)
-    r64, w64 = r.astype(np.float64).reshape(-1, 32), np.abs(w.astype(np.float64)).reshape(-1, 32)
-    np.testing.assert_allclose(rec[:, 0], (r64 ** 2).sum(1), rtol=1e-13, atol=0)
-    assert np.array_equal(rec[:, 1], (np.abs(r64) * w64).max(1))
-    # and the consumer's input equals the oracle's quantisation of RMSNorm(r) * w
-    q_ref, s_ref = O.quant_rows(O.rms_norm_f64acc(r[None], w))
-    y_or = (O.linear_i64_fast(q_ref, W).astype(np.float32) * s_ref[:, None]) * np.float32(sw)
-    assert np.array_equal(y_stats.cpu().numpy(), y_or[0])
-
-
-@pytest.mark.parametrize("kind", ["random", "ties", "zero"])
-def test_row_stats_gate_up_pair_to_down(hip, kind):
-    """The decode FFN with statistics: the gate/up pair plan (consuming h's statistics) writes
-    a = relu(g)^2 u and a's statistics against the FFN sub-norm; the down plan consuming them
-    equals the RMSNORM_SSQ down plan, and the pair's a equals the RMSNORM pair's."""
-    import torch
-
-    from rotor import _hip
-
-    D, F = 2560, 6912
-    rng = np.random.default_rng(7 + len(kind))
-    d = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
-    r, nw = _stat_row(kind, D, rng)
-    hs = hip.row_stats_buffer(D)
-    wz = hip.upload(O.pack_rotor(np.zeros((D, 2560), np.int8)), 2560, 0.02)
-    h = torch.empty(D, device="cuda")
-    prod = hip.plan_fused([wz], _hip.SRC_QUANT, d(rng.standard_normal(2560)), ys=[h], residuals=[d(r)])
-    prod.set_row_stats(d(nw), hs)
-    prod.run()
-    (Wg, sg), (Wu, su), (Wd, sd) = O.make_ternary(rng, F, D), O.make_ternary(rng, F, D), O.make_ternary(rng, D, F)
-    wg, wu = hip.upload(O.pack_rotor(Wg), D, sg), hip.upload(O.pack_rotor(Wu), D, su)
-    wd = hip.upload(O.pack_rotor(Wd), F, sd)
-    w_gu, scales = hip.interleave_gate_up(wg, wu)
-    nwf = d(rng.uniform(0.5, 1.5, F))
-    a1, a2 = torch.empty(F, device="cuda"), torch.empty(F, device="cuda")
-    q1, q2 = torch.empty(F // 32, dtype=torch.float64, device="cuda"), torch.empty(F // 32, dtype=torch.float64,
-                                                                                     device="cuda")
-    ast = hip.row_stats_buffer(F)
-    pair = hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM_STATS, h, d(nw), hs, eps=1e-6, a=a1, ssq=q1)
-    pair.set_row_stats(nwf, ast)
-    pair.run()
-    hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM, h, d(nw), eps=1e-6, a=a2, ssq=q2).run()
-    torch.cuda.synchronize()
-    assert torch.equal(a1, a2) and torch.equal(q1, q2)
-    y1, y2 = torch.empty(D, device="cuda"), torch.empty(D, device="cuda")
-    hip.plan_fused([wd], _hip.SRC_RMSNORM_STATS, a1, nwf, ast, eps=1e-6, ys=[y1]).run()
-    hip.plan_fused([wd], _hip.SRC_RMSNORM_SSQ, a2, nwf, q2, eps=1e-6, ys=[y2]).run()
-    torch.cuda.synchronize()
-    assert torch.equal(y1, y2)
-
-
-def test_row_stats_rejects_plans(hip):
-    import torch
-
-    from rotor import _hip
-
-    rng = np.random.default_rng(1)
-    d = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
-    ws = [hip.upload(O.pack_rotor(O.make_ternary(rng, 64, 128)[0]), 128, 1.0) for _ in range(2)]
-    x, ys = d(rng.standard_normal(128)), [torch.empty(64, device="cuda") for _ in range(2)]
-    two = hip.plan_fused(ws, _hip.SRC_QUANT, x, ys=ys)
-    with pytest.raises(RuntimeError, match="one-problem"):
-        two.set_row_stats(d(np.ones(64)), hip.row_stats_buffer(64))
-    with pytest.raises(ValueError):
-        two.set_row_stats(d(np.ones(64)), None)

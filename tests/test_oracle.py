@@ -426,6 +426,37 @@ def test_attention_closed_forms():
     assert np.allclose(out2[1, 0], V[0, :2].mean(0), atol=1e-6)
 
 
+def _two_key_case(hd, a, seed):
+    """q = a e_0, keys [e_0, 0], values [v0, v1]: the query at position 1 sees both keys
+    with scores a * scale and 0, so out = sig(a * scale) v0 + (1 - sig(a * scale)) v1."""
+    rng = np.random.default_rng(seed)
+    q = np.zeros((1, 1, hd), np.float32)
+    q[0, 0, 0] = a
+    K = np.zeros((1, 2, hd), np.float32)
+    K[0, 0, 0] = 1.0
+    V = rng.standard_normal((1, 2, hd)).astype(np.float32)
+    return q, K, V
+
+
+def two_key_expected(V, a, scale):
+    w0 = 1.0 / (1.0 + np.exp(-a * scale))
+    return w0 * V[0, 0].astype(np.float64) + (1.0 - w0) * V[0, 1].astype(np.float64)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_attention_score_scale_kat(hd):
+    """Known answer for the score scale 1/sqrt(head_dim) (src/rotor/transformer.py:266-267),
+    which the closed forms above leave free: with two keys whose scores are a/sqrt(hd) and 0
+    the output is the logistic mix sig(a/sqrt(hd)) v0 + (1 - sig) v1.  A scale of 1/hd, or
+    none, gives a mix that differs by more than 1e-2 here."""
+    a = 8.0
+    q, K, V = _two_key_case(hd, a, hd)
+    out = O.causal_gqa_attention(q, K, V, 1)[0, 0].astype(np.float64)
+    np.testing.assert_allclose(out, two_key_expected(V, a, 1.0 / np.sqrt(hd)), rtol=0, atol=2e-6)
+    for wrong in (1.0 / hd, 1.0):
+        assert np.abs(out - two_key_expected(V, a, wrong)).max() > 1e-2
+
+
 def test_bitnet_incremental_equals_full():
     cfg = dict(vocab_size=50, d_model=32, n_layers=2, n_heads=4, n_kv_heads=2, d_ff=48)
     p = O.make_bitnet_params(3, cfg, 16)

@@ -72,3 +72,56 @@ def test_noalloc_rejects_inputs_beyond_the_buffer(hip):
             assert rc == RT_EINVAL and "static buffer" in _hip.last_error()
             assert torch.all(y == 7.0).item()  # nothing was launched
     assert lib.rt_linear_f32_noalloc(hip.ctx, w.handle, None, 1, None) == RT_EINVAL
+
+
+# The allocation-free call captured in a HIP graph: every replay, each on a new input written
+# in place between replays (with the process's own eager launches and synchronisations in
+# between), equals the eager rt_linear_f32 bit for bit.  The child process captures each
+# shape BEFORE any launch of its kernels in that process (the tile GEMM, the split-K GEMM, the
+# 128 x 160 region GEMM, the one-launch M = 1 GEMV): the first launch of a kernel then happens
+# under the capture.
+_CAPTURE_CHILD = r"""
+import sys
+sys.path[:0] = [sys.argv[1] + "/rotor-rag_amd", sys.argv[1]]
+import numpy as np, torch
+from oracle import rotor_oracle as O
+from rotor import _hip
+from rotor.gpu_ternary import HIPTernaryOps
+hip = HIPTernaryOps(0)
+lib = _hip.load()
+for i, (M, N, K) in enumerate([(300, 640, 2560), (37, 640, 2560), (2048, 2560, 6912), (1, 6912, 2560)]):
+    print(f"capture case {i}: M={M} N={N} K={K}", flush=True)
+    x, W, scale = O.make_linear_case(200 + i, M, N, K)
+    w = hip.upload(O.pack_rotor(W), K, scale)
+    xd = torch.from_numpy(x).cuda()
+    y = torch.full((M, N), float("nan"), device="cuda")
+    y_ref = torch.empty((M, N), device="cuda")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        hip._bind_stream()
+        rc = lib.rt_linear_f32_noalloc(hip.ctx, w.handle, xd.data_ptr(), M, y.data_ptr())
+    assert rc == 0, _hip.last_error()
+    hip._bind_stream()
+    for rep in range(3):
+        xd.copy_(torch.randn((M, K), device="cuda"))
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        assert lib.rt_linear_f32(hip.ctx, w.handle, xd.data_ptr(), M, y_ref.data_ptr()) == 0, _hip.last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_ref), f"case {i} replay {rep}: max |diff| {(y - y_ref).abs().max().item()}"
+    del g
+print("CAPTURE_OK", flush=True)
+"""
+
+
+def test_noalloc_captured_in_a_graph(hip):
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, "-c", _CAPTURE_CHILD, str(root)], capture_output=True, text=True,
+                       timeout=240)
+    assert r.returncode == 0 and "CAPTURE_OK" in r.stdout, (r.stdout[-2000:], r.stderr[-3000:])

@@ -17,6 +17,9 @@ value      = algorithmic bytes of the G GEMVs per step / step time (GB/s), where
              between two HIP events on the launch stream;
 roofline   = the same bytes over the kernel's average launch duration from that same
              timed region (one step is exactly one launch of the kernel), against 8 TB/s;
+             profile_kernel_us / profile_frac: the kernel's mean duration in the committed
+             rocprofv3 kernel trace of the same command (profiles/gemv_2560x6912_m1_g128.md,
+             profile_commit = the commit it was taken on) and the fraction it gives;
 two_launch_form = the same plan as a quantiser launch + a GEMV launch (int8 x read
              by the GEMV: N*K/4 + K + 4 + 4*N + 4 bytes per GEMV), for comparison;
 cpu_baseline = the reference's CPU path np.dot(x, W_i8.T) * scale
@@ -24,7 +27,8 @@ cpu_baseline = the reference's CPU path np.dot(x, W_i8.T) * scale
              shapes with one BLAS thread and with every core of the process's affinity,
              the reference's C core (bit planes -> int8 unpack, the 1-bit-activation
              mat-vec) restated in C and built from its own source, and a capped cfg-4
-             CPU decode; `value` is the all-core NumPy rate at the metric's shape.  The GPU
+             CPU decode; `value` is the NumPy rate at the metric's shape with the faster of
+             one BLAS thread and all of them (`cores` says which).  The GPU
              result of one metric problem is checked against the oracle in the same leg.
 """
 from __future__ import annotations
@@ -50,20 +54,26 @@ D_MODEL, D_FF, HEADS, KV_HEADS, VOCAB = 2560, 6912, 20, 5, 128256
 # the seven projections of one BitNet-2B layer: (N, K)
 LAYER_SHAPES = {"q_proj": (2560, 2560), "k_proj": (640, 2560), "v_proj": (640, 2560), "o_proj": (2560, 2560),
                 "gate_proj": (6912, 2560), "up_proj": (6912, 2560), "down_proj": (2560, 6912)}
+# cfg 2's timed plan: (N, K, input index) of q, k, v (input 0), o (1), gate, up (2), down (3)
+LAYER_M64_SHAPES = [(2560, 2560, 0), (640, 2560, 0), (640, 2560, 0), (2560, 2560, 1), (6912, 2560, 2), (6912, 2560, 2),
+                    (2560, 6912, 3)]
 
 PROFILE = ROOT / "profiles" / "gemv_2560x6912_m1_g128.md"
 
 
-def profiled_traffic():
-    """HBM bytes per GEMV launch measured by the committed rocprofv3 PMC passes
-    (FETCH_SIZE/WRITE_SIZE scaled by a plain-copy calibration), or None."""
+def profile_fields():
+    """The `key: value` lines of the committed metric profile (rocprofv3 summary): the HBM
+    bytes per GEMV launch from the PMC passes (FETCH_SIZE/WRITE_SIZE scaled by a plain-copy
+    calibration), the kernel's mean duration in the kernel trace and the commit profiled."""
+    out = {}
     try:
         for line in PROFILE.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1])
+            for key in ("traffic_bytes_per_launch", "profile_kernel_us", "profile_commit"):
+                if line.startswith(key + ":"):
+                    out[key] = line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return None
+    return out
 
 
 def gemv_bytes(M, N, K):
@@ -122,8 +132,7 @@ def prefill_and_layer(torch, hip, gen, dev, reps=50, layers=20):
                      "tile": f"{tm}x{tn}", "tiles": tiles, "launches": reps}
         del plan, w, x, y
     M = 64
-    shapes = [(2560, 2560, 0), (640, 2560, 0), (640, 2560, 0), (2560, 2560, 1), (6912, 2560, 2), (6912, 2560, 2),
-              (2560, 6912, 3)]
+    shapes = LAYER_M64_SHAPES
     xs_in = [torch.randn((M, K), generator=gen, device=dev, dtype=torch.float32) for K in (2560, 2560, 2560, 6912)]
     ys = [torch.empty((M, N), device=dev, dtype=torch.float32) for N, _, _ in shapes]
     plans, keep = [], []
@@ -143,6 +152,15 @@ def prefill_and_layer(torch, hip, gen, dev, reps=50, layers=20):
     b.record()
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / (rounds * layers)
+    # the same rotation with the per-row quantisation of the fp32 inputs (cfg 2's x is fp32):
+    # run() = one quantiser launch over the 4 distinct inputs + the GEMM launch
+    a.record()
+    for _ in range(rounds):
+        for p in plans:
+            p.run()
+    b.record()
+    torch.cuda.synchronize()
+    ms_run = a.elapsed_time(b) / (rounds * layers)
     ops = sum(2.0 * M * N * K for N, K, _ in shapes)
     wbytes = sum(N * K // 4 for N, K, _ in shapes)
     abytes = wbytes + sum(M * K + 4 * M for K in (2560, 2560, 6912)) + sum(4 * M * N for N, _, _ in shapes)
@@ -150,8 +168,11 @@ def prefill_and_layer(torch, hip, gen, dev, reps=50, layers=20):
         "M": M, "us": round(ms * 1e3, 2), "TOPS": round(ops / (ms * 1e-3) / 1e12, 1),
         "GB_per_s": round(abytes / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(abytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "rotation_MB": round(layers * wbytes / 1e6, 1),
-        "note": f"7 projections of a BitNet-2B layer as one split-K launch; {layers} distinct layers in rotation "
-                "(weights stream from HBM); bytes = 2-bit weights + int8 inputs + fp32 outputs"}
+        "with_quantiser_us": round(ms_run * 1e3, 2),
+        "workgroups": plans[0].describe()[3],
+        "note": f"7 projections of a BitNet-2B layer as one split-K launch (GEMM only: p.gemv(); with_quantiser_us: "
+                f"p.run(), the per-row quantisation of the 4 distinct fp32 inputs first); {layers} distinct layers in "
+                "rotation (weights stream from HBM); bytes = 2-bit weights + int8 inputs + fp32 outputs"}
     return out
 
 
@@ -508,6 +529,8 @@ def main():
     ap.add_argument("--cpu-model-steps", type=int, default=2, help="capped cfg-4 CPU decode steps (0: skip)")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill / M=64 layer / FFN block measurements")
     ap.add_argument("--no-model", action="store_true", help="skip the cfg-4 decode measurement")
+    ap.add_argument("--extra-reps", type=int, default=50,
+                    help="launches per cfg-3 GEMM timing (cfg-2 rounds: a fifth of it; profiler runs use few)")
     ap.add_argument("--copy-calib", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (reference point for HBM counters)")
     args = ap.parse_args()
@@ -611,7 +634,7 @@ def main():
     extra = None
     if not args.no_extra:
         print("bench: cfg-3 prefill GEMMs, cfg-2 layer rotation, cfg-1 FFN block rotation", file=sys.stderr, flush=True)
-        extra = prefill_and_layer(torch, hip, gen, dev)
+        extra = prefill_and_layer(torch, hip, gen, dev, reps=args.extra_reps)
         extra["cfg1_ffn_block_m1"] = ffn_block_cfg1(torch, hip, gen, dev)
     cfg4 = None
     if not args.no_model:
@@ -628,6 +651,8 @@ def main():
         cpu, parity = cpu_baseline(hip, ws[0], xs[0], ys[0], torch, gen, dev, budget_s=args.cpu_budget,
                                    model_steps=args.cpu_model_steps)
 
+    prof = profile_fields() if G == 128 else {}
+    prof_us = float(prof["profile_kernel_us"]) if "profile_kernel_us" in prof else None
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -654,13 +679,18 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
-            "traffic": profiled_traffic() if G == 128 else None,
+            "traffic": int(prof["traffic_bytes_per_launch"]) if G == 128 and "traffic_bytes_per_launch" in prof else None,
             "traffic_source": "profiles/gemv_2560x6912_m1_g128.md (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
             "kernel": "rt::gemv_rows_kernel<1, 1>",
             "bytes_per_launch": bytes_step,
             "avg_launch_ms": round(step_ms, 5),
             "timing": "HIP events around the timed region's back-to-back launches (one launch per step)",
             "isolated_launch_ms_dist": run_dist,
+            # the same fraction from the committed rocprofv3 kernel trace of this workload (the
+            # kernel's mean duration there; another run on another box)
+            "profile_kernel_us": prof_us,
+            "profile_frac": round(bytes_step / (prof_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if prof_us else None,
+            "profile_commit": prof.get("profile_commit"),
         },
         "two_launch_form": {
             "step_ms": round(two_step_ms, 5),

@@ -214,6 +214,48 @@ def test_plan_matches_single_calls(hip, M):
             assert torch.equal(y, hip.linear_device(w, x))
 
 
+# cfg 2's timed plan (bench.py LAYER_M64_SHAPES): the seven projections of a BitNet-2B
+# layer at M = 64 as ONE split-K launch, q / k / v sharing input 0, o input 1, gate / up input
+# 2, down (K = 6912) input 3 and cut into parts
+CFG2_SHAPES = [(2560, 2560, 0), (640, 2560, 0), (640, 2560, 0), (2560, 2560, 1), (6912, 2560, 2), (6912, 2560, 2),
+               (2560, 6912, 3)]
+
+
+def test_cfg2_layer_plan_vs_oracle(hip):
+    """The exact plan bench.py times for cfg 2: one split-K launch of 436 workgroups (the 356
+    row blocks, down's 40 in three parts), every output bit-exact against the oracle's
+    int64 accumulators and exact epilogue, on two runs (the parts' arrival counts reset
+    themselves) and with the quantiser (run) or on activations quantised before (gemv)."""
+    import torch
+
+    from rotor import _hip as H_
+
+    M = 64
+    rng = np.random.default_rng(64)
+    inputs = [rng.standard_normal((M, K), dtype=np.float32) for K in (2560, 2560, 2560, 6912)]
+    xd = [torch.from_numpy(x).cuda() for x in inputs]
+    Ws, ws, ys = [], [], []
+    for N, K, _ in CFG2_SHAPES:
+        W, scale = O.make_ternary(rng, N, K)
+        Ws.append((W, scale))
+        ws.append(hip.upload(O.pack_rotor(W), K, scale))
+        ys.append(torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda"))
+    plan = hip.plan(ws, [xd[xi] for _, _, xi in CFG2_SHAPES], ys)
+    assert plan.describe() == (H_.LAUNCH_SPLITK, 64, 64, 436)
+    for rep in range(3):
+        for y in ys:
+            y.fill_(float("nan"))
+        if rep < 2:
+            plan.run()
+        else:
+            plan.gemv()  # the activations of the previous run are still in place
+        torch.cuda.synchronize()
+        for (W, scale), (N, K, xi), y in zip(Ws, CFG2_SHAPES, ys):
+            _, q, s_, acc = O.ternary_linear(inputs[xi], W, scale)
+            y_exact = (acc.astype(np.float32) * s_[:, None]) * np.float32(scale)
+            assert np.array_equal(y.cpu().numpy(), y_exact), f"run {rep}: projection {N}x{K} (input {xi})"
+
+
 # Tile-GEMM plans (M > 64) and the tile shape each must take, checked bit-exact against the
 # oracle problem by problem: name -> (M, [(N, K, input index)], (tile_m, tile_n, tiles)).
 TILE_PLANS = {

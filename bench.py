@@ -225,18 +225,15 @@ def ffn_block_cfg1(torch, hip, gen, dev, blocks=24, reps=10):
                     "back to back"}
 
 
-def decode_cfg4(torch, hip, gen, dev, n_layers=30, prompt_len=512, new_tokens=128):
-    """cfg 4: 30-layer BitNet-2B-shape random-init model (hidden 2560, ffn 6912, 20/5 heads
-    x 128, RoPE, RMSNorm, bf16 tied embedding/LM head over 128256 tokens), 512 random
-    prompt ids, greedy decode of 128 tokens with the KV cache, batch 1."""
-    import numpy as np
-
+def build_cfg4_model(torch, hip, gen, dev, n_layers=30, max_seq_len=640, max_batch_tokens=512):
+    """The cfg-4 model with seeded random-init weights drawn on the device (the
+    configurations' distributions), loaded through BitNetModel.load_state."""
     from rotor import gpu_layers
     from rotor.bitnet_model import BitNetModel
 
     D, F, H, Hkv, V = D_MODEL, D_FF, HEADS, KV_HEADS, VOCAB
     cfg = dict(vocab_size=V, d_model=D, n_layers=n_layers, n_heads=H, n_kv_heads=Hkv, d_ff=F,
-               rope_theta=500000.0, rms_norm_eps=1e-6, max_seq_len=prompt_len + new_tokens, max_batch_tokens=prompt_len)
+               rope_theta=500000.0, rms_norm_eps=1e-6, max_seq_len=max_seq_len, max_batch_tokens=max_batch_tokens)
     state = {"model.embed_tokens.weight": torch.randn((V, D), generator=gen, device=dev).to(torch.bfloat16),
              "model.norm.weight": torch.rand(D, generator=gen, device=dev) + 0.5}
     for i in range(n_layers):
@@ -255,7 +252,17 @@ def decode_cfg4(torch, hip, gen, dev, n_layers=30, prompt_len=512, new_tokens=12
         model.load_state(state)
     finally:
         gpu_layers._gpu_instance = None
-    del state
+    return model
+
+
+def decode_cfg4(torch, hip, gen, dev, n_layers=30, prompt_len=512, new_tokens=128):
+    """cfg 4: 30-layer BitNet-2B-shape random-init model (hidden 2560, ffn 6912, 20/5 heads
+    x 128, RoPE, RMSNorm, bf16 tied embedding/LM head over 128256 tokens), 512 random
+    prompt ids, greedy decode of 128 tokens with the KV cache, batch 1."""
+    import numpy as np
+
+    D, V = D_MODEL, VOCAB
+    model = build_cfg4_model(torch, hip, gen, dev, n_layers, prompt_len + new_tokens, prompt_len)
     prompt = np.random.default_rng(4).integers(0, V, prompt_len).astype(np.int32)
     model.generate_greedy(prompt, 8)  # warm-up (kernels, plans, graph)
     t = {}

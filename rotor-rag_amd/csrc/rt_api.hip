@@ -1290,7 +1290,8 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
         return fail(RT_EINVAL, std::string(who) + ": the plan's source must be a 16-byte aligned row with K % 64 == 0");
     DeviceGuard g(plan->device);
     const size_t words = (size_t)(H + 2 * Hkv) * hd;
-    const size_t bytes = words * sizeof(unsigned long long) + 256;
+    // the tagged outputs, then epoch, done, err (16 bytes) and the KV groups' arrival counts
+    const size_t bytes = words * sizeof(unsigned long long) + 256 + (size_t)Hkv * sizeof(int);
     // a launch of this plan may still be in flight on the caller's stream: wait for it
     // before the hand-off state is freed or reset
     if (plan->att_mem) RT_HIP(hipDeviceSynchronize());
@@ -1306,6 +1307,9 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
     t.epoch = reinterpret_cast<unsigned*>(tail);
     t.done = tail + 1;
     t.err = tail + 2;
+    t.gdone = tail + 4;
+    t.out = nullptr;  // rt_plan_attention_combine attaches the combine
+    t.ssq = nullptr;
     RT_HIP(attention_state_reset(plan));
     t.Kc = k_cache;
     t.Vc = v_cache;
@@ -1321,6 +1325,27 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
     plan->att_Hkv = Hkv;
     plan->att_hd = hd;
     plan->att_on = true;
+    return RT_OK;
+}
+
+int rt_plan_attention_combine(rt_plan* plan, float* out, double* ssq) {
+    const char* who = "rt_plan_attention_combine";
+    if (!plan) return fail(RT_EINVAL, std::string(who) + ": plan is NULL");
+    if (!out != !ssq) return fail(RT_EINVAL, std::string(who) + ": give both out and ssq, or neither");
+    if (out) {
+        if (!plan->att_on) return fail(RT_EINVAL, std::string(who) + ": attach the attention first "
+                                                                     "(rt_plan_attach_attention)");
+        if (plan->att.S > kAttnSMax)
+            return fail(RT_EINVAL, std::string(who) + ": at most " + std::to_string(kAttnSMax) +
+                                       " key blocks (Lmax <= " + std::to_string(64 * kAttnSMax) + ")");
+        if (((uintptr_t)out & 15u) || ((uintptr_t)ssq & 7u))
+            return fail(RT_EINVAL, std::string(who) + ": out must be 16-byte and ssq 8-byte aligned");
+    }
+    DeviceGuard g(plan->device);
+    // a launch of this plan may still be in flight on the caller's stream
+    RT_HIP(hipDeviceSynchronize());
+    plan->att.out = out;
+    plan->att.ssq = ssq;
     return RT_OK;
 }
 

@@ -92,7 +92,18 @@ __device__ __forceinline__ void attn_rope_load(const float* __restrict__ rope, i
 // summation order, and, when `writer` (the first query head of its KV group), writes them
 // into the caches of KV head kh for the later steps.  Without ROPE, qh is already rotated
 // and the caches hold the new key.
-template <int HD, bool ROPE, typename SRC>
+// A partial's value: a plain store, or (COH) a device-coherent one, for a reader in another
+// workgroup of the same launch.
+template <bool COH>
+__device__ __forceinline__ void part_store(float* p, float v) {
+    if constexpr (COH)
+        __hip_atomic_store(reinterpret_cast<unsigned*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
+
+template <int HD, bool ROPE, bool COH = false, typename SRC>
 __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float sn, float* __restrict__ Kc,
                                           float* __restrict__ Vc, int kh, bool writer, int Lmax, int pos, int j0,
                                           float scale, float* __restrict__ wp, int t, AttnLdsPtr<HD> sm,
@@ -159,8 +170,8 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
         const float z = wave_reduce63(p, 0.0f, [](float x, float y) { return x + y; });
         sm->pr[lane] = p;
         if (lane == 63) {
-            wp[HD] = mx;
-            wp[HD + 1] = z;
+            part_store<COH>(wp + HD, mx);
+            part_store<COH>(wp + HD + 1, z);
         }
     }
     attn_lds_barrier();
@@ -207,16 +218,16 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
     if (g == 0) {
         float o = sm->ored[d];
         for (int gg = 1; gg < G; ++gg) o += sm->ored[gg * HD + d];
-        wp[d] = o;
+        part_store<COH>(wp + d, o);
     }
 }
 
 // The partial of an empty block (no key at or before the position).
-template <int HD>
+template <int HD, bool COH = false>
 __device__ __forceinline__ void attn_tile_empty(float* __restrict__ wp, int t) {
     if (t == 0) {
-        wp[HD] = -INFINITY;
-        wp[HD + 1] = 0.0f;
+        part_store<COH>(wp + HD, -INFINITY);
+        part_store<COH>(wp + HD + 1, 0.0f);
     }
 }
 

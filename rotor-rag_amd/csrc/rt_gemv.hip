@@ -531,6 +531,61 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
 // the values in LDS, and the tiles of rt_attn_decode.h run on them.  Forward
 // progress: the attention workgroups wait only for GEMV workgroups, which come first in
 // the grid and never wait.
+// The last attention workgroup of KV group kh to finish combines the group's partials
+// (every block of its Gq heads) into at.out, in the operation order of
+// attn_combine_element, and writes per 32 outputs the f64 sum of their squares into at.ssq
+// (the input of an RMSNORM_SSQ prologue).  The partials are stored device-coherent; every
+// workgroup waits for its own stores, then adds one to the group's arrival count; the last
+// arriver resets the count and reads the others' partials device-coherent (the hand-off of
+// the split-K GEMM's parts).  flag: an int of the workgroup's LDS no tile uses any more.
+template <int HD>
+__device__ __forceinline__ void attn_group_combine(const AttnTail& at, int kh, __attribute__((address_space(3))) int* flag) {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if (threadIdx.x == 0) {
+        const int prev = __hip_atomic_fetch_add(at.gdone + kh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = prev == at.S - 1;
+        if (last) __hip_atomic_store(at.gdone + kh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = last ? 1 : 0;
+    }
+    attn_lds_barrier();
+    if (!*flag) return;
+    const int sub = (int)(threadIdx.x >> 8), t = (int)(threadIdx.x & 255), h = kh * at.Gq + sub, S = at.S;
+    if (t >= HD) return;  // (HD % 64 == 0: whole waves) no barrier follows
+    const unsigned* wh = reinterpret_cast<const unsigned*>(at.work + (size_t)h * S * (HD + 2));
+    auto ld = [](const unsigned* p) {
+        return __uint_as_float(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    };
+    // every load at once (blocks past S re-read block S - 1 and are ignored)
+    float m[kAttnSMax], z[kAttnSMax], p[kAttnSMax];
+#pragma unroll
+    for (int s = 0; s < kAttnSMax; ++s) {
+        const unsigned* ps = wh + (size_t)min(s, S - 1) * (HD + 2);
+        p[s] = ld(ps + t);
+        m[s] = ld(ps + HD);
+        z[s] = ld(ps + HD + 1);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kAttnSMax; ++s)
+        if (s < S) mx = fmaxf(mx, m[s]);
+    float num = 0.0f, den = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kAttnSMax; ++s) {
+        if (s >= S || m[s] == -INFINITY) continue;
+        const float f = expf(m[s] - mx);
+        num = fmaf(f, p[s], num);
+        den = fmaf(f, z[s], den);
+    }
+    const float o = num / den;
+    const int k = h * HD + t;
+    at.out[k] = o;
+    // lanes 0..31 and 32..63 of the wave: 32 consecutive outputs each
+    const double ss = half_reduce31((double)o * (double)o, 0.0, [](double x, double y) { return x + y; });
+    if ((t & 31) == 31) at.ssq[k >> 5] = ss;
+}
+
 template <int HD>
 __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb) {
     extern __shared__ __attribute__((aligned(16))) int red[];
@@ -570,11 +625,12 @@ __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb)
             qkv[e] = __uint_as_float((unsigned)w);
         }
         __syncthreads();
-        attn_tile<HD, true>(qkv + sub * HD, qkv + at.Gq * HD, qkv + (at.Gq + 1) * HD, c, sn, at.Kc, at.Vc, kh,
-                            sub == 0, at.Lmax, pos, j0, at.scale, wp, t, sm + sub, kv);
+        attn_tile<HD, true, true>(qkv + sub * HD, qkv + at.Gq * HD, qkv + (at.Gq + 1) * HD, c, sn, at.Kc, at.Vc,
+                                  kh, sub == 0, at.Lmax, pos, j0, at.scale, wp, t, sm + sub, kv);
     } else {
-        attn_tile_empty<HD>(wp, t);
+        attn_tile_empty<HD, true>(wp, t);
     }
+    if (at.out) attn_group_combine<HD>(at, kh, (__attribute__((address_space(3))) int*)qkv);
     // the last attention workgroup of the launch (every other one is past its reads) resets
     // the count and advances the epoch
     if (threadIdx.x == 0 &&

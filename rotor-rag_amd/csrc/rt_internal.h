@@ -171,6 +171,13 @@ struct AttnTail {
     int Gq, Lmax, S, nkv;        // nkv = Hkv hd: where k starts after q (H hd), v after k
     int qrows;                   // H hd
     float scale;
+    // rt_plan_attention_combine (out != nullptr, S <= kAttnSMax): the last attention
+    // workgroup of KV group kh to finish (gdone [Hkv] arrival counts, reset by it) combines
+    // the group's partials into out [H hd] and writes per 32 outputs the f64 sum of their
+    // squares into ssq [H hd / 32]
+    float* out;
+    double* ssq;
+    int* gdone;
 };
 
 struct GemvShape {

@@ -16,6 +16,10 @@
 
 #include "rt_internal.h"
 
+// every product and sum below rounds on its own unless written as fmaf (this header is
+// included before the sources' own pragmas)
+#pragma clang fp contract(off)
+
 namespace rt {
 
 typedef __attribute__((address_space(3))) float lfloat;
@@ -96,7 +100,9 @@ __device__ __forceinline__ const float* norm_weight(const QuantProb& P) {
 
 // Output element d of head h from decode-attention partials work[h][s][0..hd+2)
 // (unnormalised sum, block max, block sum of exponentials):
-// o = sum_s e^(m_s - m) o_s[d] / sum_s e^(m_s - m) z_s, m = max_s m_s, empty blocks skipped.
+// o = sum_s e^(m_s - m) o_s[d] / sum_s e^(m_s - m) z_s, m = max_s m_s, empty blocks skipped;
+// both sums are fused multiply-adds over s in order (every combine of the partials, here,
+// in attn_factors / the o_proj prologue and in the q/k/v launch, uses this order).
 __device__ __forceinline__ float attn_combine_element(const float* __restrict__ work, int hd, int S, int h, int d) {
     const float* wh = work + (size_t)h * S * (hd + 2);
     float mx = -INFINITY;
@@ -107,8 +113,8 @@ __device__ __forceinline__ float attn_combine_element(const float* __restrict__ 
         const float m_i = pi[hd];
         if (m_i == -INFINITY) continue;
         const float f = expf(m_i - mx);
-        num += f * pi[d];
-        den += f * pi[hd + 1];
+        num = fmaf(f, pi[d], num);
+        den = fmaf(f, pi[hd + 1], den);
     }
     return num / den;
 }
@@ -133,7 +139,7 @@ __device__ __forceinline__ void attn_factors(const QuantProb& P, lfloat* fac) {
             }
             const float f = expf(m_i - mx);
             fac[h * S + i] = f;
-            den += f * wh[(size_t)i * (hd + 2) + hd + 1];
+            den = fmaf(f, wh[(size_t)i * (hd + 2) + hd + 1], den);
         }
         fac[H * S + h] = den;
     }
@@ -160,10 +166,10 @@ __device__ __forceinline__ void source_group(const QuantProb& P, const float* xr
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
                 const float4 t = p[q4];
-                num[4 * q4 + 0] += f * t.x;
-                num[4 * q4 + 1] += f * t.y;
-                num[4 * q4 + 2] += f * t.z;
-                num[4 * q4 + 3] += f * t.w;
+                num[4 * q4 + 0] = fmaf(f, t.x, num[4 * q4 + 0]);
+                num[4 * q4 + 1] = fmaf(f, t.y, num[4 * q4 + 1]);
+                num[4 * q4 + 2] = fmaf(f, t.z, num[4 * q4 + 2]);
+                num[4 * q4 + 3] = fmaf(f, t.w, num[4 * q4 + 3]);
             }
         }
         const float den = fac[H * S + h];
@@ -516,8 +522,8 @@ __device__ __forceinline__ void attn_combine1(const QuantProb& P, const AttnRegs
             if (s >= S || r.m[s] == -INFINITY) continue;
             const float f = expf(r.m[s] - mx);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) num[j] += f * r.p[s][j];
-            den += f * r.z[s];
+            for (int j = 0; j < 4; ++j) num[j] = fmaf(f, r.p[s][j], num[j]);
+            den = fmaf(f, r.z[s], den);
         }
         divide_all<4>(num, den);  // den >= 1: the block holding the maximum adds f = 1 times its sum >= 1
 #pragma unroll

@@ -69,6 +69,7 @@ SIGNATURES = {
                                   ctypes.POINTER(_P), ctypes.POINTER(_P)]),
     "rt_plan_create_gate_up": (_I, [_P, _P, _F, _F, ctypes.POINTER(RtSrc), _P, _P, _P, _P, ctypes.POINTER(_P)]),
     "rt_plan_attach_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t]),
+    "rt_plan_attention_combine": (_I, [_P, _P, _P]),
     "rt_plan_attention_timeouts": (_I, [_P, _P]),
     "rt_embed": (_I, [_P, _P, _I, _I, _P, _I, _P]),
     "rt_rope_kv_append": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),

@@ -267,6 +267,11 @@ class _DeviceModel:
         # partials inside the q/k/v GEMV's launch (rt_plan_attach_attention), one launch per
         # layer fewer; False launches rt_rope_attention_decode after the GEMV
         self.attn_in_qkv = True
+        # decode, with the attention in the q/k/v launch: True (default, Lmax <= 640) also
+        # combines the split partials there (the last workgroup of each KV group), writing the
+        # attention output and its sums of squares, so o_proj's prologue only normalises and
+        # quantises (RMSNORM_SSQ); False lets every o_proj workgroup combine the partials
+        self.attn_combine_in_qkv = True
 
     def _state(self, M):
         st = self.state.get(M)
@@ -281,16 +286,24 @@ class _DeviceModel:
               "ssq": torch.empty(F // 32, dtype=torch.float64, device=dev)}
         st["qkv"], st["gu"], st["o_plan"], st["d_plan"] = [], [], [], []
         st["attn_fused"] = []  # per layer: the q/k/v plan runs the attention partials
+        st["attn_comb"] = []   # per layer: ... and combines them into o[0] (sums of squares in ossq)
+        st["ossq"] = torch.empty(H * hd // 32, dtype=torch.float64, device=dev)
         hip, eps = self.hip, self.m.eps
         for li, L in enumerate(self.layers):
             st["attn_fused"].append(False)
+            st["attn_comb"].append(False)
             if M == 1:  # decode: one launch per plan, the input row is quantised in the GEMV prologue
                 h, o, g, u = st["h"][0], st["o"][0], st["g"][0], st["u"][0]
                 st["qkv"].append(hip.plan_fused([L["q_proj"], L["k_proj"], L["v_proj"]], _hip.SRC_RMSNORM, h,
                                                 L["input_norm"], eps=eps, ys=[st["q"][0], st["k"][0], st["v"][0]]))
                 if self.attn_in_qkv and L["attn_sub_norm"] is not None and self.attn_in_prologue:
                     st["attn_fused"][li] = self._attach_attention(st["qkv"][li], L)
-                if L["attn_sub_norm"] is not None and self.attn_in_prologue:
+                if st["attn_fused"][li] and self.attn_combine_in_qkv and self.Lmax <= 640:
+                    st["qkv"][li].attention_combine(o, st["ossq"])
+                    st["attn_comb"][li] = True
+                    st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_RMSNORM_SSQ, o, L["attn_sub_norm"],
+                                                       st["ossq"], eps=eps, ys=[h], residuals=[h]))
+                elif L["attn_sub_norm"] is not None and self.attn_in_prologue:
                     st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_ATTN_NORM, self.attn_ws,
                                                        L["attn_sub_norm"], eps=eps, ys=[h], residuals=[h],
                                                        attn_head_dim=self.hd, attn_max_len=self.Lmax))
@@ -393,7 +406,7 @@ class _DeviceModel:
                                                      self.hd, self.Lmax, self.pos.data_ptr(), self.attn_ws.data_ptr(),
                                                      self.attn_ws_bytes, o.data_ptr() if combine_here else None),
                         "rt_rope_attention_decode")
-                if tb is not None and combine_here:
+                if tb is not None and (combine_here or st["attn_comb"][li]):  # o[0] holds the output
                     tb["attn"][li].copy_(o[0])
                 elif tb is not None:  # the attention output the o_proj prologue forms from the partials
                     chk(lib.rt_attention_decode_combine(ctx, self.attn_ws.data_ptr(), self.attn_ws_bytes, self.H,

@@ -105,6 +105,21 @@ class LinearPlan:
                    "rt_plan_attach_attention")
         self._keep = (self._keep, k_cache, v_cache, rope, pos, workspace)
 
+    def attention_combine(self, out, ssq) -> None:
+        """Also combine the attention partials in run()'s launch (rt_plan_attention_combine):
+        out fp32 [H*hd] receives the attention output, ssq float64 [H*hd/32] the sums of its
+        squares per 32 outputs (an SRC_RMSNORM_SSQ plan's x and aux2).  (None, None) detaches."""
+        if (out is None) != (ssq is None):
+            raise ValueError("attention_combine: give both out and ssq, or neither")
+        if out is not None:
+            torch = _torch()
+            if (out.dtype != torch.float32 or ssq.dtype != torch.float64 or not out.is_contiguous()
+                    or not ssq.is_contiguous() or ssq.numel() * 32 < out.numel()):
+                raise ValueError("attention_combine: out float32 [H*hd], ssq float64 [H*hd/32], contiguous")
+        ptr = lambda t: t.data_ptr() if t is not None else None
+        _hip.check(_hip.load().rt_plan_attention_combine(self.handle, ptr(out), ptr(ssq)), "rt_plan_attention_combine")
+        self._keep = (self._keep, out, ssq)
+
     def attention_timeouts(self) -> int:
         """Attention waits of this plan's launches that gave up (rt_plan_attention_timeouts;
         synchronises the device).  Never expected: a non-zero count means wrong results."""

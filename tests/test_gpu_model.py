@@ -281,7 +281,9 @@ def test_qkv_plan_with_attention_equals_separate_launches(hip, pos0, Lmax):
     workgroup advances the epoch.  Checked on two runs in a row and on every replay of a
     captured graph, each with a new input row: a launch whose epoch did not advance would
     let the attention start on the previous launch's q/k/v and its partials would differ.
-    No wait gives up."""
+    No wait gives up.  Where Lmax <= 640 the launch also combines the partials
+    (rt_plan_attention_combine): its output equals rt_attention_decode_combine's on the
+    reference partials bit for bit, and its per-32 sums of squares the f64 sums."""
     import torch
 
     from oracle.rotor_oracle import rope_table
@@ -324,18 +326,30 @@ def test_qkv_plan_with_attention_equals_separate_launches(hip, pos0, Lmax):
     ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
     plan = hip.plan_fused(ws_, H_.SRC_RMSNORM, x, nw, eps=1e-6, ys=[q, k, v])
     plan.attach_attention(kcf, vcf, rope, H, Hkv, hd, Lmax, pos, ws)
+    combine = Lmax <= 640
+    o_out = torch.empty(D, device="cuda")
+    o_ssq = torch.empty(D // 32, dtype=torch.float64, device="cuda")
+    o_ref = torch.empty(D, device="cuda")
+    if combine:
+        plan.attention_combine(o_out, o_ssq)
 
     def check(what):
         torch.cuda.synchronize()
         assert torch.equal(q, qr) and torch.equal(k, kr) and torch.equal(v, vr), f"q/k/v differ ({what})"
         assert torch.equal(ws, ws_ref), f"partials differ ({what})"
         assert torch.equal(kcf, kc) and torch.equal(vcf, vc), f"caches differ ({what})"
+        if combine:
+            chk(lib.rt_attention_decode_combine(hip.ctx, ws_ref.data_ptr(), nbytes, H, hd, Lmax, o_ref.data_ptr()))
+            torch.cuda.synchronize()
+            assert torch.equal(o_out, o_ref), f"combined output differs ({what})"
+            o64 = o_ref.cpu().numpy().astype(np.float64).reshape(-1, 32)
+            np.testing.assert_allclose(o_ssq.cpu().numpy(), (o64 ** 2).sum(1), rtol=1e-12, atol=0)
 
     def reset():
         # a new input row (so stale q/k/v words of an earlier launch would be wrong ones)
         x.copy_(f(D))
         reference()
-        for t in (q, k, v):
+        for t in (q, k, v, o_out, o_ssq):
             t.fill_(float("nan"))
         ws.zero_()
         kcf.copy_(kc0)
@@ -355,7 +369,11 @@ def test_qkv_plan_with_attention_equals_separate_launches(hip, pos0, Lmax):
         g.replay()
         check(f"replay {rep}")
     assert plan.attention_timeouts() == 0
+    if not combine:  # too many key blocks for the combine in the launch
+        with pytest.raises(RuntimeError, match="key blocks"):
+            plan.attention_combine(o_out, o_ssq)
     # detached, the plan runs the GEMV only
+    plan.attention_combine(None, None)
     plan.attach_attention(None, None, None, 0, 0, 0, 0, None, None)
     reset()
     plan.run()
@@ -387,6 +405,9 @@ def test_attach_attention_rejects_other_plans(hip):
         three.attach_attention(kc, vc, rope, 10, 5, hd, Lmax, pos, ws)
     with pytest.raises(RuntimeError, match="rt_plan_attach_attention"):  # workspace too small
         three.attach_attention(kc, vc, rope, 20, 5, hd, Lmax, pos, ws[:16])
+    o, ssq = torch.empty(D, device="cuda"), torch.empty(D // 32, dtype=torch.float64, device="cuda")
+    with pytest.raises(RuntimeError, match="attach the attention first"):  # no attention attached
+        three.attention_combine(o, ssq)
     three.run()
     one.run()
     torch.cuda.synchronize()

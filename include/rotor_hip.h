@@ -71,7 +71,8 @@ const char* rt_last_error(void);
  * 102 = 101 + rt_plan_describe; 103 = 102 + rt_linear_f32_noalloc; 104 = 103 + rt_plan_set_row_stats
  * and RT_SRC_RMSNORM_STATS; 105 = 104 + rt_plan_attach_attention and rt_plan_attention_timeouts;
  * 106 = 105 without rt_plan_set_row_stats and RT_SRC_RMSNORM_STATS (measured slower than each
- * decode prologue reducing its own row), + rt_attention_decode_combine. */
+ * decode prologue reducing its own row), + rt_attention_decode_combine,
+ * rt_plan_attention_combine and rt_lm_head_argmax's next_h. */
 int rt_version(void);
 
 /* Number of visible HIP devices (0 when none); RT_OK even when 0. */
@@ -331,10 +332,12 @@ int rt_rope_attention_decode(rt_ctx* ctx, const float* q, const float* k, const 
  * first index of the maximum).  `best` (device u64, zero before first use) is left
  * zero.  token <- argmax; when non-NULL: next_ids[0] <- token and, with
  * p = *pos + advance, out_tokens[p - 1 - pos_base] <- token (if in [0, out_cap)) and
- * *pos <- p (advance = tokens consumed by this forward). */
+ * *pos <- p (advance = tokens consumed by this forward); next_h fp32 [D] <- the token's
+ * embedding row (the next decode step's input, src/rotor/bitnet_model.py:220, so that step
+ * needs no rt_embed; x may be next_h). */
 int rt_lm_head_argmax(rt_ctx* ctx, const uint16_t* emb, const float* x, const float* norm_w, float eps, int V, int D,
                       float* logits, unsigned long long* best, int* token, int* pos, int advance, int* next_ids,
-                      int* out_tokens, int pos_base, int out_cap);
+                      int* out_tokens, int pos_base, int out_cap, float* next_h);
 
 #ifdef __cplusplus
 }

@@ -1123,14 +1123,14 @@ int rt_attention_decode_combine(rt_ctx* ctx, const void* workspace, size_t works
 
 int rt_lm_head_argmax(rt_ctx* ctx, const uint16_t* emb, const float* x, const float* norm_w, float eps, int V, int D,
                       float* logits, unsigned long long* best, int* token, int* pos, int advance, int* next_ids,
-                      int* out_tokens, int pos_base, int out_cap) {
+                      int* out_tokens, int pos_base, int out_cap, float* next_h) {
     if (!ctx || !emb || !x || !norm_w || !logits || !best || !token)
         return fail(RT_EINVAL, "rt_lm_head_argmax: NULL argument");
     if (V <= 0 || D <= 0 || D % 512 || (D / 512 != 1 && D / 512 != 2 && D / 512 != 4 && D / 512 != 5 && D / 512 != 8))
         return fail(RT_EINVAL, "rt_lm_head_argmax: D must be 512, 1024, 2048, 2560 or 4096");
     DeviceGuard g(ctx->device);
     RT_HIP(launch_lm_head(emb, x, norm_w, eps, V, D, logits, best, token, pos, advance, next_ids, out_tokens, pos_base,
-                          out_cap, ctx->stream));
+                          out_cap, next_h, ctx->stream));
     return RT_OK;
 }
 

@@ -363,7 +363,7 @@ hipError_t launch_attn_partial(const float* q, const float* knew, const float* v
 hipError_t launch_attn_combine(const float* work, int H, int hd, int S, float* out, hipStream_t s);
 hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w, float eps, int V, int D,
                           float* logits, unsigned long long* best, int* token, int* pos, int advance,
-                          int* next_ids, int* out_tokens, int pos_base, int out_cap, hipStream_t s);
+                          int* next_ids, int* out_tokens, int pos_base, int out_cap, float* next_h, hipStream_t s);
 
 // Host policy: tokens per workgroup for M tokens.
 inline int gemv_mt(int M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }

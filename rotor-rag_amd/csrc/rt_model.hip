@@ -437,11 +437,22 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
 }
 
 // token = argmax; optionally also written to next_ids[0] (the next step's input) and,
-// with p = *pos_p + advance, to out_tokens[p - 1 - pos_base]; then *pos_p = p.
-__global__ void argmax_finalize_kernel(unsigned long long* best, int* token, int* pos_p, int advance, int* next_ids,
-                                       int* out_tokens, int pos_base, int out_cap) {
+// with p = *pos_p + advance, to out_tokens[p - 1 - pos_base]; then *pos_p = p.  With
+// next_h, the token's embedding row E[token] (bf16 -> fp32, D values) is written there: the
+// next step's input row, so that step needs no embedding launch.
+__global__ void __launch_bounds__(256) argmax_finalize_kernel(unsigned long long* best, int* token, int* pos_p,
+                                                              int advance, int* next_ids, int* out_tokens, int pos_base,
+                                                              int out_cap, const uint16_t* __restrict__ E, int V,
+                                                              int D, float* __restrict__ next_h) {
     const unsigned long long k = *best;
     const int tok = (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull));
+    if (next_h) {
+        // (a row of NaN logits can leave `best` unset: read row 0 rather than out of range)
+        const uint16_t* row = E + (size_t)(tok >= 0 && tok < V ? tok : 0) * D;
+        for (int e = threadIdx.x; e < D; e += blockDim.x) next_h[e] = bf16_to_f32(row[e]);
+    }
+    __syncthreads();  // every thread has read *best
+    if (threadIdx.x != 0) return;
     *token = tok;
     *best = 0ull;  // ready for the next step
     if (next_ids) next_ids[0] = tok;
@@ -537,7 +548,7 @@ static hipError_t run_lm_head(const uint16_t* E, const float* x, const float* no
 
 hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w, float eps, int V, int D,
                           float* logits, unsigned long long* best, int* token, int* pos, int advance,
-                          int* next_ids, int* out_tokens, int pos_base, int out_cap, hipStream_t s) {
+                          int* next_ids, int* out_tokens, int pos_base, int out_cap, float* next_h, hipStream_t s) {
     hipError_t e = hipSuccess;
     switch (D / 512) {
         case 1: e = run_lm_head<1>(E, x, norm_w, eps, V, logits, best, s); break;
@@ -548,8 +559,8 @@ hipError_t launch_lm_head(const uint16_t* E, const float* x, const float* norm_w
         default: return hipErrorInvalidValue;
     }
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(1), 0, s, best, token, pos, advance, next_ids,
-                       out_tokens, pos_base, out_cap);
+    hipLaunchKernelGGL(argmax_finalize_kernel, dim3(1), dim3(next_h ? 256 : 64), 0, s, best, token, pos, advance,
+                       next_ids, out_tokens, pos_base, out_cap, E, V, D, next_h);
     return hipGetLastError();
 }
 

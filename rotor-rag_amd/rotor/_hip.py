@@ -79,7 +79,7 @@ SIGNATURES = {
     "rt_attention_decode_partials": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t]),
     "rt_attention_decode_combine": (_I, [_P, _P, ctypes.c_size_t, _I, _I, _I, _P]),
     "rt_rope_attention_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t, _P]),
-    "rt_lm_head_argmax": (_I, [_P, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I]),
+    "rt_lm_head_argmax": (_I, [_P, _P, _P, _P, _F, _I, _I, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P]),
 }
 
 _lib = None

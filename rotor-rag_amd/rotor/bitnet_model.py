@@ -272,6 +272,10 @@ class _DeviceModel:
         # attention output and its sums of squares, so o_proj's prologue only normalises and
         # quantises (RMSNORM_SSQ); False lets every o_proj workgroup combine the partials
         self.attn_combine_in_qkv = True
+        # generate: True (default) lets every argmax write the chosen token's embedding row into
+        # the decode input, so the decode step launches no embedding; False embeds the token
+        # from its id at the start of every step
+        self.embed_in_argmax = True
 
     def _state(self, M):
         st = self.state.get(M)
@@ -377,16 +381,19 @@ class _DeviceModel:
         else:
             self.trace[key] = rec
 
-    def _enqueue(self, M, pos_base, out_cap):
-        """Forward of the M tokens in ids[0:M] at position *pos; LM head + argmax of the last."""
+    def _enqueue(self, M, pos_base, out_cap, embed=True, next_h=None):
+        """Forward of the M tokens in ids[0:M] at position *pos; LM head + argmax of the last.
+        embed=False: h already holds the (one) token's embedding, written by the previous
+        forward's argmax (next_h = that h: the chosen token's embedding row is written there)."""
         hip, lib, ctx = self.hip, _hip.load(), self.hip.ctx
         st = self._state(M)
         tb = self._trace_bufs() if self.trace is not None else None
         h, q, k, v, o, g, u = st["h"], st["q"], st["k"], st["v"], st["o"], st["g"], st["u"]
         hip._bind_stream()
         chk = _hip.check
-        chk(lib.rt_embed(ctx, self.emb.data_ptr(), self.m.vocab_size, self.D, self.ids.data_ptr(), M, h.data_ptr()),
-            "rt_embed")
+        if embed:
+            chk(lib.rt_embed(ctx, self.emb.data_ptr(), self.m.vocab_size, self.D, self.ids.data_ptr(), M,
+                             h.data_ptr()), "rt_embed")
         eps = self.m.eps
         fused = M == 1
         for li, L in enumerate(self.layers):
@@ -442,7 +449,8 @@ class _DeviceModel:
         chk(lib.rt_lm_head_argmax(ctx, self.emb.data_ptr(), h[M - 1].data_ptr(), self.final_norm.data_ptr(), eps,
                                   self.m.vocab_size, self.D, self.logits.data_ptr(), self.best.data_ptr(),
                                   self.token.data_ptr(), self.pos.data_ptr(), M, self.ids.data_ptr(),
-                                  self.out_tokens.data_ptr(), pos_base, out_cap), "rt_lm_head_argmax")
+                                  self.out_tokens.data_ptr(), pos_base, out_cap,
+                                  next_h.data_ptr() if next_h is not None else None), "rt_lm_head_argmax")
         return st
 
     def layer_cache(self, li, length, epoch):
@@ -513,27 +521,30 @@ class _DeviceModel:
         self._state(P)
         if self.trace is not None:
             self._trace_bufs()  # before the capture (not in the graph's memory pool)
+        # every forward's argmax writes the chosen token's embedding into the decode input h,
+        # so the decode steps launch no embedding (embed_in_argmax)
+        h1 = self._state(1)["h"][0] if self.embed_in_argmax else None
+        emb1 = not self.embed_in_argmax
         g = None
         if n > 1 and graph:  # capture the decode step first (capture does not execute it)
-            self._state(1)
             torch.cuda.synchronize()
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                self._enqueue(1, pos_base=P - 1, out_cap=n)
+                self._enqueue(1, pos_base=P - 1, out_cap=n, embed=emb1, next_h=h1)
         self.ids[:P].copy_(torch.from_numpy(prompt))
         self.pos.fill_(0)
         self.best.zero_()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         rec = self._trace_record if self.trace is not None else (lambda key: None)
         ev[0].record()
-        self._enqueue(P, pos_base=P - 1, out_cap=n)            # prefill; out_tokens[0]
+        self._enqueue(P, pos_base=P - 1, out_cap=n, next_h=h1)  # prefill; out_tokens[0]
         rec("steps" if P == 1 else "prefill")
         ev[1].record()
         for _ in range(n - 1):
             if g is not None:
                 g.replay()
             else:
-                self._enqueue(1, pos_base=P - 1, out_cap=n)
+                self._enqueue(1, pos_base=P - 1, out_cap=n, embed=emb1, next_h=h1)
             rec("steps")
         ev[2].record()
         torch.cuda.synchronize()

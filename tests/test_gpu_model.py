@@ -417,7 +417,8 @@ def test_attach_attention_rejects_other_plans(hip):
 def test_lm_head_argmax(hip, V, D):
     """Fused final norm + bf16 LM head + argmax at the cfg-4 vocabulary and others: logits
     within 3e-4 + 1e-5 |ref| of the f64 head and equal to the kernel's fp32 order; the token
-    is the first index of the maximum; `best` is left zero."""
+    is the first index of the maximum; `best` is left zero; next_h receives the token's
+    embedding row."""
     import torch
 
     lib, chk = _lib()
@@ -430,13 +431,17 @@ def test_lm_head_argmax(hip, V, D):
     logits = torch.empty(V, device="cuda")
     best = torch.zeros(1, dtype=torch.int64, device="cuda")
     tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    next_h = torch.full((D,), float("nan"), device="cuda")
     hip._bind_stream()
-    for _ in range(2):  # `best` is left zero for the next call
+    for rep in range(2):  # `best` is left zero for the next call; the second writes next_h
         chk(lib.rt_lm_head_argmax(hip.ctx, Ed.data_ptr(), xd.data_ptr(), wd.data_ptr(), 1e-6, V, D, logits.data_ptr(),
-                                  best.data_ptr(), tok.data_ptr(), None, 0, None, None, 0, 0))
+                                  best.data_ptr(), tok.data_ptr(), None, 0, None, None, 0, 0,
+                                  next_h.data_ptr() if rep else None))
         lg = logits.cpu().numpy()
         assert int(tok.cpu()[0]) == int(np.argmax(lg))
         assert int(best.cpu()[0]) == 0
+    # the chosen token's embedding row, the next decode step's input
+    assert np.array_equal(next_h.cpu().numpy(), O.bf16_to_f32(E[int(np.argmax(lg))]))
     hn = O.rms_norm_f64acc(x[None], w)[0]
     E32 = O.bf16_to_f32(E)
     ref = E32.astype(np.float64) @ hn.astype(np.float64)

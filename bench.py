@@ -278,10 +278,13 @@ def decode_cfg4(torch, hip, gen, dev, n_layers=30, prompt_len=512, new_tokens=12
         "decode_weight_GB_per_s": round(per_tok_bytes * decode_tok_s / 1e9, 1),
         "decode_hbm_frac": round(per_tok_bytes * decode_tok_s / 1e9 / HBM_PEAK_GBS, 4),
         "prompt": prompt_len, "new_tokens": new_tokens, "layers": n_layers,
-        "first_tokens": [int(x) for x in toks[:8]],
-        "note": "random-init weights; decode step = one HIP graph replay (embedding, 30 x (norm+quant, qkv, "
-                "rope+kv, attention, sub-norm+quant, o+residual, norm+quant, gate/up, relu2+sub-norm+quant, "
-                "down+residual), fused final-norm LM head + argmax)",
+        "first_tokens": [int(x) for x in toks[:16]],
+        "distinct_tokens": int(len(set(int(x) for x in toks))),
+        "note": "random-init weights; decode step = one HIP graph replay (30 x (norm+quant, qkv, rope+kv, "
+                "attention partials + combine, sub-norm+quant, o+residual, norm+quant, gate/up, relu2+sub-norm+quant, "
+                "down+residual), fused final-norm LM head + argmax + next token's embedding).  Runs of one token are "
+                "the random-init tied-embedding model's own greedy fixed points (fed token t, t's logit is the "
+                "largest), held bit-exact against the oracle in tests/test_gpu_model.py",
     }
 
 

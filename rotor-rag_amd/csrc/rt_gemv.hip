@@ -327,8 +327,8 @@ constexpr int kAttnMaxThreads = 640;
 // a = relu(g)^2 * u of those 32 (g and u rounded as emit rounds y) and their f64 sum of
 // squares, the two inputs of the down projection's sub-norm.
 // Tail = AttnTail (M = 1, fp32 outputs): the attention partials of the token run in the
-// same launch (qkv_attn_block): the GEMV's outputs are stored device-coherent and, once
-// they are written, the workgroup adds one to the arrival count of its KV group.
+// same launch (qkv_attn_block): the GEMV's outputs are also stored as epoch-tagged
+// device-coherent words, which the attention workgroups poll.
 struct NoTail {};
 template <int HD>
 __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb);

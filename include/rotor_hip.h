@@ -261,19 +261,21 @@ int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, fl
 int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, const float* rope, int H, int Hkv,
                              int hd, int Lmax, const int* pos, void* workspace, size_t workspace_bytes);
 /* Let a q/k/v plan with the attention attached also finish the attention in its launch:
- * the last attention workgroup of each KV group combines that group's partials (as
- * rt_attention_decode_combine does, same values) into out fp32 [H*hd] (device, 16-byte
- * aligned) and writes, per 32 consecutive outputs, the f64 sum of their squares into
- * ssq [H*hd/32] (device): the x and aux2 of an RT_SRC_RMSNORM_SSQ plan for o_proj, which
- * then needs neither the partials nor a reduction of its own.  At most 10 key blocks
- * (Lmax <= 640).  NULL, NULL detaches (o_proj then reads the partials: RT_SRC_ATTN_NORM).
+ * the attention workgroups of each KV group share the combine of that group's partials (as
+ * rt_attention_decode_combine does, same values; each reads its peers' partials from
+ * (epoch, value) words, a bounded wait) into out fp32 [H*hd] (device, 16-byte aligned) and
+ * write, per 32 consecutive outputs, the f64 sum of their squares into ssq [H*hd/32]
+ * (device): the x and aux2 of an RT_SRC_RMSNORM_SSQ plan for o_proj, which then needs
+ * neither the partials nor a reduction of its own.  At most 10 key blocks (Lmax <= 640), and
+ * the device must hold all of the launch's workgroups at once (RT_EINVAL otherwise).
+ * NULL, NULL detaches (o_proj then reads the partials: RT_SRC_ATTN_NORM).
  * Replaces, for one token, src/rotor/transformer.py:268-281 (softmax and the weighted sum of
  * the values) and the sum of squares of the sub-norm that follows them. */
 int rt_plan_attention_combine(rt_plan* plan, float* out, double* ssq);
 /* Number of attention waits of the plan's launches that gave up (never expected; the
  * results of such a launch are wrong).  Synchronises the device; a non-zero count also
- * resets the plan's hand-off state (tagged outputs and epoch).  No counterpart in the
- * reference (its attention runs after the projections on the host). */
+ * resets the plan's hand-off state (tagged words and the count the epoch follows from).
+ * No counterpart in the reference (its attention runs after the projections on the host). */
 int rt_plan_attention_timeouts(rt_plan* plan, int* count);
 
 /* ---- kernels around the linears for BitNet-2B-shape inference ----------------------

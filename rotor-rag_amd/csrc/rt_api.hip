@@ -1251,12 +1251,10 @@ int rt_plan_create_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, fl
     return RT_OK;
 }
 
-// The device state of the attention partials in a qkv launch: the tagged outputs (zero),
-// then the epoch (1), the done count and the error count (0).
+// The device state of the attention partials in a qkv launch: the tagged words, the done
+// count (epoch 1) and the error count, all zero.
 static hipError_t attention_state_reset(rt_plan* plan) {
     hipError_t e = hipMemset(plan->att_mem, 0, plan->att_bytes);
-    const unsigned one = 1;
-    if (e == hipSuccess) e = hipMemcpy(plan->att.epoch, &one, sizeof(one), hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     return e;
 }
@@ -1290,8 +1288,10 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
         return fail(RT_EINVAL, std::string(who) + ": the plan's source must be a 16-byte aligned row with K % 64 == 0");
     DeviceGuard g(plan->device);
     const size_t words = (size_t)(H + 2 * Hkv) * hd;
-    // the tagged outputs, then epoch, done, err (16 bytes) and the KV groups' arrival counts
-    const size_t bytes = words * sizeof(unsigned long long) + 256 + (size_t)Hkv * sizeof(int);
+    const size_t pwords = (size_t)H * attn_splits(Lmax) * (hd + 2);
+    // the tagged outputs, the tagged partials (for rt_plan_attention_combine), then done and
+    // err
+    const size_t bytes = (words + pwords) * sizeof(unsigned long long) + 256;
     // a launch of this plan may still be in flight on the caller's stream: wait for it
     // before the hand-off state is freed or reset
     if (plan->att_mem) RT_HIP(hipDeviceSynchronize());
@@ -1303,11 +1303,10 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
     plan->att_bytes = bytes;
     AttnTail& t = plan->att;
     t.tagged = static_cast<unsigned long long*>(plan->att_mem);
-    int* tail = reinterpret_cast<int*>(t.tagged + words);
-    t.epoch = reinterpret_cast<unsigned*>(tail);
-    t.done = tail + 1;
-    t.err = tail + 2;
-    t.gdone = tail + 4;
+    t.ptag = t.tagged + words;
+    int* tail = reinterpret_cast<int*>(t.ptag + pwords);
+    t.done = reinterpret_cast<unsigned*>(tail);
+    t.err = tail + 1;
     t.out = nullptr;  // rt_plan_attention_combine attaches the combine
     t.ssq = nullptr;
     RT_HIP(attention_state_reset(plan));
@@ -1319,6 +1318,7 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
     t.Gq = Gq;
     t.Lmax = Lmax;
     t.S = attn_splits(Lmax);
+    t.natt = (unsigned)(Hkv * t.S);
     t.qrows = H * hd;
     t.nkv = Hkv * hd;
     t.scale = 1.0f / sqrtf((float)hd);
@@ -1340,6 +1340,19 @@ int rt_plan_attention_combine(rt_plan* plan, float* out, double* ssq) {
                                        " key blocks (Lmax <= " + std::to_string(64 * kAttnSMax) + ")");
         if (((uintptr_t)out & 15u) || ((uintptr_t)ssq & 7u))
             return fail(RT_EINVAL, std::string(who) + ": out must be 16-byte and ssq 8-byte aligned");
+        // the workgroups of a KV group wait for each other's partials: every workgroup of the
+        // launch must be resident at once, and a workgroup's chunks of 32 outputs must fit it
+        const int NC = plan->att.Gq * plan->att_hd / 32, S = plan->att.S;
+        if (32 * ((NC + S - 1) / S) > 64 * plan->shape.nw)
+            return fail(RT_EINVAL, std::string(who) + ": too few key blocks for the group's outputs");
+        DeviceGuard g(plan->device);
+        int resident = 0;
+        RT_HIP(gemv_attn_capacity(plan->pro.K, plan->pro.Kp, plan->shape.nw, plan->att.Gq, &resident));
+        if (plan->total_rb + plan->att_Hkv * S > resident)
+            return fail(RT_EINVAL, std::string(who) + ": the launch's " +
+                                       std::to_string(plan->total_rb + plan->att_Hkv * S) +
+                                       " workgroups exceed the " + std::to_string(resident) +
+                                       " the device holds at once");
     }
     DeviceGuard g(plan->device);
     // a launch of this plan may still be in flight on the caller's stream

@@ -9,9 +9,9 @@
 // The tile (h, s) handles keys [64 s, 64 s + 64) of query head h for the single query at
 // position pos and writes a partial result wp[0..HD+2): the unnormalised output
 // sum_j e^(s_j - m) V_j (HD values), the block maximum m and the sum of exponentials z
-// (m = -inf, z = 0 for an empty block).  The partials are combined by attn_combine_kernel
-// or by the prologue of the o_proj GEMV (rt_rowquant.h, kAttnNorm); both use
-// attn_combine_element, so the two give identical values.
+// (m = -inf, z = 0 for an empty block).  The partials are combined by attn_combine_kernel,
+// by the prologue of the o_proj GEMV (rt_rowquant.h, kAttnNorm) or in the qkv launch; all
+// use the operation order of attn_combine_element, so they give identical values.
 #pragma once
 
 #include "rt_internal.h"
@@ -92,22 +92,22 @@ __device__ __forceinline__ void attn_rope_load(const float* __restrict__ rope, i
 // summation order, and, when `writer` (the first query head of its KV group), writes them
 // into the caches of KV head kh for the later steps.  Without ROPE, qh is already rotated
 // and the caches hold the new key.
-// A partial's value: a plain store, or (COH) a device-coherent one, for a reader in another
-// workgroup of the same launch.
-template <bool COH>
-__device__ __forceinline__ void part_store(float* p, float v) {
-    if constexpr (COH)
-        __hip_atomic_store(reinterpret_cast<unsigned*>(p), __float_as_uint(v), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    else
-        *p = v;
+// Value i of a partial: a plain store to wp, and (TAG, wt not null) a copy as the 64-bit
+// word tag | bits(v) to wt, device-coherent, for readers in other workgroups of the same
+// launch (tag = epoch << 32).
+template <bool TAG>
+__device__ __forceinline__ void part_store(float* wp, unsigned long long* wt, unsigned long long tag, int i,
+                                           float v) {
+    wp[i] = v;
+    if constexpr (TAG)
+        if (wt) __hip_atomic_store(wt + i, tag | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int HD, bool ROPE, bool COH = false, typename SRC>
+template <int HD, bool ROPE, bool TAG = false, typename SRC>
 __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float sn, float* __restrict__ Kc,
                                           float* __restrict__ Vc, int kh, bool writer, int Lmax, int pos, int j0,
-                                          float scale, float* __restrict__ wp, int t, AttnLdsPtr<HD> sm,
-                                          const AttnKV<HD>& kv) {
+                                          float scale, float* __restrict__ wp, unsigned long long* __restrict__ wt,
+                                          unsigned long long tag, int t, AttnLdsPtr<HD> sm, const AttnKV<HD>& kv) {
 #pragma clang fp contract(off)  // every product and sum rounds on its own
     static_assert(HD / 2 <= 256, "one rotation pair per thread");
     using KV = AttnKV<HD>;
@@ -170,8 +170,8 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
         const float z = wave_reduce63(p, 0.0f, [](float x, float y) { return x + y; });
         sm->pr[lane] = p;
         if (lane == 63) {
-            part_store<COH>(wp + HD, mx);
-            part_store<COH>(wp + HD + 1, z);
+            part_store<TAG>(wp, wt, tag, HD, mx);
+            part_store<TAG>(wp, wt, tag, HD + 1, z);
         }
     }
     attn_lds_barrier();
@@ -218,17 +218,23 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
     if (g == 0) {
         float o = sm->ored[d];
         for (int gg = 1; gg < G; ++gg) o += sm->ored[gg * HD + d];
-        part_store<COH>(wp + d, o);
+        part_store<TAG>(wp, wt, tag, d, o);
     }
 }
 
-// The partial of an empty block (no key at or before the position).
-template <int HD, bool COH = false>
-__device__ __forceinline__ void attn_tile_empty(float* __restrict__ wp, int t) {
+// The partial of an empty block (no key at or before the position): m = -inf, z = 0; with
+// TAG every word of the tagged copy is written (the values as 0), so a reader can wait for
+// all of them.
+template <int HD, bool TAG = false>
+__device__ __forceinline__ void attn_tile_empty(float* __restrict__ wp, unsigned long long* __restrict__ wt,
+                                                unsigned long long tag, int t) {
     if (t == 0) {
-        part_store<COH>(wp + HD, -INFINITY);
-        part_store<COH>(wp + HD + 1, 0.0f);
+        part_store<TAG>(wp, wt, tag, HD, -INFINITY);
+        part_store<TAG>(wp, wt, tag, HD + 1, 0.0f);
     }
+    if constexpr (TAG)
+        if (wt)
+            for (int d = t; d < HD; d += 256) __hip_atomic_store(wt + d, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace rt

@@ -332,6 +332,10 @@ constexpr int kAttnMaxThreads = 640;
 struct NoTail {};
 template <int HD>
 __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb);
+// The launch's epoch (AttnTail): *done / natt + 1, the same for every workgroup of a launch.
+__device__ __forceinline__ unsigned attn_epoch(const AttnTail& at) {
+    return __hip_atomic_load(at.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) / at.natt + 1u;
+}
 template <int MT, int PRO, bool PAIR = false, typename Tail = NoTail>
 __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     gemv_ksplit_kernel(const float* pro_x, const float* pro_aux, const float* pro_aux2, int pro_K, int pro_mode,
@@ -437,7 +441,7 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
     unsigned long long tag = 0;
     if constexpr (SIG) {
         tagged = at.tagged + (size_t)blockIdx.x * kRowBlock;
-        tag = (unsigned long long)__hip_atomic_load(at.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) << 32;
+        tag = (unsigned long long)attn_epoch(at) << 32;
         asm volatile("" ::"s"(tagged), "s"(tag));
     }
     float sx_pro = -1.0f;
@@ -531,59 +535,66 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
 // the values in LDS, and the tiles of rt_attn_decode.h run on them.  Forward
 // progress: the attention workgroups wait only for GEMV workgroups, which come first in
 // the grid and never wait.
-// The last attention workgroup of KV group kh to finish combines the group's partials
-// (every block of its Gq heads) into at.out, in the operation order of
-// attn_combine_element, and writes per 32 outputs the f64 sum of their squares into at.ssq
-// (the input of an RMSNORM_SSQ prologue).  The partials are stored device-coherent; every
-// workgroup waits for its own stores, then adds one to the group's arrival count; the last
-// arriver resets the count and reads the others' partials device-coherent (the hand-off of
-// the split-K GEMM's parts).  flag: an int of the workgroup's LDS no tile uses any more.
+// With rt_plan_attention_combine (at.out set) the S attention workgroups of KV group kh
+// share the group's combine: workgroup s takes the chunks of 32 outputs s, s + S, ..
+// (< Gq HD / 32), one output per thread (chunk i on threads [32 i, 32 i + 32): the host
+// allows the combine where they fit the workgroup).  A thread reads its output's partial value and the
+// (m, z) of every block of its head from the tagged copies, polling (bounded) until every
+// word carries the launch's epoch, combines them in the operation order of
+// attn_combine_element and writes the output and, per chunk, the f64 sum of the squares of
+// its 32 outputs (for an RMSNORM_SSQ prologue).  A workgroup waits only for its peers'
+// partials, which every peer stores before any wait of its own; the host allows the combine
+// only when the device holds the whole grid at once.
 template <int HD>
-__device__ __forceinline__ void attn_group_combine(const AttnTail& at, int kh, __attribute__((address_space(3))) int* flag) {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    if (threadIdx.x == 0) {
-        const int prev = __hip_atomic_fetch_add(at.gdone + kh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const bool last = prev == at.S - 1;
-        if (last) __hip_atomic_store(at.gdone + kh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = last ? 1 : 0;
-    }
-    attn_lds_barrier();
-    if (!*flag) return;
-    const int sub = (int)(threadIdx.x >> 8), t = (int)(threadIdx.x & 255), h = kh * at.Gq + sub, S = at.S;
-    if (t >= HD) return;  // (HD % 64 == 0: whole waves) no barrier follows
-    const unsigned* wh = reinterpret_cast<const unsigned*>(at.work + (size_t)h * S * (HD + 2));
-    auto ld = [](const unsigned* p) {
-        return __uint_as_float(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+__device__ __forceinline__ void attn_peer_combine(const AttnTail& at, int kh, int s, unsigned ep) {
+    const int S = at.S, NC = at.Gq * HD / 32;
+    const int t = (int)threadIdx.x;
+    if (s + 2 * (t >> 6) * S >= NC) return;  // waves past the workgroup's chunks (no barrier follows)
+    const int c = s + (t >> 5) * S;
+    const bool act = c < NC;  // lanes of a chunk past the group re-read the last one's words
+    const int e = min(c, NC - 1) * 32 + (t & 31);
+    const int hg = e / HD, d = e % HD, h = kh * at.Gq + hg;
+    const unsigned long long* ph = at.ptag + (size_t)h * S * (HD + 2);
+    auto ld = [](const unsigned long long* q) {
+        return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
-    // every load at once (blocks past S re-read block S - 1 and are ignored)
     float m[kAttnSMax], z[kAttnSMax], p[kAttnSMax];
+    for (unsigned it = 0;; ++it) {
+        bool ok = true;
 #pragma unroll
-    for (int s = 0; s < kAttnSMax; ++s) {
-        const unsigned* ps = wh + (size_t)min(s, S - 1) * (HD + 2);
-        p[s] = ld(ps + t);
-        m[s] = ld(ps + HD);
-        z[s] = ld(ps + HD + 1);
+        for (int sb = 0; sb < kAttnSMax; ++sb) {  // blocks past S re-read block S - 1
+            const unsigned long long* q = ph + (size_t)min(sb, S - 1) * (HD + 2);
+            const unsigned long long wv = ld(q + d), wm = ld(q + HD), wz = ld(q + HD + 1);
+            ok &= (unsigned)(wv >> 32) == ep && (unsigned)(wm >> 32) == ep && (unsigned)(wz >> 32) == ep;
+            p[sb] = __uint_as_float((unsigned)wv);
+            m[sb] = __uint_as_float((unsigned)wm);
+            z[sb] = __uint_as_float((unsigned)wz);
+        }
+        if (__all(ok)) break;
+        if (it >= kAttnSpinLimit) {  // never expected: counted, and the launch goes on
+            if (t == 0) __hip_atomic_fetch_add(at.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < kAttnSMax; ++s)
-        if (s < S) mx = fmaxf(mx, m[s]);
+    for (int sb = 0; sb < kAttnSMax; ++sb)
+        if (sb < S) mx = fmaxf(mx, m[sb]);
     float num = 0.0f, den = 0.0f;
 #pragma unroll
-    for (int s = 0; s < kAttnSMax; ++s) {
-        if (s >= S || m[s] == -INFINITY) continue;
-        const float f = expf(m[s] - mx);
-        num = fmaf(f, p[s], num);
-        den = fmaf(f, z[s], den);
+    for (int sb = 0; sb < kAttnSMax; ++sb) {
+        if (sb >= S || m[sb] == -INFINITY) continue;
+        const float f = expf(m[sb] - mx);
+        num = fmaf(f, p[sb], num);
+        den = fmaf(f, z[sb], den);
     }
     const float o = num / den;
-    const int k = h * HD + t;
-    at.out[k] = o;
+    const int k = h * HD + d;
+    if (act) at.out[k] = o;
     // lanes 0..31 and 32..63 of the wave: 32 consecutive outputs each
     const double ss = half_reduce31((double)o * (double)o, 0.0, [](double x, double y) { return x + y; });
-    if ((t & 31) == 31) at.ssq[k >> 5] = ss;
+    if (act && (t & 31) == 31) at.ssq[k >> 5] = ss;
 }
 
 template <int HD>
@@ -599,9 +610,12 @@ __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb)
     const int nin = (at.Gq + 2) * HD;
     AttnKV<HD> kv;
     attn_kv_load<HD>(at.Kc, at.Vc, kh, j0, at.Lmax, t, kv);
-    const unsigned ep = __hip_atomic_load(at.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned ep = attn_epoch(at);
     const int pos = *at.pos;
     float* wp = at.work + ((size_t)h * at.S + s) * (HD + 2);
+    // with the combine in this launch the partials are also stored as tagged words
+    unsigned long long* wt = at.out ? at.ptag + ((size_t)h * at.S + s) * (HD + 2) : nullptr;
+    const unsigned long long tag = (unsigned long long)ep << 32;
     const bool live = pos >= j0;
     if (live) {
         float c, sn;
@@ -626,18 +640,14 @@ __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb)
         }
         __syncthreads();
         attn_tile<HD, true, true>(qkv + sub * HD, qkv + at.Gq * HD, qkv + (at.Gq + 1) * HD, c, sn, at.Kc, at.Vc,
-                                  kh, sub == 0, at.Lmax, pos, j0, at.scale, wp, t, sm + sub, kv);
+                                  kh, sub == 0, at.Lmax, pos, j0, at.scale, wp, wt, tag, t, sm + sub, kv);
     } else {
-        attn_tile_empty<HD, true>(wp, t);
+        attn_tile_empty<HD, true>(wp, wt, tag, t);
     }
-    if (at.out) attn_group_combine<HD>(at, kh, (__attribute__((address_space(3))) int*)qkv);
-    // the last attention workgroup of the launch (every other one is past its reads) resets
-    // the count and advances the epoch
-    if (threadIdx.x == 0 &&
-        __hip_atomic_fetch_add(at.done, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - total_rb - 1) {
-        __hip_atomic_store(at.done, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(at.epoch, ep + 1 == 0 ? 1u : ep + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (at.out) attn_peer_combine<HD>(at, kh, s, ep);
+    // this workgroup is past its reads of the launch's tagged words: count it (the epoch of
+    // the next launch follows from the count; no result to wait for)
+    if (threadIdx.x == 0) (void)__hip_atomic_fetch_add(at.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 GemvShape gemv_shape_fused(int total_rb, int min_C) {
@@ -796,5 +806,23 @@ hipError_t launch_gemv_attn(const GemvArgs& args, const AttnTail& at, int Hkv, i
     else launch_qkv_attn<6>(grid, nw, lds, s, a, at);
     return hipGetLastError();
 }
+
+hipError_t gemv_attn_capacity(int K, int Kp, int nw, int Gq, int* workgroups) {
+    *workgroups = 0;
+    const int E = K % 64 == 0 ? vec_elements(K, 64 * nw) : 0;
+    if (E == 0) return hipErrorInvalidValue;
+    const size_t lds = std::max((size_t)nw * kRowBlock * sizeof(int) + (size_t)Kp + sizeof(RowSmem),
+                                (size_t)Gq * sizeof(AttnTileLds<128>) + (size_t)(Gq + 2) * 128 * sizeof(float));
+    const void* k = E == 4   ? reinterpret_cast<const void*>(&gemv_ksplit_kernel<1, 3, false, AttnTail>)
+                    : E == 8 ? reinterpret_cast<const void*>(&gemv_ksplit_kernel<1, 4, false, AttnTail>)
+                             : reinterpret_cast<const void*>(&gemv_ksplit_kernel<1, 6, false, AttnTail>);
+    int per_cu = 0, dev = 0, cus = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, 64 * nw, lds);
+    if (e == hipSuccess) e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) *workgroups = per_cu * cus;
+    return e;
+}
+
 
 }  // namespace rt

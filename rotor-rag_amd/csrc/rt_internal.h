@@ -153,16 +153,20 @@ struct GemvArgs {
 // Attention partials in the qkv GEMV's launch (gemv_ksplit_kernel with an AttnTail): the
 // GEMV workgroups also store every output y of the q, k and v problems (concatenated, row
 // n of the launch at index n) as tagged[n] = epoch << 32 | bits(y), a 64-bit
-// device-coherent store; the Hkv * S attention workgroups read the epoch at their start and
-// poll their group's q, k and v words until every one carries it (bounded; err counts the
-// waits that gave up, never expected).  Each attention workgroup counts itself in *done;
-// the last one resets *done and advances *epoch, so the next launch's tags differ.
+// device-coherent store; the natt = Hkv * S attention workgroups poll their group's q, k and
+// v words until every one carries the epoch (bounded; err counts the waits that gave up,
+// never expected).  Each attention workgroup adds one to *done when it has finished, without
+// waiting for the result, and a launch's epoch is *done / natt + 1, read by every workgroup
+// at its start: the count grows by natt per launch and reaches the next multiple only when
+// every attention workgroup of the launch has finished, after every workgroup read it (the
+// GEMV workgroups before storing the outputs all attention workgroups wait for), so the
+// epoch is the same throughout a launch and the next launch's tags differ.
 constexpr unsigned kAttnSpinLimit = 1u << 18;
 struct AttnTail {
     unsigned long long* tagged;  // [H hd + 2 Hkv hd]
-    unsigned* epoch;             // [1], >= 1
-    int* done;                   // [1]
+    unsigned* done;              // [1]
     int* err;                    // [1]
+    unsigned natt;               // Hkv S
     float* Kc;                   // [Hkv][hd][Lmax]
     float* Vc;                   // [Hkv][Lmax][hd]
     const float* rope;
@@ -171,13 +175,14 @@ struct AttnTail {
     int Gq, Lmax, S, nkv;        // nkv = Hkv hd: where k starts after q (H hd), v after k
     int qrows;                   // H hd
     float scale;
-    // rt_plan_attention_combine (out != nullptr, S <= kAttnSMax): the last attention
-    // workgroup of KV group kh to finish (gdone [Hkv] arrival counts, reset by it) combines
-    // the group's partials into out [H hd] and writes per 32 outputs the f64 sum of their
-    // squares into ssq [H hd / 32]
+    // rt_plan_attention_combine (out != nullptr, S <= kAttnSMax): the attention workgroups
+    // also store their partials as tagged words ptag [H][S][hd + 2] (epoch << 32 | bits),
+    // and the S workgroups of KV group kh share its combine: each polls the partials of its
+    // share of the group's outputs, combines them into out [H hd] and writes per 32 outputs
+    // the f64 sum of their squares into ssq [H hd / 32]
     float* out;
     double* ssq;
-    int* gdone;
+    unsigned long long* ptag;
 };
 
 struct GemvShape {
@@ -340,6 +345,9 @@ hipError_t launch_gemm_tiles(const GemmArgs* dev, const int* tile2p, int total_t
 // workgroup) with the attention partials of its token in the same launch.
 hipError_t launch_gemv_attn(const GemvArgs& args, const AttnTail& at, int Hkv, int hd, GemvShape shape,
                             hipStream_t s);
+// Workgroups of that launch (source row of K elements, nw waves, Gq query heads per KV head)
+// that the current device holds at once.
+hipError_t gemv_attn_capacity(int K, int Kp, int nw, int Gq, int* workgroups);
 hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, int total_rb, hipStream_t s);
 // Once per device (current) before any launch: the function attributes the GEMM kernels
 // and the prefill attention need (dynamic LDS above 64 KiB).

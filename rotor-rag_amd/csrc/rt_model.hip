@@ -321,14 +321,14 @@ __global__ void __launch_bounds__(256) attn_partial_kernel(const float* __restri
     const int pos = *pos_p;
     float* wp = work + ((size_t)h * S + s) * (HD + 2);
     if (pos < j0) {
-        attn_tile_empty<HD>(wp, t);
+        attn_tile_empty<HD>(wp, nullptr, 0ull, t);
         return;
     }
     float c = 0.0f, sn = 0.0f;
     if (ROPE) attn_rope_load<HD>(rope, pos, t, c, sn);
     attn_tile<HD, ROPE>(q + (size_t)h * HD, ROPE ? knew + (size_t)kh * HD : nullptr,
                         ROPE ? vnew + (size_t)kh * HD : nullptr, c, sn, Kc, Vc, kh, h % Gq == 0, Lmax, pos, j0, scale,
-                        wp, t, (AttnLdsPtr<HD>)&sm, kv);
+                        wp, nullptr, 0ull, t, (AttnLdsPtr<HD>)&sm, kv);
 }
 
 // out[h*hd + d] from the S partials of head h (one thread per output element)

@@ -277,13 +277,15 @@ def test_qkv_plan_with_attention_equals_separate_launches(hip, pos0, Lmax):
     in the GEMV's launch) gives the q, k, v outputs, the partials and the caches of the plan
     followed by rt_rope_attention_decode, bit for bit.  The hand-off: the GEMV also stores
     every q/k/v output as a 64-bit word (epoch << 32 | value bits), the attention workgroups
-    poll those words until they carry the launch's epoch, and the launch's last attention
-    workgroup advances the epoch.  Checked on two runs in a row and on every replay of a
-    captured graph, each with a new input row: a launch whose epoch did not advance would
-    let the attention start on the previous launch's q/k/v and its partials would differ.
-    No wait gives up.  Where Lmax <= 640 the launch also combines the partials
-    (rt_plan_attention_combine): its output equals rt_attention_decode_combine's on the
-    reference partials bit for bit, and its per-32 sums of squares the f64 sums."""
+    poll those words until they carry the launch's epoch, and the epoch follows from a count
+    of finished attention workgroups, so it advances with every launch.  Checked on two runs
+    in a row and on every replay of a captured graph, each with a new input row: a launch
+    whose epoch did not advance would let the attention start on the previous launch's
+    q/k/v and its partials would differ.  No wait gives up.  Where Lmax <= 640 the launch
+    also combines the partials (rt_plan_attention_combine: the workgroups of a KV group
+    share it, reading each other's partials as tagged words): its output equals
+    rt_attention_decode_combine's on the reference partials bit for bit, and its per-32 sums
+    of squares the f64 sums."""
     import torch
 
     from oracle.rotor_oracle import rope_table

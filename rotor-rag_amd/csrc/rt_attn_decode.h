@@ -108,7 +108,7 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
                                           float* __restrict__ Vc, int kh, bool writer, int Lmax, int pos, int j0,
                                           float scale, float* __restrict__ wp, unsigned long long* __restrict__ wt,
                                           unsigned long long tag, int t, AttnLdsPtr<HD> sm, const AttnKV<HD>& kv) {
-#pragma clang fp contract(off)  // every product and sum rounds on its own
+#pragma clang fp contract(off)  // every operation rounds on its own, fmaf where written
     static_assert(HD / 2 <= 256, "one rotation pair per thread");
     using KV = AttnKV<HD>;
     constexpr int BL = kAttnBlock, half = HD / 2, G = KV::G, KD = KV::KD, VN = KV::VN;
@@ -154,10 +154,10 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
 #pragma unroll
     for (int i = 0; i < KD; i += 4) {
         const int dd = wave * KD + i;
-        a0 += sm->qs[dd + 0] * kk[i + 0];
-        a1 += sm->qs[dd + 1] * kk[i + 1];
-        a2 += sm->qs[dd + 2] * kk[i + 2];
-        a3 += sm->qs[dd + 3] * kk[i + 3];
+        a0 = fmaf(sm->qs[dd + 0], kk[i + 0], a0);
+        a1 = fmaf(sm->qs[dd + 1], kk[i + 1], a1);
+        a2 = fmaf(sm->qs[dd + 2], kk[i + 2], a2);
+        a3 = fmaf(sm->qs[dd + 3], kk[i + 3], a3);
     }
     sm->part[wave][lane] = (a0 + a1) + (a2 + a3);
     attn_lds_barrier();
@@ -176,7 +176,7 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
     }
     attn_lds_barrier();
     // unnormalised output: thread (d, g) sums keys g, g + G, ... of the block, two
-    // alternating partial sums.  The new key's value and the mask of keys past the
+    // alternating partial sums of fused multiply-adds (as the scores' four).  The new key's value and the mask of keys past the
     // position cost VALU work only where they apply: four tiles share a CU in the qkv
     // launch, where this loop is VALU-bound.  The keys go in runs of CH; g is uniform
     // over a wave and nk over the workgroup, so a run lies wholly before nk (plain sums),
@@ -200,14 +200,14 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
         if (last < nk) {
 #pragma unroll
             for (int i = c0; i < c0 + CH; i += 2) {
-                o0 += sm->pr[g + i * G] * vv[i];
-                o1 += sm->pr[g + (i + 1) * G] * vv[i + 1];
+                o0 = fmaf(sm->pr[g + i * G], vv[i], o0);
+                o1 = fmaf(sm->pr[g + (i + 1) * G], vv[i + 1], o1);
             }
         } else if (first < nk) {
 #pragma unroll
             for (int i = c0; i < c0 + CH; i += 2) {
                 const int ja = g + i * G, jb = g + (i + 1) * G;
-                const float sa = o0 + sm->pr[ja] * vv[i], sb = o1 + sm->pr[jb] * vv[i + 1];
+                const float sa = fmaf(sm->pr[ja], vv[i], o0), sb = fmaf(sm->pr[jb], vv[i + 1], o1);
                 o0 = ja < nk ? sa : o0;
                 o1 = jb < nk ? sb : o1;
             }

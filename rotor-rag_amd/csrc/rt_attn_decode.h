@@ -89,8 +89,8 @@ __device__ __forceinline__ void attn_rope_load(const float* __restrict__ rope, i
 // ROPE: qh, kn, vn are the raw projection outputs of the token at pos.  The tile rotates
 // its head's q (the arithmetic of rope_append_kernel); the tile whose block holds position
 // pos takes that key and value from LDS (rotated kn, vn) instead of the cache, in the same
-// summation order, and, when `writer` (the first query head of its KV group), writes them
-// into the caches of KV head kh for the later steps.  Without ROPE, qh is already rotated
+// summation order, and, when `writer` (one query head of its KV group), writes them into
+// the caches of KV head kh for the later steps, once its partial is stored.  Without ROPE, qh is already rotated
 // and the caches hold the new key.
 // Value i of a partial: a plain store to wp, and (TAG, wt not null) a copy as the 64-bit
 // word tag | bits(v) to wt, device-coherent, for readers in other workgroups of the same
@@ -134,11 +134,6 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
         for (int e = t; e < HD; e += 256) sm->qs[e] = qh[e];
     }
     attn_lds_barrier();
-    if (holds_new && writer)  // one writer per KV head
-        for (int e = t; e < HD; e += 256) {
-            Kc[((size_t)kh * HD + e) * Lmax + pos] = sm->ks[e];
-            Vc[((size_t)kh * Lmax + pos) * HD + e] = sm->vs[e];
-        }
     // scores: wave w sums its dims for key j0 + lane (the new key from LDS: the one lane
     // that holds it takes its dims first, in a branch that every other wave skips).
     // Branch-free otherwise: every lane computes (keys past the block's last are discarded
@@ -220,6 +215,13 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
         for (int gg = 1; gg < G; ++gg) o += sm->ored[gg * HD + d];
         part_store<TAG>(wp, wt, tag, d, o);
     }
+    // the new key and value into the caches of KV head kh (one writer tile per KV head),
+    // after the partial: only later steps read them, and nothing here waits for the stores
+    if (holds_new && writer)
+        for (int e = t; e < HD; e += 256) {
+            Kc[((size_t)kh * HD + e) * Lmax + pos] = sm->ks[e];
+            Vc[((size_t)kh * Lmax + pos) * HD + e] = sm->vs[e];
+        }
 }
 
 // The partial of an empty block (no key at or before the position): m = -inf, z = 0; with

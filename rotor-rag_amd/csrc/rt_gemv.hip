@@ -640,7 +640,7 @@ __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb)
         }
         __syncthreads();
         attn_tile<HD, true, true>(qkv + sub * HD, qkv + at.Gq * HD, qkv + (at.Gq + 1) * HD, c, sn, at.Kc, at.Vc,
-                                  kh, sub == 0, at.Lmax, pos, j0, at.scale, wp, wt, tag, t, sm + sub, kv);
+                                  kh, sub == at.Gq - 1, at.Lmax, pos, j0, at.scale, wp, wt, tag, t, sm + sub, kv);
     } else {
         attn_tile_empty<HD, true>(wp, wt, tag, t);
     }

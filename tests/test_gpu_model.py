@@ -271,7 +271,11 @@ def test_rope_attention_decode_equals_separate_launches(hip, pos0, H, Hkv, hd, L
     assert torch.equal(ws, ws_ref)
 
 
-@pytest.mark.parametrize("pos0,Lmax", [(0, 640), (63, 640), (64, 640), (639, 640), (1000, 2048)])
+# Lmax 640: 10 key blocks, each workgroup combines 2 of a KV group's 16 chunks of 32 outputs;
+# 256 / 192 / 64: 4 / 3 / 1 blocks, 4 / 6 (the last one past the group) / 16 chunks per
+# workgroup on several waves; 2048: no combine in the launch
+@pytest.mark.parametrize("pos0,Lmax", [(0, 640), (63, 640), (64, 640), (639, 640), (1000, 2048), (10, 256), (100, 192),
+                                       (0, 64), (63, 64)])
 def test_qkv_plan_with_attention_equals_separate_launches(hip, pos0, Lmax):
     """The q/k/v decode plan with the attention attached (RoPE + KV append + split-L partials
     in the GEMV's launch) gives the q, k, v outputs, the partials and the caches of the plan

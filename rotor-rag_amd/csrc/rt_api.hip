@@ -1319,6 +1319,7 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
     t.Lmax = Lmax;
     t.S = attn_splits(Lmax);
     t.natt = (unsigned)(Hkv * t.S);
+    t.wrap = t.natt * (0xFFFFFFFFu / t.natt) - 1u;
     t.qrows = H * hd;
     t.nkv = Hkv * hd;
     t.scale = 1.0f / sqrtf((float)hd);

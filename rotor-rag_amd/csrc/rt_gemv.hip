@@ -647,7 +647,7 @@ __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb)
     if (at.out) attn_peer_combine<HD>(at, kh, s, ep);
     // this workgroup is past its reads of the launch's tagged words: count it (the epoch of
     // the next launch follows from the count; no result to wait for)
-    if (threadIdx.x == 0) (void)__hip_atomic_fetch_add(at.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) (void)__builtin_amdgcn_atomic_inc32(at.done, at.wrap, __ATOMIC_RELAXED, "agent");
 }
 
 GemvShape gemv_shape_fused(int total_rb, int min_C) {

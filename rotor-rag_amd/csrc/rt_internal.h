@@ -160,13 +160,17 @@ struct GemvArgs {
 // at its start: the count grows by natt per launch and reaches the next multiple only when
 // every attention workgroup of the launch has finished, after every workgroup read it (the
 // GEMV workgroups before storing the outputs all attention workgroups wait for), so the
-// epoch is the same throughout a launch and the next launch's tags differ.
+// epoch is the same throughout a launch and the next launch's tags differ.  The count wraps
+// to 0 after wrap (a wrapping increment), wrap + 1 being the largest multiple of natt below
+// 2^32, so every launch starts on a multiple of natt; epochs repeat only after
+// (wrap + 1) / natt launches, long after any word of theirs was overwritten.
 constexpr unsigned kAttnSpinLimit = 1u << 18;
 struct AttnTail {
     unsigned long long* tagged;  // [H hd + 2 Hkv hd]
     unsigned* done;              // [1]
     int* err;                    // [1]
     unsigned natt;               // Hkv S
+    unsigned wrap;               // natt floor((2^32 - 1) / natt) - 1
     float* Kc;                   // [Hkv][hd][Lmax]
     float* Vc;                   // [Hkv][Lmax][hd]
     const float* rope;

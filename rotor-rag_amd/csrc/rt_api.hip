@@ -579,7 +579,13 @@ static hipError_t upload_splitk_group(rt_plan* p) {
         if (e == hipSuccess) e = hipMalloc(&p->gemm_ws, ws_n * sizeof(int));
         if (e != hipSuccess) return e;
     }
-    for (size_t i = 0; i < g.size(); ++i) {
+    // the split problems' workgroups first in the grid: they walk their part of K and then
+    // hand over, so starting them first shortens the launch
+    std::vector<size_t> order;
+    for (int pass = 0; pass < 2; ++pass)
+        for (size_t i = 0; i < g.size(); ++i)
+            if ((splitk_parts(g[i].C, Cmin) > 1) == (pass == 0)) order.push_back(i);
+    for (size_t i : order) {
         const int parts = splitk_parts(g[i].C, Cmin), nrb = g[i].Np / kRowBlock;
         for (int kp = 0; kp < parts; ++kp) {
             GemmArgs a = g[i];

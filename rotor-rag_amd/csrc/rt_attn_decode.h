@@ -182,9 +182,10 @@ __device__ __forceinline__ void attn_tile(SRC qh, SRC kn, SRC vn, float c, float
 #pragma unroll
     for (int i = 0; i < VN; ++i) vv[i] = kv.v[i];
     if (holds_new) {
-        const float vs_d = sm->vs[d];
-#pragma unroll
-        for (int i = 0; i < VN; ++i) vv[i] = g + i * G == lp ? vs_d : vv[i];
+        // the new key's slot among this thread's keys g, g + G, ..: g and lp are uniform over
+        // the wave, so one indexed register write takes the place of a select per key
+        const int rel = __builtin_amdgcn_readfirstlane(lp - g);
+        if (rel >= 0 && rel % G == 0) vv[rel / G] = sm->vs[d];
     }
     float o0 = 0.f, o1 = 0.f;
     constexpr int CH = VN >= 8 ? 8 : VN;

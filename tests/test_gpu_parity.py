@@ -256,6 +256,40 @@ def test_cfg2_layer_plan_vs_oracle(hip):
             assert np.array_equal(y.cpu().numpy(), y_exact), f"run {rep}: projection {N}x{K} (input {xi})"
 
 
+@pytest.mark.parametrize("K_long,parts", [(1280, 2), (1920, 3), (2560, 4), (3200, 5), (7040, 8)])
+def test_splitk_parts_vs_oracle(hip, K_long, parts):
+    """A split-K plan (M = 33) whose long problem is cut into 2-8 parts of about the short
+    problem's 10 chunks: the last part of each row block to arrive adds the other parts'
+    tiles and resets the row block's count for the next run.  Ragged N on both problems;
+    every output bit-exact against the oracle on three runs."""
+    import torch
+
+    from rotor import _hip as H_
+
+    M = 33
+    rng = np.random.default_rng(K_long)
+    shapes = [(100, 640), (200, K_long)]  # 2 and 4 row blocks
+    ws, xs, ys, cases = [], [], [], []
+    for N, K in shapes:
+        x = rng.standard_normal((M, K), dtype=np.float32)
+        W, scale = O.make_ternary(rng, N, K)
+        cases.append((x, W, scale))
+        ws.append(hip.upload(O.pack_rotor(W), K, scale))
+        xs.append(torch.from_numpy(x).cuda())
+        ys.append(torch.empty((M, N), dtype=torch.float32, device="cuda"))
+    plan = hip.plan(ws, xs, ys)
+    assert plan.describe() == (H_.LAUNCH_SPLITK, 64, 64, 2 + 4 * parts)
+    for rep in range(3):
+        for y in ys:
+            y.fill_(float("nan"))
+        plan.run()
+        torch.cuda.synchronize()
+        for (x, W, scale), y in zip(cases, ys):
+            _, q, s_, acc = O.ternary_linear(x, W, scale)
+            y_exact = (acc.astype(np.float32) * s_[:, None]) * np.float32(scale)
+            assert np.array_equal(y.cpu().numpy(), y_exact), f"run {rep}: {y.shape[1]}x{x.shape[1]}"
+
+
 # Tile-GEMM plans (M > 64) and the tile shape each must take, checked bit-exact against the
 # oracle problem by problem: name -> (M, [(N, K, input index)], (tile_m, tile_n, tiles)).
 TILE_PLANS = {

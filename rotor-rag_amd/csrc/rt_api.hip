@@ -1285,9 +1285,11 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
     const int Gq = H / Hkv;
     if (plan->probs[0].N != H * hd || plan->probs[1].N != Hkv * hd || plan->probs[2].N != Hkv * hd)
         return fail(RT_EINVAL, std::string(who) + ": the plan's outputs must be q [H * hd], k and v [Hkv * hd]");
-    if (64 * plan->shape.nw != 256 * Gq)
+    // (the poll of an attention workgroup takes one thread per q value of its heads and k, v
+    // value of its group: Gq >= 2)
+    if (64 * plan->shape.nw != 256 * Gq || Gq < 2)
         return fail(RT_EINVAL, std::string(who) + ": the plan's workgroups must hold one 256-thread attention tile "
-                                                  "per query head of a KV group (H / Hkv = 4 for this plan)");
+                                                  "per query head of a KV group, H / Hkv >= 2 (H / Hkv = 4 for this plan)");
     const QuantProb& P = plan->pro;
     if (P.mode == kAttnNorm || P.K % 64 ||
         vec_elements(P.K, 64 * plan->shape.nw) == 0 || ((uintptr_t)P.x & 15u) || ((uintptr_t)P.aux & 15u))
@@ -1324,7 +1326,10 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
     t.Gq = Gq;
     t.Lmax = Lmax;
     t.S = attn_splits(Lmax);
-    t.natt = (unsigned)(Hkv * t.S);
+    // the group's query heads two to a workgroup where they split evenly: the tiles' arithmetic
+    // (one CU per workgroup) then spreads over twice the CUs
+    t.hpw = Gq % 2 == 0 && Gq >= 4 ? Gq / 2 : Gq;
+    t.natt = (unsigned)(Hkv * t.S * (Gq / t.hpw));
     t.wrap = t.natt * (0xFFFFFFFFu / t.natt) - 1u;
     t.qrows = H * hd;
     t.nkv = Hkv * hd;
@@ -1349,15 +1354,15 @@ int rt_plan_attention_combine(rt_plan* plan, float* out, double* ssq) {
             return fail(RT_EINVAL, std::string(who) + ": out must be 16-byte and ssq 8-byte aligned");
         // the workgroups of a KV group wait for each other's partials: every workgroup of the
         // launch must be resident at once, and a workgroup's chunks of 32 outputs must fit it
-        const int NC = plan->att.Gq * plan->att_hd / 32, S = plan->att.S;
-        if (32 * ((NC + S - 1) / S) > 64 * plan->shape.nw)
+        const int NC = plan->att.Gq * plan->att_hd / 32, P = (int)plan->att.natt / plan->att_Hkv;
+        if (32 * ((NC + P - 1) / P) > 256 * plan->att.hpw)
             return fail(RT_EINVAL, std::string(who) + ": too few key blocks for the group's outputs");
         DeviceGuard g(plan->device);
         int resident = 0;
         RT_HIP(gemv_attn_capacity(plan->pro.K, plan->pro.Kp, plan->shape.nw, plan->att.Gq, &resident));
-        if (plan->total_rb + plan->att_Hkv * S > resident)
+        if (plan->total_rb + (int)plan->att.natt > resident)
             return fail(RT_EINVAL, std::string(who) + ": the launch's " +
-                                       std::to_string(plan->total_rb + plan->att_Hkv * S) +
+                                       std::to_string(plan->total_rb + (int)plan->att.natt) +
                                        " workgroups exceed the " + std::to_string(resident) +
                                        " the device holds at once");
     }

@@ -527,18 +527,20 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
 
 // Decode qkv GEMV (E-element RMSNorm prologue) with the attention partials of the token in
 // the same launch: workgroups [0, total_rb) are the GEMV's row blocks (q, k, v problems),
-// the following Hkv * S workgroups the attention of (KV head kh, key block s), kh slowest,
-// each of Gq 256-thread tiles (the Gq query heads of kh; blockDim = 256 Gq).  An attention
+// the following Hkv * P workgroups (P = S Gq / hpw) the attention of (KV head kh, key block
+// s, query heads hp hpw .. hp hpw + hpw - 1 of the group), kh slowest, then hp, each of hpw
+// 256-thread tiles (blockDim = 256 Gq: the waves past hpw tiles end at once).  Splitting a
+// group's heads over workgroups spreads the tiles' arithmetic over more CUs.  An attention
 // workgroup issues its key block's loads and reads the position and the epoch; when its
-// block holds a key, its first (Gq + 2) hd threads (one per q, k and v value of its KV
-// group) poll the GEMV's tagged outputs (bounded) until each carries the epoch and leave
-// the values in LDS, and the tiles of rt_attn_decode.h run on them.  Forward
-// progress: the attention workgroups wait only for GEMV workgroups, which come first in
-// the grid and never wait.
-// With rt_plan_attention_combine (at.out set) the S attention workgroups of KV group kh
-// share the group's combine: workgroup s takes the chunks of 32 outputs s, s + S, ..
+// block holds a key, its first (hpw + 2) hd threads (one per q value of its heads and k, v
+// value of its KV group) poll the GEMV's tagged outputs (bounded) until each carries the
+// epoch and leave the values in LDS, and the tiles of rt_attn_decode.h run on them.
+// Forward progress: the attention workgroups wait only for GEMV workgroups, which come
+// first in the grid and never wait.
+// With rt_plan_attention_combine (at.out set) the P attention workgroups of KV group kh
+// share the group's combine: peer r = hp S + s takes the chunks of 32 outputs r, r + P, ..
 // (< Gq HD / 32), one output per thread (chunk i on threads [32 i, 32 i + 32): the host
-// allows the combine where they fit the workgroup).  A thread reads its output's partial value and the
+// allows the combine where they fit the workgroup's live threads).  A thread reads its output's partial value and the
 // (m, z) of every block of its head from the tagged copies, polling (bounded) until every
 // word carries the launch's epoch, combines them in the operation order of
 // attn_combine_element and writes the output and, per chunk, the f64 sum of the squares of
@@ -546,11 +548,11 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
 // partials, which every peer stores before any wait of its own; the host allows the combine
 // only when the device holds the whole grid at once.
 template <int HD>
-__device__ __forceinline__ void attn_peer_combine(const AttnTail& at, int kh, int s, unsigned ep) {
-    const int S = at.S, NC = at.Gq * HD / 32;
+__device__ __forceinline__ void attn_peer_combine(const AttnTail& at, int kh, int r, unsigned ep) {
+    const int S = at.S, NC = at.Gq * HD / 32, P = S * (at.Gq / at.hpw);  // P: workgroups of a KV group
     const int t = (int)threadIdx.x;
-    if (s + 2 * (t >> 6) * S >= NC) return;  // waves past the workgroup's chunks (no barrier follows)
-    const int c = s + (t >> 5) * S;
+    if (r + 2 * (t >> 6) * P >= NC) return;  // waves past the workgroup's chunks (no barrier follows)
+    const int c = r + (t >> 5) * P;
     const bool act = c < NC;  // lanes of a chunk past the group re-read the last one's words
     const int e = min(c, NC - 1) * 32 + (t & 31);
     const int hg = e / HD, d = e % HD, h = kh * at.Gq + hg;
@@ -600,14 +602,19 @@ __device__ __forceinline__ void attn_peer_combine(const AttnTail& at, int kh, in
 template <int HD>
 __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb) {
     extern __shared__ __attribute__((aligned(16))) int red[];
+    // attention workgroup i: KV group kh, peer r = hp S + s in the group (key block s, query
+    // heads [hp hpw, hp hpw + hpw) of the group), one 256-thread tile per head; the waves past
+    // them end here, before any barrier
+    const int i = (int)blockIdx.x - total_rb, P = at.S * (at.Gq / at.hpw);
+    const int kh = i / P, r = i - kh * P, hp = r / at.S, s = r - hp * at.S;
+    const int sub = (int)(threadIdx.x >> 8), t = (int)(threadIdx.x & 255);
+    if (sub >= at.hpw) return;
+    const int h0 = kh * at.Gq + hp * at.hpw, h = h0 + sub;
     const AttnLdsPtr<HD> sm = (AttnLdsPtr<HD>)red;
     typedef __attribute__((address_space(3))) float lfl;
-    lfl* const qkv = (lfl*)(sm + at.Gq);  // the group's q (Gq HD), k (HD), v (HD)
-    const int i = (int)blockIdx.x - total_rb;
-    const int kh = i / at.S, s = i - kh * at.S;
-    const int sub = (int)(threadIdx.x >> 8), t = (int)(threadIdx.x & 255), h = kh * at.Gq + sub;
+    lfl* const qkv = (lfl*)(sm + at.hpw);  // the heads' q (hpw HD), the group's k (HD), v (HD)
     const int j0 = s * kAttnBlock;
-    const int nin = (at.Gq + 2) * HD;
+    const int nin = (at.hpw + 2) * HD;
     AttnKV<HD> kv;
     attn_kv_load<HD>(at.Kc, at.Vc, kh, j0, at.Lmax, t, kv);
     const unsigned ep = attn_epoch(at);
@@ -621,10 +628,10 @@ __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb)
         float c, sn;
         attn_rope_load<HD>(at.rope, pos, t, c, sn);
         const int e = (int)threadIdx.x;
-        if (e < nin) {  // waves whose lanes all hold a value of the group (nin % 64 == 0)
-            const int g = e < at.Gq * HD ? kh * at.Gq * HD + e
-                                         : at.qrows + (e < (at.Gq + 1) * HD ? 0 : at.nkv) + kh * HD +
-                                               (e - at.Gq * HD) % HD;
+        if (e < nin) {  // waves whose lanes all hold a value of the heads or the group (nin % 64 == 0)
+            const int g = e < at.hpw * HD ? h0 * HD + e
+                                          : at.qrows + (e < (at.hpw + 1) * HD ? 0 : at.nkv) + kh * HD +
+                                                (e - at.hpw * HD) % HD;
             unsigned it = 0;
             unsigned long long w;
             while (true) {
@@ -639,12 +646,14 @@ __device__ __forceinline__ void qkv_attn_block(const AttnTail& at, int total_rb)
             qkv[e] = __uint_as_float((unsigned)w);
         }
         __syncthreads();
-        attn_tile<HD, true, true>(qkv + sub * HD, qkv + at.Gq * HD, qkv + (at.Gq + 1) * HD, c, sn, at.Kc, at.Vc,
-                                  kh, sub == at.Gq - 1, at.Lmax, pos, j0, at.scale, wp, wt, tag, t, sm + sub, kv);
+        // one writer of the new key and value per KV group: the group's last head
+        attn_tile<HD, true, true>(qkv + sub * HD, qkv + at.hpw * HD, qkv + (at.hpw + 1) * HD, c, sn, at.Kc, at.Vc,
+                                  kh, h == kh * at.Gq + at.Gq - 1, at.Lmax, pos, j0, at.scale, wp, wt, tag, t,
+                                  sm + sub, kv);
     } else {
         attn_tile_empty<HD, true>(wp, wt, tag, t);
     }
-    if (at.out) attn_peer_combine<HD>(at, kh, s, ep);
+    if (at.out) attn_peer_combine<HD>(at, kh, r, ep);
     // this workgroup is past its reads of the launch's tagged words: count it (the epoch of
     // the next launch follows from the count; no result to wait for)
     if (threadIdx.x == 0) (void)__builtin_amdgcn_atomic_inc32(at.done, at.wrap, __ATOMIC_RELAXED, "agent");
@@ -789,16 +798,18 @@ hipError_t launch_gemv_attn(const GemvArgs& args, const AttnTail& at, int Hkv, i
     const int nw = shape.nw;
     // the shapes the kernel assumes: three inline problems over one RMSNorm-quantised row,
     // one row block per workgroup, a 256-thread tile per query head of a KV group, groups of
-    // whole row blocks
+    // whole row blocks; an attention workgroup's live threads (256 hpw) hold its poll's
+    // (hpw + 2) hd values, so hpw >= 2 at hd = 128
     const bool vec = P.K % 64 == 0 && aligned16(P.x) && aligned16(P.aux) && aligned16(P.aux2);
     const int E = vec ? vec_elements(P.K, 64 * nw) : 0;
     if (a.has_pro != 1 || a.M != 1 || a.out_i32 || a.pair_a || a.ninl != 3 || !shape.ksplit ||
         E == 0 || P.mode == kAttnNorm || hd != 128 || 64 * nw != 256 * at.Gq ||
         at.qrows != at.Gq * Hkv * hd || at.nkv != Hkv * hd || a.inl[0].N != at.qrows || a.inl[1].N != at.nkv ||
         a.inl[2].N != at.nkv || a.inl[1].wg_begin * kRowBlock != at.qrows ||
-        a.inl[2].wg_begin * kRowBlock != at.qrows + at.nkv || at.S <= 0 || at.S != attn_splits(at.Lmax))
+        a.inl[2].wg_begin * kRowBlock != at.qrows + at.nkv || at.S <= 0 || at.S != attn_splits(at.Lmax) ||
+        at.hpw < 2 || at.Gq % at.hpw || at.natt != (unsigned)(Hkv * at.S * (at.Gq / at.hpw)))
         return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(a.total_rb + Hkv * at.S), 1);
+    const dim3 grid((unsigned)(a.total_rb + (int)at.natt), 1);
     const size_t lds = std::max((size_t)nw * kRowBlock * sizeof(int) + (size_t)P.Kp + sizeof(RowSmem),
                                 (size_t)at.Gq * sizeof(AttnTileLds<128>) + (size_t)(at.Gq + 2) * hd * sizeof(float));
     if (E == 4) launch_qkv_attn<3>(grid, nw, lds, s, a, at);

@@ -153,8 +153,9 @@ struct GemvArgs {
 // Attention partials in the qkv GEMV's launch (gemv_ksplit_kernel with an AttnTail): the
 // GEMV workgroups also store every output y of the q, k and v problems (concatenated, row
 // n of the launch at index n) as tagged[n] = epoch << 32 | bits(y), a 64-bit
-// device-coherent store; the natt = Hkv * S attention workgroups poll their group's q, k and
-// v words until every one carries the epoch (bounded; err counts the waits that gave up,
+// device-coherent store; the natt = Hkv * S * Gq / hpw attention workgroups (hpw query heads
+// of a KV group and one key block each) poll their heads' q and the group's k and v words
+// until every one carries the epoch (bounded; err counts the waits that gave up,
 // never expected).  Each attention workgroup adds one to *done when it has finished, without
 // waiting for the result, and a launch's epoch is *done / natt + 1, read by every workgroup
 // at its start: the count grows by natt per launch and reaches the next multiple only when
@@ -169,7 +170,7 @@ struct AttnTail {
     unsigned long long* tagged;  // [H hd + 2 Hkv hd]
     unsigned* done;              // [1]
     int* err;                    // [1]
-    unsigned natt;               // Hkv S
+    unsigned natt;               // Hkv S Gq / hpw: the attention workgroups of a launch
     unsigned wrap;               // natt floor((2^32 - 1) / natt) - 1
     float* Kc;                   // [Hkv][hd][Lmax]
     float* Vc;                   // [Hkv][Lmax][hd]
@@ -177,12 +178,13 @@ struct AttnTail {
     const int* pos;
     float* work;                 // partials [H][S][hd + 2]
     int Gq, Lmax, S, nkv;        // nkv = Hkv hd: where k starts after q (H hd), v after k
+    int hpw;                     // query heads per attention workgroup (Gq / hpw of them per key block)
     int qrows;                   // H hd
     float scale;
     // rt_plan_attention_combine (out != nullptr, S <= kAttnSMax): the attention workgroups
     // also store their partials as tagged words ptag [H][S][hd + 2] (epoch << 32 | bits),
-    // and the S workgroups of KV group kh share its combine: each polls the partials of its
-    // share of the group's outputs, combines them into out [H hd] and writes per 32 outputs
+    // and the S Gq / hpw workgroups of KV group kh share its combine: each polls the partials
+    // of its share of the group's outputs, combines them into out [H hd] and writes per 32 outputs
     // the f64 sum of their squares into ssq [H hd / 32]
     float* out;
     double* ssq;

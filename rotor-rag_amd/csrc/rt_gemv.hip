@@ -583,13 +583,22 @@ __device__ __forceinline__ void attn_peer_combine(const AttnTail& at, int kh, in
 #pragma unroll
     for (int sb = 0; sb < kAttnSMax; ++sb)
         if (sb < S) mx = fmaxf(mx, m[sb]);
+    // the factors expf(m_sb - mx) are the same for the 32 outputs of a chunk (one head): lane
+    // sb of the chunk computes block sb's, and every lane takes them from there
+    const int cl = t & 31, cbase = t & 32;
+    float mj = m[0];
+#pragma unroll
+    for (int sb = 1; sb < kAttnSMax; ++sb) mj = cl == sb ? m[sb] : mj;
+    const float fj = expf(mj - mx);
+    float f[kAttnSMax];
+#pragma unroll
+    for (int sb = 0; sb < kAttnSMax; ++sb) f[sb] = __shfl(fj, cbase + sb, 64);
     float num = 0.0f, den = 0.0f;
 #pragma unroll
     for (int sb = 0; sb < kAttnSMax; ++sb) {
         if (sb >= S || m[sb] == -INFINITY) continue;
-        const float f = expf(m[sb] - mx);
-        num = fmaf(f, p[sb], num);
-        den = fmaf(f, z[sb], den);
+        num = fmaf(f[sb], p[sb], num);
+        den = fmaf(f[sb], z[sb], den);
     }
     const float o = num / den;
     const int k = h * HD + d;

@@ -161,6 +161,7 @@ struct rt_plan {
     int gemm_cfg = 0, gemm_tiles = 0;  // M > 64: tile shape, tiles over all problems
     int gemm_units = 0;              // 8 < M <= 64: workgroups of the split-K launch (parts x row blocks)
     int* dev_unit2d = nullptr;       // 8 < M <= 64: descriptor of every unit
+    std::vector<int> gemm_bnd;       // M > 8: first unit (tile) of descriptors 1.. (launch arguments)
     int* gemm_cnt = nullptr;         // split problems: arrivals per row block (zero between launches)
     int* gemm_ws = nullptr;          // split problems: int32 partial tiles
     std::vector<const rt_act*> acts; // plans over caller-quantised activations
@@ -556,6 +557,12 @@ int rt_plan_free(rt_plan* plan) {
 // 8), so that no workgroup walks far more chunks than the others.
 static int splitk_parts(int C, int Cmin) { return std::max(1, std::min(8, (C + Cmin / 2) / std::max(Cmin, 1))); }
 
+// the bounds a grouped GEMM launch passes in its arguments (-1: too many descriptors, the
+// launch reads its unit -> descriptor table instead)
+static int group_bounds(const rt_plan* p) {
+    return (int)p->gemm_bnd.size() <= kGroupBounds ? (int)p->gemm_bnd.size() : -1;
+}
+
 static hipError_t upload_splitk_group(rt_plan* p) {
     const std::vector<GemmArgs>& g = p->gemms;
     int Cmin = 1 << 30;
@@ -596,6 +603,7 @@ static hipError_t upload_splitk_group(rt_plan* p) {
             a.c1 = (int)((long long)(kp + 1) * a.C / parts);
             a.cnt = parts > 1 ? p->gemm_cnt + offs[i].first : nullptr;
             a.part_ws = parts > 1 ? p->gemm_ws + offs[i].second : nullptr;
+            if (!d.empty()) p->gemm_bnd.push_back((int)unit2d.size());
             unit2d.insert(unit2d.end(), (size_t)nrb, (int)d.size());
             d.push_back(a);
         }
@@ -624,6 +632,7 @@ static hipError_t upload_gemm_group(rt_plan* p) {
     long long total = 0;
     for (size_t i = 0; i < g.size(); ++i) {
         g[i].wg_begin = (int)total;
+        if (i > 0) p->gemm_bnd.push_back((int)total);
         const long long n = gemm_tile_count(p->gemm_cfg, p->M, g[i].N);
         tile2p.insert(tile2p.end(), (size_t)n, (int)i);
         total += n;
@@ -860,11 +869,13 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
     a.out_i32 = 0;
     a.total_rb = plan->total_rb;
     if (plan->dev_tile2p) {
-        RT_HIP(launch_gemm_tiles(plan->dev_gemms, plan->dev_tile2p, plan->gemm_tiles, plan->gemm_cfg, ctx->stream));
+        RT_HIP(launch_gemm_tiles(plan->dev_gemms, plan->dev_tile2p, plan->gemm_bnd.data(), group_bounds(plan),
+                                 plan->gemm_tiles, plan->gemm_cfg, ctx->stream));
         return RT_OK;
     }
     if (plan->dev_gemms) {
-        RT_HIP(launch_gemm_group(plan->dev_gemms, plan->dev_unit2d, plan->gemm_units, ctx->stream));
+        RT_HIP(launch_gemm_group(plan->dev_gemms, plan->dev_unit2d, plan->gemm_bnd.data(), group_bounds(plan),
+                                 plan->gemm_units, ctx->stream));
         return RT_OK;
     }
     if (plan->att_on)

@@ -158,6 +158,10 @@ struct GemmGroupArgs {
     const GemmArgs* dev;
     const int* rb2p;
     GemmArgs one;
+    // nb >= 0: descriptor i + 1 starts at unit bnd[i] (i < nb), so a unit finds its descriptor
+    // by comparing with these arguments instead of loading rb2p [unit] first; nb < 0: rb2p
+    int nb;
+    int bnd[kGroupBounds];
 };
 
 // Problem of unit b, read through constant-address-space pointers so that it stays
@@ -165,8 +169,16 @@ struct GemmGroupArgs {
 typedef __attribute__((address_space(4))) const GemmArgs cgemm;
 typedef __attribute__((address_space(4))) const int cidx_g;
 __device__ __forceinline__ GemmArgs find_gemm(const GemmGroupArgs& ga, int b) {
+    // the bounds are read before the branch (the empty asm keeps them there), so their loads
+    // go out with the first ones
+    const int nb = ga.nb;
+    int j = 0;
+#pragma unroll
+    for (int i = 0; i < kGroupBounds; ++i) j += i < nb && b >= ga.bnd[i] ? 1 : 0;
+    asm volatile("" ::"s"(j), "s"(nb));
     if (!ga.dev) return ga.one;
-    const cgemm* q = (cgemm*)ga.dev + ((cidx_g*)ga.rb2p)[b];
+    if (nb < 0) j = ((cidx_g*)ga.rb2p)[b];
+    const cgemm* q = (cgemm*)ga.dev + j;
     return GemmArgs{q->w,  q->qx,       q->sx, q->rs, q->out, q->s_w, q->M,     q->N,   q->Np,
                     q->C,  q->ldo,      q->out_i32, q->res, q->wg_begin, q->c0, q->c1, q->kp, q->parts,
                     q->cnt, q->part_ws};
@@ -811,9 +823,19 @@ static hipError_t launch_splitk(const GemmGroupArgs& ga, int blocks, hipStream_t
 // against eight waves, 160 KiB, one workgroup per CU and 1.4 rounds).
 constexpr int kSplitkWaves = 4;
 
-hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, int total_rb, hipStream_t s) {
+static GemmGroupArgs group_args(const GemmArgs* dev, const int* u2p, const int* bnd, int nb) {
+    GemmGroupArgs ga{dev, u2p, GemmArgs{}, -1, {}};
+    if (bnd && nb >= 0 && nb <= kGroupBounds) {
+        ga.nb = nb;
+        for (int i = 0; i < nb; ++i) ga.bnd[i] = bnd[i];
+    }
+    return ga;
+}
+
+hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, const int* bnd, int nb, int total_rb,
+                             hipStream_t s) {
     if (total_rb <= 0) return hipSuccess;
-    return launch_splitk<kSplitkWaves, 4>(GemmGroupArgs{dev, rb2p, GemmArgs{}}, total_rb, s);
+    return launch_splitk<kSplitkWaves, 4>(group_args(dev, rb2p, bnd, nb), total_rb, s);
 }
 
 template <int BM, int BN, int WAVES_M, int STAGES>
@@ -897,8 +919,9 @@ long long gemm_tile_count(int cfg, int M, int N) {
     return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn);
 }
 
-hipError_t launch_gemm_tiles(const GemmArgs* dev, const int* tile2p, int total_tiles, int cfg, hipStream_t s) {
-    return launch_tile_cfg(cfg, GemmGroupArgs{dev, tile2p, GemmArgs{}}, total_tiles, s);
+hipError_t launch_gemm_tiles(const GemmArgs* dev, const int* tile2p, const int* bnd, int nb, int total_tiles, int cfg,
+                             hipStream_t s) {
+    return launch_tile_cfg(cfg, group_args(dev, tile2p, bnd, nb), total_tiles, s);
 }
 
 hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
@@ -910,12 +933,12 @@ hipError_t launch_gemm(const GemmArgs& a, hipStream_t s) {
     if (bm == 64) {
         GemmArgs one = a;
         one.wg_begin = 0;
-        return launch_splitk<kSplitkWaves, 4>(GemmGroupArgs{nullptr, nullptr, one}, a.Np / kRowBlock, s);
+        return launch_splitk<kSplitkWaves, 4>(GemmGroupArgs{nullptr, nullptr, one, -1, {}}, a.Np / kRowBlock, s);
     }
     const int cfg = gemm_tile_cfg(a.M, &a.N, &a.C, 1);
     GemmArgs one = a;
     one.wg_begin = 0;
-    return launch_tile_cfg(cfg, GemmGroupArgs{nullptr, nullptr, one}, (int)gemm_tile_count(cfg, a.M, a.N), s);
+    return launch_tile_cfg(cfg, GemmGroupArgs{nullptr, nullptr, one, -1, {}}, (int)gemm_tile_count(cfg, a.M, a.N), s);
 }
 
 }  // namespace rt

@@ -225,6 +225,11 @@ struct GemmArgs {
 
 constexpr int kBufDword3 = 0x00020000;  // buffer resource word 3 for gfx9 raw buffers
 
+// Grouped GEMM launches of at most kGroupBounds + 1 descriptors pass the first unit of each
+// descriptor after the first in their arguments (a unit then finds its descriptor without
+// a table load)
+constexpr int kGroupBounds = 15;
+
 // Wave64 reductions on the DPP network: row_shr 1, 2, 4, 8 leave each 16-lane row's
 // total in its lane 15, row_bcast 15 and 31 carry the row totals into lane 63, which
 // ends up holding op over all 64 lanes (the other lanes hold partial results).  A lane
@@ -344,7 +349,8 @@ int gemm_tile_cfg(int M, const int* N, const int* C, int G);
 long long gemm_tile_count(int cfg, int M, int N);
 // G problems with M > 64 in one tile launch: dev [G] (wg_begin = first tile of the
 // problem), tile2p [total_tiles] problem of every tile, cfg from gemm_tile_cfg.
-hipError_t launch_gemm_tiles(const GemmArgs* dev, const int* tile2p, int total_tiles, int cfg, hipStream_t s);
+hipError_t launch_gemm_tiles(const GemmArgs* dev, const int* tile2p, const int* bnd, int nb, int total_tiles, int cfg,
+                             hipStream_t s);
 // M <= 64 (gemm_bm(M) == 64): G problems in one launch over all their row blocks;
 // dev [G] (wg_begin set), rb2p [total_rb] problem of every global row block.
 // The M = 1 qkv plan (three inline problems, E-element RMSNorm prologue, 256 Gq threads per
@@ -354,7 +360,8 @@ hipError_t launch_gemv_attn(const GemvArgs& args, const AttnTail& at, int Hkv, i
 // Workgroups of that launch (source row of K elements, nw waves, Gq query heads per KV head)
 // that the current device holds at once.
 hipError_t gemv_attn_capacity(int K, int Kp, int nw, int Gq, int* workgroups);
-hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, int total_rb, hipStream_t s);
+hipError_t launch_gemm_group(const GemmArgs* dev, const int* rb2p, const int* bnd, int nb, int total_rb,
+                             hipStream_t s);
 // Once per device (current) before any launch: the function attributes the GEMM kernels
 // and the prefill attention need (dynamic LDS above 64 KiB).
 hipError_t gemm_prepare_device();

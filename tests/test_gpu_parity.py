@@ -290,6 +290,32 @@ def test_splitk_parts_vs_oracle(hip, K_long, parts):
             assert np.array_equal(y.cpu().numpy(), y_exact), f"run {rep}: {y.shape[1]}x{x.shape[1]}"
 
 
+@pytest.mark.parametrize("G", [3, 16, 17, 20])
+@pytest.mark.parametrize("M", [20, 100])
+def test_grouped_gemm_descriptor_lookup(hip, G, M):
+    """A grouped GEMM launch finds a workgroup's problem from the first units of problems
+    1.. passed in its arguments (up to 16 problems) or from its unit table (17 and more):
+    both give every problem's output bit-exact against its single call (split-K at M = 20,
+    tiles at M = 100; problems of 1-3 row blocks and two K, two shared inputs)."""
+    import torch
+
+    rng = np.random.default_rng(1000 * G + M)
+    xs_by_k = {K: torch.from_numpy(rng.standard_normal((M, K), dtype=np.float32)).cuda() for K in (256, 640)}
+    ws, xs, ys = [], [], []
+    for g in range(G):
+        N, K = 64 * (1 + g % 3) - (g % 2) * 7, (256, 640)[g % 2]
+        W, scale = O.make_ternary(rng, N, K)
+        ws.append(hip.upload(O.pack_rotor(W), K, scale))
+        xs.append(xs_by_k[K])
+        ys.append(torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda"))
+    plan = hip.plan(ws, xs, ys)
+    for _ in range(2):
+        plan.run()
+        torch.cuda.synchronize()
+        for g, (w, x, y) in enumerate(zip(ws, xs, ys)):
+            assert torch.equal(y, hip.linear_device(w, x)), f"problem {g}"
+
+
 # Tile-GEMM plans (M > 64) and the tile shape each must take, checked bit-exact against the
 # oracle problem by problem: name -> (M, [(N, K, input index)], (tile_m, tile_n, tiles)).
 TILE_PLANS = {

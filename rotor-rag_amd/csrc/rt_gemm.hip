@@ -643,6 +643,17 @@ __global__ void __launch_bounds__(2 * NW * 64, 4) gemm_splitk_kernel(GemmGroupAr
     const int cw = loader ? wave - NW : wave;  // the compute wave this wave is or feeds
     const GemmArgs a = find_gemm(ga, blockIdx.x);
     const int C = a.C, rb = (int)blockIdx.x - a.wg_begin, n0 = rb * kRowBlock;
+    // the epilogue's scales (thread t: column n0 + t % 64, rows t / 64 + 2 NW j), requested now
+    // so that the epilogue does not wait for them (a load wave's ring waits count them too:
+    // they are older than its ring loads)
+    constexpr int EPT = 64 * 64 / NT, RS = NT / 64;  // elements per thread; row stride
+    const int n = n0 + lane, mb = t >> 6;
+    float sw = 0.0f, sxv[EPT];
+    if (!a.out_i32) {
+        sw = a.rs ? a.rs[min(n, a.N - 1)] : a.s_w;
+#pragma unroll
+        for (int j = 0; j < EPT; ++j) sxv[j] = a.sx[mb + RS * j];  // sx holds the 64 padded rows
+    }
     // this unit's chunks (one part of a split problem, or all), split over the compute waves
     const int k0 = a.c1 > 0 ? a.c0 : 0, len = (a.c1 > 0 ? a.c1 : C) - k0;
     const int cb = k0 + __builtin_amdgcn_readfirstlane((cw * len) / NW);
@@ -726,10 +737,8 @@ __global__ void __launch_bounds__(2 * NW * 64, 4) gemm_splitk_kernel(GemmGroupAr
                     part[(i * 32 + 8 * (k >> 2) + 4 * g + (k & 3)) * 64 + j * 32 + r32] = acc[i][j][k];
     }
     __syncthreads();
-    // thread t: column n0 + t % 64, rows t / 64 + 2 NW j, j < EPT; output and residual as
-    // raw buffers over M rows (rows past M fall outside; a column past N adds bit 31)
-    constexpr int EPT = 64 * 64 / NT, RS = NT / 64;  // elements per thread; row stride
-    const int n = n0 + lane, mb = t >> 6;
+    // thread t: column n, rows mb + RS j, j < EPT; output and residual as raw buffers over M
+    // rows (rows past M fall outside; a column past N adds bit 31)
     int v[EPT];
 #pragma unroll
     for (int j = 0; j < EPT; ++j) {
@@ -778,10 +787,7 @@ __global__ void __launch_bounds__(2 * NW * 64, 4) gemm_splitk_kernel(GemmGroupAr
             __builtin_amdgcn_raw_buffer_store_b32((unsigned)v[j], out, (mb + RS * j) * a.ldo * 4 + coff, 0, 0);
         return;
     }
-    const float sw = a.rs ? a.rs[min(n, a.N - 1)] : a.s_w;
-    float sxv[EPT], rv[EPT];
-#pragma unroll
-    for (int j = 0; j < EPT; ++j) sxv[j] = a.sx[mb + RS * j];  // sx holds the 64 padded rows
+    float rv[EPT];
     const __amdgpu_buffer_rsrc_t res =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.res, 0, a.res ? range : 0u, kBufDword3);
     if (a.res) {

@@ -350,6 +350,8 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, unsigned idx) 
     return ((unsigned long long)b << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
 }
 
+constexpr int kLmAuxNT = 2;  // buffer-load cache policy: non-temporal
+
 template <int SLICES>
 __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict__ E, const float* __restrict__ x,
                                                       const float* __restrict__ norm_w, float eps, int V,
@@ -365,13 +367,19 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
     // Two batches alternate (A, B): the next batch's loads are in flight during the current
     // one's arithmetic, and the first batch is issued before the RMSNorm below.
     v4u wa[RB][SLICES], wb[RB][SLICES];
+    // the wave's rows as one buffer (32-bit offsets from its first row), read with the
+    // non-temporal policy (streamed once): buffer loads measured 1.6 % faster than global ones
+    // (with one atomic per workgroup below)
+    const __amdgpu_buffer_rsrc_t er = __builtin_amdgcn_make_buffer_rsrc((void*)(E + (size_t)min(r0, V - 1) * D), 0,
+                                                                        0x7FFFFFFF, kBufDword3);
     auto load_batch = [&](v4u (&w)[RB][SLICES], int rb) {
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
-            const int r = min(rb + i, V - 1);  // rows past V re-read the last row (discarded)
-            const v4u* row = reinterpret_cast<const v4u*>(E + (size_t)r * D);
+            const int r = min(rb + i, V - 1) - min(r0, V - 1);  // rows past V re-read the last row (discarded)
 #pragma unroll
-            for (int sl = 0; sl < SLICES; ++sl) w[i][sl] = __builtin_nontemporal_load(row + sl * 64 + lane);
+            for (int sl = 0; sl < SLICES; ++sl)
+                w[i][sl] = __builtin_bit_cast(
+                    v4u, __builtin_amdgcn_raw_buffer_load_b128(er, r * D * 2 + (sl * 64 + lane) * 16, 0, kLmAuxNT));
         }
     };
     if (r0 < r1) load_batch(wa, r0);
@@ -433,7 +441,16 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
         if (rb + 2 * RB < r1) load_batch(wa, rb + 2 * RB);
         batch_math(wb, rb + RB);
     }
-    if (lane == 63 && key) atomicMax(best, key);
+    // the workgroup's largest key, one atomic per workgroup
+    __shared__ unsigned long long wkey[4];
+    if (lane == 63) wkey[wave] = key;
+    __syncthreads();
+    if (t == 0) {
+        const unsigned long long k01 = wkey[0] > wkey[1] ? wkey[0] : wkey[1];
+        const unsigned long long k23 = wkey[2] > wkey[3] ? wkey[2] : wkey[3];
+        const unsigned long long k = k01 > k23 ? k01 : k23;
+        if (k) atomicMax(best, k);
+    }
 }
 
 // token = argmax; optionally also written to next_ids[0] (the next step's input) and,
@@ -541,6 +558,8 @@ static hipError_t run_lm_head(const uint16_t* E, const float* x, const float* no
     }
     int rpw = (V + 4 * slots[dev] - 1) / (4 * slots[dev]);
     rpw = (rpw + 7) / 8 * 8;
+    // a wave reads its rows through one buffer resource with 32-bit offsets
+    if ((long long)rpw * SLICES * 512 * 2 >= (1LL << 31)) return hipErrorInvalidValue;
     const unsigned blocks = (unsigned)((V + 4 * rpw - 1) / (4 * rpw));
     hipLaunchKernelGGL(lm_head_kernel<SLICES>, dim3(blocks), dim3(256), 0, s, E, x, norm_w, eps, V, rpw, logits, best);
     return hipGetLastError();

@@ -316,6 +316,29 @@ def test_grouped_gemm_descriptor_lookup(hip, G, M):
             assert torch.equal(y, hip.linear_device(w, x)), f"problem {g}"
 
 
+@pytest.mark.parametrize("K", [64, 128, 192, 256, 320, 384, 448, 576, 704])
+def test_tile256_short_k(hip, K):
+    """The 256 x 256 tile (cfg 3 gate/up shape) with K of 1 to 11 chunks: fewer chunks than
+    its ring holds, about as many, and a few more (the ring's fill, steady state and tail),
+    every output bit-exact against the oracle."""
+    import torch
+
+    from rotor import _hip as H_
+
+    M, N = 2048, 6912
+    rng = np.random.default_rng(K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    W, scale = O.make_ternary(rng, N, K)
+    w = hip.upload(O.pack_rotor(W), K, scale)
+    y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    plan = hip.plan([w], [torch.from_numpy(x).cuda()], [y])
+    assert plan.describe() == (H_.LAUNCH_TILES, 256, 256, 216)
+    plan.run()
+    torch.cuda.synchronize()
+    _, q, s_, acc = O.ternary_linear(x, W, scale)
+    assert np.array_equal(y.cpu().numpy(), (acc.astype(np.float32) * s_[:, None]) * np.float32(scale))
+
+
 # Tile-GEMM plans (M > 64) and the tile shape each must take, checked bit-exact against the
 # oracle problem by problem: name -> (M, [(N, K, input index)], (tile_m, tile_n, tiles)).
 TILE_PLANS = {

@@ -271,12 +271,17 @@ def test_rope_attention_decode_equals_separate_launches(hip, pos0, H, Hkv, hd, L
     assert torch.equal(ws, ws_ref)
 
 
-# Lmax 640: 10 key blocks, each workgroup combines 2 of a KV group's 16 chunks of 32 outputs;
-# 256 / 192 / 64: 4 / 3 / 1 blocks, 4 / 6 (the last one past the group) / 16 chunks per
-# workgroup on several waves; 2048: no combine in the launch
-@pytest.mark.parametrize("pos0,Lmax", [(0, 640), (63, 640), (64, 640), (639, 640), (1000, 2048), (10, 256), (100, 192),
-                                       (0, 64), (63, 64)])
-def test_qkv_plan_with_attention_equals_separate_launches(hip, pos0, Lmax):
+# H / Hkv = 20 / 5 (two query heads per attention workgroup, 20 workgroups per KV group at
+# Lmax 640): Lmax 640: 10 key blocks, each workgroup combines at most one of a KV group's 16
+# chunks of 32 outputs; 256 / 192 / 64: 4 / 3 / 1 blocks, 2 / 3 (the last one past the
+# group) / 8 chunks per workgroup; 2048: no combine in the launch.  64 / 32 and 54 / 18
+# (H / Hkv = 2 and 3: one workgroup per KV group and key block, 8- and 12-wave
+# workgroups, K = 8192 and 6912) at Lmax <= 256, where the whole grid is resident.
+@pytest.mark.parametrize("H,Hkv,pos0,Lmax", [(20, 5, 0, 640), (20, 5, 63, 640), (20, 5, 64, 640), (20, 5, 639, 640),
+                                             (20, 5, 1000, 2048), (20, 5, 10, 256), (20, 5, 100, 192), (20, 5, 0, 64),
+                                             (20, 5, 63, 64), (64, 32, 100, 256), (64, 32, 255, 256),
+                                             (54, 18, 0, 192), (54, 18, 200, 256)])
+def test_qkv_plan_with_attention_equals_separate_launches(hip, H, Hkv, pos0, Lmax):
     """The q/k/v decode plan with the attention attached (RoPE + KV append + split-L partials
     in the GEMV's launch) gives the q, k, v outputs, the partials and the caches of the plan
     followed by rt_rope_attention_decode, bit for bit.  The hand-off: the GEMV also stores
@@ -296,9 +301,9 @@ def test_qkv_plan_with_attention_equals_separate_launches(hip, pos0, Lmax):
     from rotor import _hip as H_
 
     lib, chk = _lib()
-    H, Hkv, hd = 20, 5, 128
+    hd = 128
     D = H * hd
-    rng = np.random.default_rng(pos0 + Lmax)
+    rng = np.random.default_rng(pos0 + Lmax + H)
     f = lambda *shape: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).cuda()
     ws_ = [hip.upload(O.pack_rotor(W), D, s) for W, s in (O.make_ternary(rng, n, D) for n in (D, Hkv * hd, Hkv * hd))]
     x = f(D)

@@ -72,7 +72,7 @@ const char* rt_last_error(void);
  * and RT_SRC_RMSNORM_STATS; 105 = 104 + rt_plan_attach_attention and rt_plan_attention_timeouts;
  * 106 = 105 without rt_plan_set_row_stats and RT_SRC_RMSNORM_STATS (measured slower than each
  * decode prologue reducing its own row), + rt_attention_decode_combine,
- * rt_plan_attention_combine and rt_lm_head_argmax's next_h. */
+ * rt_plan_attention_combine and rt_lm_head_argmax's next_h; 107 = 106 + rt_plan_set_output_ssq. */
 int rt_version(void);
 
 /* Number of visible HIP devices (0 when none); RT_OK even when 0. */
@@ -272,6 +272,13 @@ int rt_plan_attach_attention(rt_plan* plan, float* k_cache, float* v_cache, cons
  * Replaces, for one token, src/rotor/transformer.py:268-281 (softmax and the weighted sum of
  * the values) and the sum of squares of the sub-norm that follows them. */
 int rt_plan_attention_combine(rt_plan* plan, float* out, double* ssq);
+/* Let a one-problem fused decode plan (rt_plan_create_fused, G = 1) also write, per 32
+ * consecutive outputs y (after the residual), the f64 sum of their squares into ssq
+ * [ceil(N / 32)] (device, 8-byte aligned): the aux2 of an RT_SRC_RMSNORM_SSQ plan whose input
+ * row is y, which then needs no reduction of its own (o_proj's output for the gate/up plan,
+ * down's for the next layer's q/k/v plan).  NULL detaches.  No counterpart in the reference
+ * (decode-graph fusion of src/rotor/transformer.py:24-36's sum of squares). */
+int rt_plan_set_output_ssq(rt_plan* plan, double* ssq);
 /* Number of attention waits of the plan's launches that gave up (never expected; the
  * results of such a launch are wrong).  Synchronises the device; a non-zero count also
  * resets the plan's hand-off state (tagged words and the count the epoch follows from).

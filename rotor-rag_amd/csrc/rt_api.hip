@@ -174,6 +174,7 @@ struct rt_plan {
     GemvShape run_shape{};
     float* pair_a = nullptr;      // gate/up pair plan: relu(g)^2 * u [N / 2]
     double* pair_ssq = nullptr;   // its sum of squares per 32 outputs
+    double* out_ssq = nullptr;    // rt_plan_set_output_ssq: f64 sums of squares per 32 outputs
     float* pair_g = nullptr;      // optional g, u [N / 2]
     float* pair_u = nullptr;
     float pair_sg = 1.0f, pair_su = 1.0f;  // gate and up scales
@@ -203,7 +204,7 @@ extern "C" {
 
 const char* rt_last_error(void) { return g_err.c_str(); }
 
-int rt_version(void) { return 106; }
+int rt_version(void) { return 107; }
 
 int rt_device_count(int* n) {
     if (!n) return fail(RT_EINVAL, "rt_device_count: n is NULL");
@@ -856,6 +857,7 @@ int rt_plan_gemv(rt_ctx* ctx, const rt_plan* plan) {
         a.pro = plan->pro;
         a.pair_a = plan->pair_a;
         a.pair_ssq = plan->pair_ssq;
+        a.out_ssq = plan->out_ssq;
         a.pair_g = plan->pair_g;
         a.pair_u = plan->pair_u;
         a.pair_sg = plan->pair_sg;
@@ -1382,6 +1384,22 @@ int rt_plan_attention_combine(rt_plan* plan, float* out, double* ssq) {
     RT_HIP(hipDeviceSynchronize());
     plan->att.out = out;
     plan->att.ssq = ssq;
+    return RT_OK;
+}
+
+int rt_plan_set_output_ssq(rt_plan* plan, double* ssq) {
+    const char* who = "rt_plan_set_output_ssq";
+    if (!plan) return fail(RT_EINVAL, std::string(who) + ": plan is NULL");
+    if (ssq) {
+        if (!plan->fused || plan->G != 1 || plan->M != 1 || plan->pair_a)
+            return fail(RT_EINVAL, std::string(who) + ": needs a one-problem fused decode plan "
+                                                      "(rt_plan_create_fused, G = 1, not a gate/up pair)");
+        if ((uintptr_t)ssq & 7u) return fail(RT_EINVAL, std::string(who) + ": ssq must be 8-byte aligned");
+    }
+    DeviceGuard g(plan->device);
+    // a launch of this plan may still be in flight on the caller's stream
+    RT_HIP(hipDeviceSynchronize());
+    plan->out_ssq = ssq;
     return RT_OK;
 }
 

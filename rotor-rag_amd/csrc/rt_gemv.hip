@@ -514,6 +514,10 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
                 // rows past N are not read (every problem of a joint launch has N % 64 == 0)
                 __hip_atomic_store(tagged + r, tag | __float_as_uint(o), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
+            if (a.out_ssq) {  // the next plan's RMSNORM_SSQ input (rows past N add 0)
+                const double ss = half_reduce31((double)o * (double)o, 0.0, [](double x, double y) { return x + y; });
+                if ((r & 31) == 31) a.out_ssq[(rb * kRowBlock + r) >> 5] = ss;
+            }
         }
         return;
     }

@@ -148,6 +148,9 @@ struct GemvArgs {
     float* pair_g;
     float* pair_u;
     float pair_sg, pair_su;  // the gate and up scales
+    // one-token plans with a prologue and fp32 outputs: out_ssq[j] = sum over outputs
+    // 32 j .. 32 j + 31 of (double) y^2 (rt_plan_set_output_ssq), when not null
+    double* out_ssq;
 };
 
 // Attention partials in the qkv GEMV's launch (gemv_ksplit_kernel with an AttnTail): the

@@ -15,7 +15,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "librotor_hip.so"
-ABI_VERSION = 106  # rt_version() of the library this table binds
+ABI_VERSION = 107  # rt_version() of the library this table binds
 
 class RtSrc(ctypes.Structure):
     """rt_src of include/rotor_hip.h"""
@@ -71,6 +71,7 @@ SIGNATURES = {
     "rt_plan_attach_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t]),
     "rt_plan_attention_combine": (_I, [_P, _P, _P]),
     "rt_plan_attention_timeouts": (_I, [_P, _P]),
+    "rt_plan_set_output_ssq": (_I, [_P, _P]),
     "rt_embed": (_I, [_P, _P, _I, _I, _P, _I, _P]),
     "rt_rope_kv_append": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "rt_attention": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),

@@ -268,14 +268,18 @@ class _DeviceModel:
         # layer fewer; False launches rt_rope_attention_decode after the GEMV
         self.attn_in_qkv = True
         # decode, with the attention in the q/k/v launch: True (default, Lmax <= 640) also
-        # combines the split partials there (the last workgroup of each KV group), writing the
-        # attention output and its sums of squares, so o_proj's prologue only normalises and
+        # combines the split partials there (shared by the workgroups of each KV group), writing
+        # the attention output and its sums of squares, so o_proj's prologue only normalises and
         # quantises (RMSNORM_SSQ); False lets every o_proj workgroup combine the partials
         self.attn_combine_in_qkv = True
         # generate: True (default) lets every argmax write the chosen token's embedding row into
         # the decode input, so the decode step launches no embedding; False embeds the token
         # from its id at the start of every step
         self.embed_in_argmax = True
+        # decode: True (default) lets o_proj and down also write the per-32 sums of squares of
+        # the residual stream they produce, so the gate/up plan and the next layer's q/k/v
+        # plan normalise from them (RMSNORM_SSQ) instead of reducing the row again
+        self.ssq_chain = True
 
     def _state(self, M):
         st = self.state.get(M)
@@ -287,19 +291,25 @@ class _DeviceModel:
         e = lambda *s: torch.empty(s, dtype=torch.float32, device=dev)
         st = {"h": e(M, D), "q": e(M, H * hd), "k": e(M, Hkv * hd), "v": e(M, Hkv * hd), "o": e(M, H * hd),
               "g": e(M, F), "u": e(M, F), "a": e(F),
-              "ssq": torch.empty(F // 32, dtype=torch.float64, device=dev)}
+              "ssq": torch.empty(F // 32, dtype=torch.float64, device=dev),
+              "hssq": torch.empty((D + 31) // 32, dtype=torch.float64, device=dev)}
         st["qkv"], st["gu"], st["o_plan"], st["d_plan"] = [], [], [], []
         st["attn_fused"] = []  # per layer: the q/k/v plan runs the attention partials
         st["attn_comb"] = []   # per layer: ... and combines them into o[0] (sums of squares in ossq)
         st["ossq"] = torch.empty(H * hd // 32, dtype=torch.float64, device=dev)
         hip, eps = self.hip, self.m.eps
+        chain = M == 1 and self.ssq_chain
         for li, L in enumerate(self.layers):
             st["attn_fused"].append(False)
             st["attn_comb"].append(False)
             if M == 1:  # decode: one launch per plan, the input row is quantised in the GEMV prologue
                 h, o, g, u = st["h"][0], st["o"][0], st["g"][0], st["u"][0]
-                st["qkv"].append(hip.plan_fused([L["q_proj"], L["k_proj"], L["v_proj"]], _hip.SRC_RMSNORM, h,
-                                                L["input_norm"], eps=eps, ys=[st["q"][0], st["k"][0], st["v"][0]]))
+                qkv_w, qkv_ys = [L["q_proj"], L["k_proj"], L["v_proj"]], [st["q"][0], st["k"][0], st["v"][0]]
+                if chain and li > 0:  # the previous layer's down wrote the sums of squares of h
+                    st["qkv"].append(hip.plan_fused(qkv_w, _hip.SRC_RMSNORM_SSQ, h, L["input_norm"], st["hssq"],
+                                                    eps=eps, ys=qkv_ys))
+                else:
+                    st["qkv"].append(hip.plan_fused(qkv_w, _hip.SRC_RMSNORM, h, L["input_norm"], eps=eps, ys=qkv_ys))
                 if self.attn_in_qkv and L["attn_sub_norm"] is not None and self.attn_in_prologue:
                     st["attn_fused"][li] = self._attach_attention(st["qkv"][li], L)
                 if st["attn_fused"][li] and self.attn_combine_in_qkv and self.Lmax <= 640:
@@ -316,23 +326,30 @@ class _DeviceModel:
                                                        eps=eps, ys=[h], residuals=[h]))
                 else:
                     st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_QUANT, o, ys=[h], residuals=[h]))
+                if chain:
+                    st["o_plan"][li].set_output_ssq(st["hssq"])
+                # the gate/up source: h after o_proj, normalised from o_proj's sums of squares
+                gu_src = ((_hip.SRC_RMSNORM_SSQ, h, L["post_norm"], st["hssq"]) if chain
+                          else (_hip.SRC_RMSNORM, h, L["post_norm"]))
                 if L["ffn_sub_norm"] is not None and self.ffn_pair:
                     if "gate_up" not in L:  # the interleaved copy the pair plan runs (decode only)
                         L["gate_up"] = hip.interleave_gate_up(L["gate_proj"], L["up_proj"])
                     w_gu, scales = L["gate_up"]
-                    st["gu"].append(hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM, h, L["post_norm"], eps=eps,
-                                                     a=st["a"], ssq=st["ssq"]))
+                    st["gu"].append(hip.plan_gate_up(w_gu, scales, *gu_src, eps=eps, a=st["a"], ssq=st["ssq"]))
                     st["d_plan"].append(hip.plan_fused([L["down_proj"]], _hip.SRC_RMSNORM_SSQ, st["a"],
                                                        L["ffn_sub_norm"], st["ssq"], eps=eps, ys=[h], residuals=[h]))
+                    if chain and li + 1 < len(self.layers):
+                        st["d_plan"][li].set_output_ssq(st["hssq"])
                     continue
-                st["gu"].append(hip.plan_fused([L["gate_proj"], L["up_proj"]], _hip.SRC_RMSNORM, h, L["post_norm"],
-                                               eps=eps, ys=[g, u]))
+                st["gu"].append(hip.plan_fused([L["gate_proj"], L["up_proj"]], *gu_src, eps=eps, ys=[g, u]))
                 if L["ffn_sub_norm"] is not None:
                     st["d_plan"].append(hip.plan_fused([L["down_proj"]], _hip.SRC_RELU2MUL_NORM, g, u,
                                                        L["ffn_sub_norm"], eps=eps, ys=[h], residuals=[h]))
                 else:
                     st["d_plan"].append(hip.plan_fused([L["down_proj"]], _hip.SRC_RELU2MUL, g, u, ys=[h],
                                                        residuals=[h]))
+                if chain and li + 1 < len(self.layers):
+                    st["d_plan"][li].set_output_ssq(st["hssq"])
             else:
                 st["qkv"].append(hip.plan_act([L["q_proj"], L["k_proj"], L["v_proj"]], [self.act_d] * 3, M,
                                               [st["q"], st["k"], st["v"]]))

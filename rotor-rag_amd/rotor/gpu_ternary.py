@@ -120,6 +120,18 @@ class LinearPlan:
         _hip.check(_hip.load().rt_plan_attention_combine(self.handle, ptr(out), ptr(ssq)), "rt_plan_attention_combine")
         self._keep = (self._keep, out, ssq)
 
+    def set_output_ssq(self, ssq) -> None:
+        """Also write, per 32 outputs (after the residual), the float64 sum of their squares
+        into ssq [ceil(N/32)] (rt_plan_set_output_ssq; one-problem fused decode plans): the
+        aux2 of an SRC_RMSNORM_SSQ plan reading this plan's output.  None detaches."""
+        if ssq is not None:
+            torch = _torch()
+            if ssq.dtype != torch.float64 or not ssq.is_contiguous():
+                raise ValueError("set_output_ssq: ssq float64, contiguous")
+        _hip.check(_hip.load().rt_plan_set_output_ssq(self.handle, ssq.data_ptr() if ssq is not None else None),
+                   "rt_plan_set_output_ssq")
+        self._keep = (self._keep, ssq)
+
     def attention_timeouts(self) -> int:
         """Attention waits of this plan's launches that gave up (rt_plan_attention_timeouts;
         synchronises the device).  Never expected: a non-zero count means wrong results."""

@@ -257,3 +257,78 @@ def test_gate_up_pair_plan_rejects_shapes(hip):
     a, ssq = torch.empty(64, device="cuda"), torch.empty(2, dtype=torch.float64, device="cuda")
     with pytest.raises(RuntimeError, match="K % 64"):
         hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM, h, nw, a=a, ssq=ssq)
+
+
+@pytest.mark.parametrize("D,N,F", [(2560, 2560, 6912), (640, 200, 256), (1024, 96, 512)])
+def test_output_ssq_feeds_rmsnorm_ssq(hip, D, N, F):
+    """A one-problem fused decode plan with rt_plan_set_output_ssq writes, per 32 outputs
+    (after the residual; a last partial group adds only its outputs), the f64 sum of their
+    squares; a plan reading that row through RMSNORM_SSQ gives exactly what the same plan
+    reducing the row itself (RMSNORM) gives, as a gate/up pair plan and as a q/k/v-style
+    plan.  Detached, the plan writes no sums."""
+    import torch
+
+    from rotor import _hip
+
+    rng = np.random.default_rng(D + N)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    x, nw1, nw2 = d(rng.standard_normal(D) * 2), d(rng.uniform(0.5, 1.5, D)), d(rng.uniform(0.5, 1.5, N))
+    (Wo, so), (Wq, sq) = O.make_ternary(rng, N, D), O.make_ternary(rng, 2 * 64, N)
+    wo, wq = hip.upload(O.pack_rotor(Wo), D, so), hip.upload(O.pack_rotor(Wq), N, sq)
+    h0 = d(rng.standard_normal(N))
+    h = h0.clone()
+    ss = torch.full(((N + 31) // 32,), float("nan"), dtype=torch.float64, device="cuda")
+    po = hip.plan_fused([wo], _hip.SRC_RMSNORM, x, nw1, eps=1e-6, ys=[h], residuals=[h])
+    po.set_output_ssq(ss)
+    po.run()
+    torch.cuda.synchronize()
+    hn = _np(h).astype(np.float64)
+    hp = np.concatenate([hn, np.zeros(-N % 32)]).reshape(-1, 32)
+    np.testing.assert_allclose(_np(ss), (hp ** 2).sum(1), rtol=1e-12, atol=0)
+    # consumers: RMSNORM_SSQ on (h, ss) == RMSNORM on h
+    if N % 64 == 0:
+        y1, y2 = torch.empty(2 * 64, device="cuda"), torch.empty(2 * 64, device="cuda")
+        hip.plan_fused([wq], _hip.SRC_RMSNORM, h, nw2, eps=1e-6, ys=[y1]).run()
+        hip.plan_fused([wq], _hip.SRC_RMSNORM_SSQ, h, nw2, ss, eps=1e-6, ys=[y2]).run()
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2)
+        (Wg, sg), (Wu, su) = O.make_ternary(rng, F, N), O.make_ternary(rng, F, N)
+        w_gu, scales = hip.interleave_gate_up(hip.upload(O.pack_rotor(Wg), N, sg), hip.upload(O.pack_rotor(Wu), N, su))
+        outs = []
+        for src in ((_hip.SRC_RMSNORM, h, nw2), (_hip.SRC_RMSNORM_SSQ, h, nw2, ss)):
+            a = torch.empty(F, device="cuda")
+            assq = torch.empty(F // 32, dtype=torch.float64, device="cuda")
+            hip.plan_gate_up(w_gu, scales, *src, eps=1e-6, a=a, ssq=assq).run()
+            outs.append((a, assq))
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    # detached: the sums are left alone
+    po.set_output_ssq(None)
+    ss.fill_(-1.0)
+    h.copy_(h0)
+    po.run()
+    torch.cuda.synchronize()
+    assert (ss == -1.0).all()
+
+
+def test_output_ssq_rejects_other_plans(hip):
+    import torch
+
+    from rotor import _hip
+
+    rng = np.random.default_rng(9)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.float32)).cuda()
+    x, nw = d(rng.standard_normal(256)), d(np.ones(256))
+    w1, w2 = (hip.upload(O.pack_rotor(O.make_ternary(rng, 64, 256)[0]), 256, 1.0) for _ in range(2))
+    ss = torch.empty(4, dtype=torch.float64, device="cuda")
+    two = hip.plan_fused([w1, w2], _hip.SRC_RMSNORM, x, nw, eps=1e-6, ys=[torch.empty(64, device="cuda")] * 2)
+    with pytest.raises(RuntimeError, match="rt_plan_set_output_ssq"):
+        two.set_output_ssq(ss)
+    w_gu, scales = hip.interleave_gate_up(w1, w2)
+    pair = hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM, x, nw, a=torch.empty(64, device="cuda"),
+                            ssq=torch.empty(2, dtype=torch.float64, device="cuda"))
+    with pytest.raises(RuntimeError, match="rt_plan_set_output_ssq"):
+        pair.set_output_ssq(ss)
+    with pytest.raises(ValueError):
+        hip.plan_fused([w1], _hip.SRC_RMSNORM, x, nw, eps=1e-6, ys=[torch.empty(64, device="cuda")]).set_output_ssq(
+            torch.empty(4, device="cuda"))

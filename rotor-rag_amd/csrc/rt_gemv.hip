@@ -516,7 +516,8 @@ __global__ void __launch_bounds__(PRO == 2 ? kAttnMaxThreads : 1024)
             }
             if (a.out_ssq) {  // the next plan's RMSNORM_SSQ input (rows past N add 0)
                 const double ss = half_reduce31((double)o * (double)o, 0.0, [](double x, double y) { return x + y; });
-                if ((r & 31) == 31) a.out_ssq[(rb * kRowBlock + r) >> 5] = ss;
+                const int grp = (rb * kRowBlock + r) >> 5;  // groups wholly past N have no entry
+                if ((r & 31) == 31 && grp * 32 < P.N) a.out_ssq[grp] = ss;
             }
         }
         return;

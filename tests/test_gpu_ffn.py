@@ -259,7 +259,7 @@ def test_gate_up_pair_plan_rejects_shapes(hip):
         hip.plan_gate_up(w_gu, scales, _hip.SRC_RMSNORM, h, nw, a=a, ssq=ssq)
 
 
-@pytest.mark.parametrize("D,N,F", [(2560, 2560, 6912), (640, 200, 256), (1024, 96, 512)])
+@pytest.mark.parametrize("D,N,F", [(2560, 2560, 6912), (640, 200, 256), (1024, 96, 512), (640, 224, 256)])
 def test_output_ssq_feeds_rmsnorm_ssq(hip, D, N, F):
     """A one-problem fused decode plan with rt_plan_set_output_ssq writes, per 32 outputs
     (after the residual; a last partial group adds only its outputs), the f64 sum of their
@@ -277,7 +277,9 @@ def test_output_ssq_feeds_rmsnorm_ssq(hip, D, N, F):
     wo, wq = hip.upload(O.pack_rotor(Wo), D, so), hip.upload(O.pack_rotor(Wq), N, sq)
     h0 = d(rng.standard_normal(N))
     h = h0.clone()
-    ss = torch.full(((N + 31) // 32,), float("nan"), dtype=torch.float64, device="cuda")
+    # one sentinel entry past the ceil(N / 32) sums: no group wholly past N is written
+    ss_buf = torch.full(((N + 31) // 32 + 1,), float("nan"), dtype=torch.float64, device="cuda")
+    ss = ss_buf[:-1]
     po = hip.plan_fused([wo], _hip.SRC_RMSNORM, x, nw1, eps=1e-6, ys=[h], residuals=[h])
     po.set_output_ssq(ss)
     po.run()
@@ -285,6 +287,7 @@ def test_output_ssq_feeds_rmsnorm_ssq(hip, D, N, F):
     hn = _np(h).astype(np.float64)
     hp = np.concatenate([hn, np.zeros(-N % 32)]).reshape(-1, 32)
     np.testing.assert_allclose(_np(ss), (hp ** 2).sum(1), rtol=1e-12, atol=0)
+    assert np.isnan(_np(ss_buf)[-1])
     # consumers: RMSNORM_SSQ on (h, ss) == RMSNORM on h
     if N % 64 == 0:
         y1, y2 = torch.empty(2 * 64, device="cuda"), torch.empty(2 * 64, device="cuda")

@@ -313,8 +313,8 @@ class _DeviceModel:
                 if self.attn_in_qkv and L["attn_sub_norm"] is not None and self.attn_in_prologue:
                     st["attn_fused"][li] = self._attach_attention(st["qkv"][li], L)
                 if st["attn_fused"][li] and self.attn_combine_in_qkv and self.Lmax <= 640:
-                    st["qkv"][li].attention_combine(o, st["ossq"])
-                    st["attn_comb"][li] = True
+                    st["attn_comb"][li] = self._attach_combine(st["qkv"][li], o, st["ossq"])
+                if st["attn_comb"][li]:
                     st["o_plan"].append(hip.plan_fused([L["o_proj"]], _hip.SRC_RMSNORM_SSQ, o, L["attn_sub_norm"],
                                                        st["ossq"], eps=eps, ys=[h], residuals=[h]))
                 elif L["attn_sub_norm"] is not None and self.attn_in_prologue:
@@ -366,6 +366,18 @@ class _DeviceModel:
                                   self.attn_ws)
         except RuntimeError as e:
             if "rt_plan_attach_attention" not in str(e):
+                raise
+            return False
+        return True
+
+    def _attach_combine(self, plan, out, ssq):
+        """Let layer L's q/k/v plan also combine the attention partials (into out, sums of
+        squares into ssq); False where the library refuses (the device cannot hold the launch's
+        workgroups at once), which leaves the combine to o_proj's prologue."""
+        try:
+            plan.attention_combine(out, ssq)
+        except RuntimeError as e:
+            if "rt_plan_attention_combine" not in str(e):
                 raise
             return False
         return True

@@ -111,11 +111,13 @@ hipError_t launch_quant(const QuantArgs& a, hipStream_t s, int maxK) {
     if (maxK > 0) {  // every problem passed quant_rows_ok; maxK: the largest K
         const dim3 grid((unsigned)a.Mpad, (unsigned)a.U);
         const size_t lds = 8192 + sizeof(RowSmem);
-        // whole waves (the workgroup reductions take one slot per wave)
+        // whole waves (the workgroup reductions take one slot per wave); 8 or 16 elements per
+        // thread: fewer waves in the row's two reductions (512-token prefill 4.70 -> 4.59 ms
+        // against 4 and 8)
         if (maxK <= 4096) {
-            hipLaunchKernelGGL((quant_rows_kernel<4>), grid, dim3((unsigned)((maxK / 4 + 63) / 64 * 64)), lds, s, a);
-        } else {
             hipLaunchKernelGGL((quant_rows_kernel<8>), grid, dim3((unsigned)((maxK / 8 + 63) / 64 * 64)), lds, s, a);
+        } else {
+            hipLaunchKernelGGL((quant_rows_kernel<16>), grid, dim3((unsigned)((maxK / 16 + 63) / 64 * 64)), lds, s, a);
         }
         return hipGetLastError();
     }

@@ -91,7 +91,7 @@ def test_embed_exact(hip):
 ATTN_CASES = [(1, 0, 20, 5, 128, 64), (1, 37, 20, 5, 128, 64), (7, 3, 8, 2, 64, 64), (16, 0, 4, 4, 64, 64),
               (100, 50, 20, 5, 128, 256), (70, 0, 8, 4, 64, 128), (130, 5, 4, 4, 64, 192), (33, 20, 6, 2, 64, 64),
               (40, 10, 8, 8, 128, 128), (50, 0, 16, 2, 128, 68), (200, 300, 20, 5, 128, 520),
-              (130, 0, 4, 2, 128, 192), (20, 0, 4, 2, 128, 192), (130, 0, 8, 2, 64, 192)]
+              (130, 0, 4, 2, 128, 192), (20, 0, 4, 2, 128, 192), (130, 0, 8, 2, 64, 192), (512, 0, 20, 5, 128, 640)]
 
 
 @pytest.mark.parametrize("M,pos0,H,Hkv,hd,Lmax", ATTN_CASES)
@@ -129,6 +129,11 @@ def test_rope_append_and_attention(hip, M, pos0, H, Hkv, hd, Lmax):
     assert np.array_equal(vcd.cpu().numpy()[:, :pos0 + M], V)
     ref = O.causal_gqa_attention(qr, K, V, pos0).reshape(M, H * hd)
     np.testing.assert_allclose(out.cpu().numpy(), ref, atol=2e-5, rtol=1e-4)
+    # again on the same context: the same output, bit for bit
+    out2 = torch.full((M, H * hd), float("nan"), device="cuda")
+    chk(lib.rt_attention(hip.ctx, qd.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), out2.data_ptr(), M, H, Hkv, hd, Lmax,
+                         pos.data_ptr()))
+    assert torch.equal(out, out2)
 
 
 # The last block's key count nk = pos0 % 64 + 1 walks the value sums' runs of 8 key pairs:

@@ -458,24 +458,60 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
 // with p = *pos_p + advance, to out_tokens[p - 1 - pos_base]; then *pos_p = p.  With
 // next_h, the token's embedding row E[token] (bf16 -> fp32, D values) is written there: the
 // next step's input row, so that step needs no embedding launch.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 __global__ void __launch_bounds__(256) argmax_finalize_kernel(unsigned long long* best, int* token, int* pos_p,
                                                               int advance, int* next_ids, int* out_tokens, int pos_base,
                                                               int out_cap, const uint16_t* __restrict__ E, int V,
                                                               int D, float* __restrict__ next_h) {
+    const int t = threadIdx.x;
+    // the maximum and the position are read together (one memory latency for both; without a
+    // position the second read re-reads the maximum and is discarded)
+    const int* pp = pos_p ? pos_p : reinterpret_cast<const int*>(best);
     const unsigned long long k = *best;
+    int p = *pp;
     const int tok = (int)(0xFFFFFFFFu - (unsigned)(k & 0xFFFFFFFFull));
     if (next_h) {
         // (a row of NaN logits can leave `best` unset: read row 0 rather than out of range)
         const uint16_t* row = E + (size_t)(tok >= 0 && tok < V ? tok : 0) * D;
-        for (int e = threadIdx.x; e < D; e += blockDim.x) next_h[e] = bf16_to_f32(row[e]);
+        const int D8 = D / 8;
+        if (D % 8 == 0 && D8 <= 2 * (int)blockDim.x && (((uintptr_t)E | (uintptr_t)next_h) & 15u) == 0) {
+            // eight values per 16-byte load, both of a thread's loads issued before its stores
+            const int e0 = t, e1 = t + (int)blockDim.x;
+            v4u u0{}, u1{};
+            if (e0 < D8) u0 = reinterpret_cast<const v4u*>(row)[e0];
+            if (e1 < D8) u1 = reinterpret_cast<const v4u*>(row)[e1];
+            auto put = [&](int e, const v4u& u) {
+                v4f lo, hi;
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    lo[2 * j] = __uint_as_float(u[j] << 16);
+                    lo[2 * j + 1] = __uint_as_float(u[j] & 0xFFFF0000u);
+                    hi[2 * j] = __uint_as_float(u[j + 2] << 16);
+                    hi[2 * j + 1] = __uint_as_float(u[j + 2] & 0xFFFF0000u);
+                }
+                reinterpret_cast<v4f*>(next_h)[2 * e] = lo;
+                reinterpret_cast<v4f*>(next_h)[2 * e + 1] = hi;
+            };
+            if (e0 < D8) put(e0, u0);
+            if (e1 < D8) put(e1, u1);
+        } else {
+            for (int e = t; e < D; e += blockDim.x) next_h[e] = bf16_to_f32(row[e]);
+        }
     }
-    __syncthreads();  // every thread has read *best
-    if (threadIdx.x != 0) return;
+    // Thread 0 resets *best below: every thread has its value by then (the empty asm needs it
+    // in a register, so the wave waits for its load before the barrier).  The barrier does not
+    // wait for the row's stores: nothing here reads them.
+    asm volatile("" ::"v"(tok));
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (t != 0) return;
     *token = tok;
     *best = 0ull;  // ready for the next step
     if (next_ids) next_ids[0] = tok;
     if (pos_p) {
-        const int p = *pos_p + advance;
+        p += advance;
         const int i = p - 1 - pos_base;
         if (out_tokens && i >= 0 && i < out_cap) out_tokens[i] = tok;
         *pos_p = p;

@@ -454,12 +454,12 @@ __global__ void __launch_bounds__(256) lm_head_kernel(const uint16_t* __restrict
     }
 }
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 // token = argmax; optionally also written to next_ids[0] (the next step's input) and,
 // with p = *pos_p + advance, to out_tokens[p - 1 - pos_base]; then *pos_p = p.  With
 // next_h, the token's embedding row E[token] (bf16 -> fp32, D values) is written there: the
 // next step's input row, so that step needs no embedding launch.
-typedef float v4f __attribute__((ext_vector_type(4)));
-
 __global__ void __launch_bounds__(256) argmax_finalize_kernel(unsigned long long* best, int* token, int* pos_p,
                                                               int advance, int* next_ids, int* out_tokens, int pos_base,
                                                               int out_cap, const uint16_t* __restrict__ E, int V,

@@ -458,6 +458,12 @@ def test_lm_head_argmax(hip, V, D):
         assert int(best.cpu()[0]) == 0
     # the chosen token's embedding row, the next decode step's input
     assert np.array_equal(next_h.cpu().numpy(), O.bf16_to_f32(E[int(np.argmax(lg))]))
+    # the same into a row that is not 16-byte aligned (the element-wise copy)
+    nh_buf = torch.full((D + 1,), float("nan"), device="cuda")
+    chk(lib.rt_lm_head_argmax(hip.ctx, Ed.data_ptr(), xd.data_ptr(), wd.data_ptr(), 1e-6, V, D, logits.data_ptr(),
+                              best.data_ptr(), tok.data_ptr(), None, 0, None, None, 0, 0, nh_buf[1:].data_ptr()))
+    assert np.array_equal(nh_buf[1:].cpu().numpy(), O.bf16_to_f32(E[int(np.argmax(lg))]))
+    assert int(best.cpu()[0]) == 0
     hn = O.rms_norm_f64acc(x[None], w)[0]
     E32 = O.bf16_to_f32(E)
     ref = E32.astype(np.float64) @ hn.astype(np.float64)

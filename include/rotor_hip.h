@@ -72,7 +72,8 @@ const char* rt_last_error(void);
  * and RT_SRC_RMSNORM_STATS; 105 = 104 + rt_plan_attach_attention and rt_plan_attention_timeouts;
  * 106 = 105 without rt_plan_set_row_stats and RT_SRC_RMSNORM_STATS (measured slower than each
  * decode prologue reducing its own row), + rt_attention_decode_combine,
- * rt_plan_attention_combine and rt_lm_head_argmax's next_h; 107 = 106 + rt_plan_set_output_ssq. */
+ * rt_plan_attention_combine and rt_lm_head_argmax's next_h; 107 = 106 + rt_plan_set_output_ssq;
+ * 108 = 107 + rt_plan_create_act_gate_up. */
 int rt_version(void);
 
 /* Number of visible HIP devices (0 when none); RT_OK even when 0. */
@@ -220,6 +221,17 @@ int rt_linear_act_f32(rt_ctx* ctx, const rt_weights* w, const rt_act* act, const
  * no-op and rt_plan_gemv / rt_plan_run launch the matrix kernels only. */
 int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_act* const* act, int M,
                        float* const* y, rt_plan** out);
+
+/* The gated FFN's gate and up projections for M > 64 tokens (prefill) over caller-filled
+ * activations, in ONE tile-GEMM launch on the matrix of rt_plan_create_gate_up's layout
+ * (gate and up [F][K] interleaved in groups of 32 rows, N = 2F, N % 64 == 0): writes
+ * a fp32 [M][F] = relu(g)^2 * u with g = ((float)acc * s_x) * s_gate and u likewise with
+ * s_up -- the values rt_act_relu2_mul_quantize forms from the two outputs of an
+ * rt_plan_create_act plan over gate and up, bit for bit -- instead of g and u.  Run with
+ * rt_plan_gemv.  Fuses the elementwise gate of GatedFFN.forward
+ * (src/rotor/transformer.py:329-337) into the projections' epilogue. */
+int rt_plan_create_act_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, float s_up, const rt_act* act,
+                               int M, float* a, rt_plan** out);
 
 /* Fused decode plan (one token): G linears sharing one input row, in ONE launch whose
  * workgroups each quantise that row (fused with its producer as `src` says) into LDS

@@ -159,6 +159,7 @@ struct rt_plan {
     GemmArgs* dev_gemms = nullptr;   // M > 8: the problems of one grouped launch [G]
     int* dev_tile2p = nullptr;       // M > 64: problem of every tile of that launch
     int gemm_cfg = 0, gemm_tiles = 0;  // M > 64: tile shape, tiles over all problems
+    bool pair_gemm = false;            // rt_plan_create_act_gate_up: tiles whose waves pair columns
     int gemm_units = 0;              // 8 < M <= 64: workgroups of the split-K launch (parts x row blocks)
     int* dev_unit2d = nullptr;       // 8 < M <= 64: descriptor of every unit
     std::vector<int> gemm_bnd;       // M > 8: first unit (tile) of descriptors 1.. (launch arguments)
@@ -204,7 +205,7 @@ extern "C" {
 
 const char* rt_last_error(void) { return g_err.c_str(); }
 
-int rt_version(void) { return 107; }
+int rt_version(void) { return 108; }
 
 int rt_device_count(int* n) {
     if (!n) return fail(RT_EINVAL, "rt_device_count: n is NULL");
@@ -630,6 +631,10 @@ static hipError_t upload_gemm_group(rt_plan* p) {
         Cs[i] = g[i].C;
     }
     p->gemm_cfg = gemm_tile_cfg(p->M, Ns.data(), Cs.data(), (int)g.size());
+    // the pair epilogue runs in tiles whose waves hold one 64-column group: not the 64-row
+    // tile's 32 columns, the 256-column tile's 128 or the region kernel (its own epilogue)
+    if (p->pair_gemm && (p->gemm_cfg == kTile64x128 || p->gemm_cfg == kRegion128x160)) p->gemm_cfg = kTile128x128;
+    if (p->pair_gemm && p->gemm_cfg == kTile256x256) p->gemm_cfg = kTile256x128;
     long long total = 0;
     for (size_t i = 0; i < g.size(); ++i) {
         g[i].wg_begin = (int)total;
@@ -1028,6 +1033,45 @@ int rt_plan_create_act(rt_ctx* ctx, int G, const rt_weights* const* w, const rt_
     if (e != hipSuccess) {
         rt_plan_free(p);
         return hip_fail(e, "rt_plan_create_act");
+    }
+    *out = p;
+    return RT_OK;
+}
+
+int rt_plan_create_act_gate_up(rt_ctx* ctx, const rt_weights* w_gu, float s_gate, float s_up, const rt_act* act,
+                               int M, float* a_out, rt_plan** out) {
+    const char* who = "rt_plan_create_act_gate_up";
+    if (!ctx || !w_gu || !act || !a_out || !out) return fail(RT_EINVAL, std::string(who) + ": NULL argument");
+    *out = nullptr;
+    if (act->K != w_gu->K) return fail(RT_EINVAL, std::string(who) + ": activation K differs from weights");
+    if (M <= 64 || M > act->Mcap)
+        return fail(RT_EINVAL, std::string(who) + ": M must exceed 64 (the tile GEMM) and fit the activations");
+    if (w_gu->N % 64) return fail(RT_EINVAL, std::string(who) + ": the interleaved matrix needs N % 64 == 0");
+    if (w_gu->device != ctx->device || act->device != ctx->device)
+        return fail(RT_EINVAL, std::string(who) + ": operands live on another device");
+    if (!gemm_ldo_ok(M, w_gu->N)) return fail(RT_EINVAL, std::string(who) + ": N too large for 32-bit offsets");
+    DeviceGuard guard(ctx->device);
+    rt_plan* p = new rt_plan();
+    p->device = ctx->device;
+    p->G = 1;
+    p->M = M;
+    p->mt = gemv_mt(M);
+    p->Mpad = act_rows(M);
+    p->U = 0;  // the input is quantised by the caller
+    p->acts.assign(1, act);
+    p->pair_gemm = true;
+    const int F = w_gu->N / 2;
+    p->probs.assign(1, GemvProb{w_gu->tiles, act->qx, act->sx, nullptr, a_out, 1.0f, w_gu->N, w_gu->C, F, 0});
+    p->total_rb = w_gu->Np / kRowBlock;
+    GemmArgs ga{w_gu->tiles, act->qx, act->sx, nullptr, nullptr, 1.0f, M, w_gu->N, w_gu->Np, w_gu->C, F, 0};
+    ga.pair_a = a_out;
+    ga.pair_sg = s_gate;
+    ga.pair_su = s_up;
+    p->gemms.push_back(ga);
+    hipError_t e = upload_gemm_group(p);
+    if (e != hipSuccess) {
+        rt_plan_free(p);
+        return hip_fail(e, who);
     }
     *out = p;
     return RT_OK;

@@ -151,6 +151,47 @@ __device__ __forceinline__ void store_tile(const v16i (&acc)[FI][FJ], const Gemm
     }
 }
 
+// The gate/up pair's epilogue (GemmArgs::pair_a): the wave's column blocks 2 jp and 2 jp + 1
+// are the gate and up rows of the same 32 outputs (their 64-column group starts at a multiple
+// of 64), so lane l forms a = relu(g)^2 * u of output 32 (n / 64) + l % 32 for its 16 rows,
+// g and u rounded as store_tile's fp32 epilogue rounds y, a in the order of the quantiser's
+// relu^2 * up.  Rows and columns past the problem fall outside the buffer (as store_tile).
+template <int FI, int FJ>
+__device__ __forceinline__ void store_tile_pair(const v16i (&acc)[FI][FJ], const GemmArgs& a, int m0, int rows,
+                                                int mrow, int nb, const float* sx_lds) {
+    static_assert(FJ % 2 == 0, "gate and up blocks in pairs");
+    const unsigned range = (unsigned)rows * (unsigned)a.ldo * 4u;
+    const __amdgpu_buffer_rsrc_t out =
+        __builtin_amdgcn_make_buffer_rsrc(a.pair_a + (size_t)m0 * a.ldo, 0, range, kBufDword3);
+    int coff[FJ / 2];
+#pragma unroll
+    for (int jp = 0; jp < FJ / 2; ++jp) {
+        const int n = nb + jp * 64, no = 32 * (n >> 6) + (n & 31);  // gate column, output column
+        coff[jp] = (int)((unsigned)no * 4u + ((unsigned)(n >= a.N) << 31));
+    }
+    const int row_bytes = a.ldo * 4;
+#pragma unroll
+    for (int i = 0; i < FI; ++i) {
+        float sxv[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {  // rows mrow + 32 i + 8 q + 0..3
+            const v4f s4 = *reinterpret_cast<const v4f*>(sx_lds + mrow + i * 32 + q * 8);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sxv[q * 4 + r] = s4[r];
+        }
+#pragma unroll
+        for (int jp = 0; jp < FJ / 2; ++jp)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int off = (mrow + i * 32 + 8 * (k >> 2) + (k & 3)) * row_bytes + coff[jp];
+                const float g = ((float)acc[i][2 * jp][k] * sxv[k]) * a.pair_sg;
+                const float u = ((float)acc[i][2 * jp + 1][k] * sxv[k]) * a.pair_su;
+                const float av = g > 0.0f ? (g * g) * u : 0.0f;
+                __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, av), out, off, 0, 0);
+            }
+    }
+}
+
 // One problem, or a group of them (dev != nullptr): unit b (a row block of the split-K
 // kernel, a tile of the tile kernel) serves problem rb2p[b], whose units start at its
 // wg_begin.
@@ -181,7 +222,7 @@ __device__ __forceinline__ GemmArgs find_gemm(const GemmGroupArgs& ga, int b) {
     const cgemm* q = (cgemm*)ga.dev + j;
     return GemmArgs{q->w,  q->qx,       q->sx, q->rs, q->out, q->s_w, q->M,     q->N,   q->Np,
                     q->C,  q->ldo,      q->out_i32, q->res, q->wg_begin, q->c0, q->c1, q->kp, q->parts,
-                    q->cnt, q->part_ws};
+                    q->cnt, q->part_ws, q->pair_a, q->pair_sg, q->pair_su};
 }
 
 template <int BM, int BN, int WAVES_M, int STAGES>
@@ -340,9 +381,17 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmGroupArgs ga) {
     // epilogue (this barrier publishes the row scales)
     wait_barrier<0>();
     const int rows = min(BM, a.M - m0);
-    if (a.out_i32) store_tile<FI, FJ, 0>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
-    else if (a.res) store_tile<FI, FJ, 2>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
-    else store_tile<FI, FJ, 1>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
+    if (a.out_i32) {
+        store_tile<FI, FJ, 0>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
+    } else if (FJ == 2 && a.pair_a) {
+        // the host pairs only tiles whose waves hold one 64-column group (in the 256-column
+        // tile, even holding pair_a through the main loop made it spill)
+        if constexpr (FJ == 2) store_tile_pair<FI, FJ>(acc, a, m0, rows, mrow, nb, sx_lds);
+    } else if (a.res) {
+        store_tile<FI, FJ, 2>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
+    } else {
+        store_tile<FI, FJ, 1>(acc, a, m0, rows, mrow, nb, sx_lds, swv);
+    }
 }
 
 // ---- long K, one round over the CUs: 128 x 160 regions -------------------------------

@@ -224,6 +224,12 @@ struct GemmArgs {
     int c0, c1, kp, parts;
     int* cnt;
     int* part_ws;
+    // gate/up pair (tile GEMM, rt_plan_create_act_gate_up): the matrix interleaves gate and up
+    // in groups of 32 rows (row 64 j + r: gate row 32 j + r for r < 32, up row 32 j + r - 32),
+    // and the epilogue writes, instead of out, pair_a [M][ldo = N / 2] = relu(g)^2 * u with
+    // g = ((float)acc * sx) * pair_sg and u likewise with pair_su
+    float* pair_a;
+    float pair_sg, pair_su;
 };
 
 constexpr int kBufDword3 = 0x00020000;  // buffer resource word 3 for gfx9 raw buffers

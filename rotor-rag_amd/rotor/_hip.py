@@ -15,7 +15,7 @@ import os
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "librotor_hip.so"
-ABI_VERSION = 107  # rt_version() of the library this table binds
+ABI_VERSION = 108  # rt_version() of the library this table binds
 
 class RtSrc(ctypes.Structure):
     """rt_src of include/rotor_hip.h"""
@@ -68,6 +68,7 @@ SIGNATURES = {
     "rt_plan_create_fused": (_I, [_P, _I, ctypes.POINTER(_P), ctypes.POINTER(RtSrc), ctypes.POINTER(_P),
                                   ctypes.POINTER(_P), ctypes.POINTER(_P)]),
     "rt_plan_create_gate_up": (_I, [_P, _P, _F, _F, ctypes.POINTER(RtSrc), _P, _P, _P, _P, ctypes.POINTER(_P)]),
+    "rt_plan_create_act_gate_up": (_I, [_P, _P, _F, _F, _P, _I, _P, ctypes.POINTER(_P)]),
     "rt_plan_attach_attention": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, ctypes.c_size_t]),
     "rt_plan_attention_combine": (_I, [_P, _P, _P]),
     "rt_plan_attention_timeouts": (_I, [_P, _P]),

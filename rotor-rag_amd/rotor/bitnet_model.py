@@ -296,6 +296,7 @@ class _DeviceModel:
         st["qkv"], st["gu"], st["o_plan"], st["d_plan"] = [], [], [], []
         st["attn_fused"] = []  # per layer: the q/k/v plan runs the attention partials
         st["attn_comb"] = []   # per layer: ... and combines them into o[0] (sums of squares in ossq)
+        st["gu_pair"] = []     # per layer (M > 64): the gate/up GEMM writes relu(g)^2 * u into am
         st["ossq"] = torch.empty(H * hd // 32, dtype=torch.float64, device=dev)
         hip, eps = self.hip, self.m.eps
         chain = M == 1 and self.ssq_chain
@@ -353,7 +354,19 @@ class _DeviceModel:
             else:
                 st["qkv"].append(hip.plan_act([L["q_proj"], L["k_proj"], L["v_proj"]], [self.act_d] * 3, M,
                                               [st["q"], st["k"], st["v"]]))
-                st["gu"].append(hip.plan_act([L["gate_proj"], L["up_proj"]], [self.act_d] * 2, M, [st["g"], st["u"]]))
+                if M > 64 and L["ffn_sub_norm"] is not None and self.ffn_pair:
+                    # one GEMM over the interleaved gate/up matrix writes relu(g)^2 * u (am)
+                    if "gate_up" not in L:
+                        L["gate_up"] = hip.interleave_gate_up(L["gate_proj"], L["up_proj"])
+                    if "am" not in st:
+                        st["am"] = e(M, F)
+                    w_gu, scales = L["gate_up"]
+                    st["gu"].append(hip.plan_act_gate_up(w_gu, scales, self.act_d, M, st["am"]))
+                    st["gu_pair"].append(True)
+                else:
+                    st["gu_pair"].append(False)
+                    st["gu"].append(hip.plan_act([L["gate_proj"], L["up_proj"]], [self.act_d] * 2, M,
+                                                 [st["g"], st["u"]]))
         self.state[M] = st
         return st
 
@@ -468,7 +481,9 @@ class _DeviceModel:
             hip.linear_act(L["o_proj"], self.act_d, out=h, residual=h)
             hip.act_rmsnorm_quantize(h, L["post_norm"], self.act_d, eps)
             st["gu"][li].gemv()
-            if L["ffn_sub_norm"] is not None:
+            if st["gu_pair"][li]:  # the gate/up launch wrote relu(g)^2 * u: the same values, sub-normed
+                hip.act_rmsnorm_quantize(st["am"], L["ffn_sub_norm"], self.act_f, eps)
+            elif L["ffn_sub_norm"] is not None:
                 hip.act_relu2_mul_norm_quantize(g, u, L["ffn_sub_norm"], self.act_f, eps)
             else:
                 hip.act_relu2_mul_quantize(g, u, self.act_f)

@@ -434,6 +434,21 @@ class HIPTernaryOps:
         _hip.check(self.lib.rt_plan_create_act(self.ctx, G, wa, aa, int(M), ya, ctypes.byref(h)), "rt_plan_create_act")
         return LinearPlan(self, h, (list(weights), list(acts), list(ys)))
 
+    def plan_act_gate_up(self, w_gu, scales, act, M: int, a) -> LinearPlan:
+        """Gate and up for M > 64 tokens over caller-filled activations in one GEMM launch
+        (rt_plan_create_act_gate_up) on the matrix of interleave_gate_up: a fp32 [M, F] =
+        relu(g)^2 * u, the values act_relu2_mul_quantize forms from separate g and u."""
+        torch = _torch()
+        N, K = w_gu.out_features, w_gu.in_features
+        if act.in_features != K or a.dtype != torch.float32 or tuple(a.shape) != (M, N // 2) or not a.is_contiguous():
+            raise ValueError("plan_act_gate_up: shapes do not match")
+        h = ctypes.c_void_p()
+        s_gate, s_up = scales
+        _hip.check(self.lib.rt_plan_create_act_gate_up(self.ctx, w_gu.handle, float(s_gate), float(s_up), act.handle,
+                                                       int(M), a.data_ptr(), ctypes.byref(h)),
+                   "rt_plan_create_act_gate_up")
+        return LinearPlan(self, h, (w_gu, act, a))
+
     def plan_fused(self, weights, mode: int, x, aux=None, aux2=None, eps: float = 1e-6, ys=None, residuals=None,
                    attn_head_dim: int = 0, attn_max_len: int = 0):
         """One-token plan whose single launch quantises its input row in the prologue:

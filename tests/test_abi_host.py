@@ -60,7 +60,7 @@ def test_ctypes_table_matches_header():
 
     assert sorted(_hip.SIGNATURES) == declared_functions()
     lib = _hip.load()
-    assert lib.rt_version() == _hip.ABI_VERSION == 107
+    assert lib.rt_version() == _hip.ABI_VERSION == 108
 
 
 def test_no_gpu_context_creation_fails_cleanly():

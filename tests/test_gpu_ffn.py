@@ -335,3 +335,35 @@ def test_output_ssq_rejects_other_plans(hip):
     with pytest.raises(ValueError):
         hip.plan_fused([w1], _hip.SRC_RMSNORM, x, nw, eps=1e-6, ys=[torch.empty(64, device="cuda")]).set_output_ssq(
             torch.empty(4, device="cuda"))
+
+
+# (M, F, K): the tile the pair epilogue runs on -- 128 x 128 (M <= 128), 64 x 128 promoted to
+# 128 x 128 (few tiles), 192 x 128, 256 x 128 (the 512-token prefill), and 256 x 256 taken as
+# 256 x 128 (M = 2048)
+@pytest.mark.parametrize("M,F,K", [(70, 256, 128), (200, 512, 256), (300, 1024, 640), (512, 6912, 2560),
+                                   (2048, 6912, 2560)])
+def test_act_gate_up_pair_equals_separate(hip, M, F, K):
+    """rt_plan_create_act_gate_up: one GEMM over the interleaved gate/up matrix writes
+    a = relu(g)^2 * u, bit for bit the product of the g and u an rt_plan_create_act plan over
+    the two matrices writes (each rounded as the fp32 epilogue rounds y, the product in the
+    order of the quantiser's relu^2 * up: (g g) u).  Rows past M are not written."""
+    import torch
+
+    rng = np.random.default_rng(M + F + K)
+    (Wg, sg), (Wu, su) = O.make_ternary(rng, F, K), O.make_ternary(rng, F, K)
+    wg, wu = hip.upload(O.pack_rotor(Wg), K, sg), hip.upload(O.pack_rotor(Wu), K, su)
+    w_gu, scales = hip.interleave_gate_up(wg, wu)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+    act = hip.activations(M, K)
+    hip.act_quantize(x, act)
+    g, u = torch.empty(M, F, device="cuda"), torch.empty(M, F, device="cuda")
+    hip.plan_act([wg, wu], [act, act], M, [g, u]).gemv()
+    a_buf = torch.full((M + 1, F), float("nan"), device="cuda")
+    a = a_buf[:M]
+    hip.plan_act_gate_up(w_gu, scales, act, M, a).gemv()
+    torch.cuda.synchronize()
+    ref = torch.where(g > 0, (g * g) * u, torch.zeros_like(g))
+    assert torch.equal(a, ref)
+    assert torch.isnan(a_buf[M]).all()
+    with pytest.raises(RuntimeError, match="rt_plan_create_act_gate_up"):
+        hip.plan_act_gate_up(w_gu, scales, hip.activations(64, K), 64, torch.empty(64, F, device="cuda"))
